@@ -1,0 +1,142 @@
+/*
+ * lowbit_hip.h -- C-ABI of liblowbit_hip.so, the MI355X (gfx950) low-bit
+ * quantized linear path: W8 per-output-channel, INT4 group-wise and NF4
+ * codebook dequant-GEMV/GEMM with an optional fused rank-r low-rank
+ * correction y += fp16(fp16(x.V^T).U^T).
+ *
+ * Conventions (adopted from the reference's native boundary, not its code):
+ *   - Status codes keep the numbering of npunlock_status
+ *     (reference: npunlock/include/npunlock/error.h:12-26).
+ *   - Argument structs are versioned by a leading struct_size, as
+ *     graphinfer_* structs are (npunlock/include/npunlock/graphinfer.h:31-198).
+ *   - The caller owns every buffer.  All pointers are device pointers except
+ *     the argument struct itself.  Buffers are borrowed until the work queued
+ *     on `stream` completes; nothing is freed or retained by the library.
+ *   - Outputs may not alias inputs (reference: backend.cpp:265-272).
+ *   - Calls are asynchronous and ordered on `stream` (a hipStream_t; NULL is
+ *     the default stream).  No entry point allocates device memory; scratch
+ *     comes from a caller workspace sized by lb_workspace_bytes().
+ *   - On any status other than LB_OK, lb_last_error() returns a thread-local
+ *     message describing the failure, valid until the next call on the same
+ *     thread.  Argument errors are detected before anything is launched.
+ *
+ * Packed layouts are exactly the reference's PackedWeight bytes
+ * (torch_npu_lowbit.py:24-75):
+ *   int8: N*K signed bytes, row-major [N,K].
+ *   int4/nf4: ceil(N*K/2) bytes; flat element 2i in the low nibble of byte i,
+ *             element 2i+1 in the high nibble (rows are not padded, so for odd
+ *             K a row may start mid-byte).
+ *   scales: fp16 [N, K/group_size] row-major.
+ * Decoded integer value q: int8 as stored; int4 ((c ^ 8) - 8) in [-8,7];
+ * nf4 the fp16-rounded codebook entry NF4[c].
+ */
+#ifndef LOWBIT_HIP_H
+#define LOWBIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LB_ABI_VERSION 1
+
+typedef enum lb_status {
+  LB_OK = 0,
+  LB_INVALID_ARGUMENT = 1,
+  LB_OUT_OF_MEMORY = 2,
+  LB_UNSUPPORTED = 5,
+  LB_DEVICE_FAILED = 10,
+  LB_INTERNAL = 12
+} lb_status;
+
+typedef enum lb_format {
+  LB_FORMAT_INT8 = 0,
+  LB_FORMAT_INT4 = 1,
+  LB_FORMAT_NF4 = 2,
+  LB_FORMAT_FP16 = 3 /* dense fp16 [N,K] weights (protected projections, tied head); scales unused */
+} lb_format;
+
+/* lb_linear_args.flags */
+#define LB_FLAG_FORCE_GEMV    0x1u /* decode-regime kernel regardless of M (M <= 32) */
+#define LB_FLAG_FORCE_GEMM    0x2u /* prefill-regime MFMA GEMM regardless of M */
+#define LB_FLAG_FORCE_GENERIC 0x4u /* shape-agnostic fallback kernel (any N, K, group) */
+
+typedef struct lb_linear_args {
+  uint32_t struct_size;     /* sizeof(lb_linear_args) */
+  uint32_t format;          /* lb_format */
+  int64_t M, N, K;          /* y[M,N] = x[M,K] . W[N,K]^T */
+  int64_t group_size;       /* K % group_size == 0; == K for per-row scales */
+  const void *codes;        /* PackedWeight.data bytes (or fp16 [N,K] for LB_FORMAT_FP16) */
+  const void *scales;       /* fp16 [N, K/group_size] */
+  const void *x;            /* fp16 [M,K], row stride ldx elements */
+  int64_t ldx;
+  void *y;                  /* fp16 [M,N], row stride ldy elements */
+  int64_t ldy;
+  const void *bias;         /* fp16 [N] or NULL */
+  int64_t rank;             /* 0: no correction */
+  const void *down;         /* V fp16 [rank, K] row-major (row stride K) */
+  const void *up;           /* U fp16 [N, up_ld], first `rank` columns used */
+  int64_t up_ld;            /* row stride of U in elements (0 means rank) */
+  void *workspace;          /* caller-owned device scratch */
+  size_t workspace_bytes;   /* >= lb_workspace_bytes(args) */
+  uint32_t flags;           /* LB_FLAG_* */
+  uint32_t reserved;
+} lb_linear_args;
+
+/* ABI version of the loaded library (LB_ABI_VERSION at build time). */
+int lb_abi_version(void);
+
+/* Static name of a status, e.g. "LB_INVALID_ARGUMENT". */
+const char *lb_status_name(lb_status status);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char *lb_last_error(void);
+
+/*
+ * Bytes of device workspace lb_linear needs for these arguments (0 when none).
+ * Host-only; validates args.  Replaces nothing in the reference: the NPU graph
+ * owned its intermediates (torch_npu_lowbit.py:189-277).
+ */
+lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes);
+
+/*
+ * y = x . dequant(W)^T [+ bias] [+ fp16(fp16(x.V^T).U^T)], fp32 accumulation,
+ * fp16 output with the reference's staging:
+ *   main = fp16(acc); with bias: fp16(main + b); with correction:
+ *   z = fp16(x.V^T), d = fp16(z.U^T), y = fp16(y + d).
+ * Weight values: int8 with per-row scales use the exact product q*s
+ * (acc * s in fp32); every other case uses fp16(q*s), the reference's
+ * PackedWeight.dequantize() value.
+ * Replaces the lowbit_linear graph of weight_graph()
+ * (torch_npu_lowbit.py:189-277) executed through _C.run / run_many_impl
+ * (npunlock-probe/torch-device/backend.cpp:253-348) and
+ * graphinfer_session_infer (npunlock/include/npunlock/graphinfer.h:173-176),
+ * plus the correction MatMul/MatMul/Add of the SmolLM linear()
+ * (torch_npu_smollm.py:254-258).
+ */
+lb_status lb_linear(const lb_linear_args *args, void *stream);
+
+/*
+ * Bit-exact decode of packed codes to int8 out[N*K] (row-major):
+ * int8 -> value, int4 -> ((c ^ 8) - 8), nf4 -> code index c in 0..15.
+ * Device counterpart of the Convert(i4/nf4/i8) decode of weight_graph
+ * (torch_npu_lowbit.py:216-220) and of the unpack in
+ * PackedWeight.dequantize (torch_npu_lowbit.py:69-73).
+ */
+lb_status lb_unpack_codes(uint32_t format, int64_t N, int64_t K, const void *codes,
+                          int8_t *out, void *stream);
+
+/*
+ * w[N,K] fp16 = fp16(q * s), bit-identical to PackedWeight.dequantize()
+ * (torch_npu_lowbit.py:67-75).
+ */
+lb_status lb_dequantize(uint32_t format, int64_t N, int64_t K, int64_t group_size,
+                        const void *codes, const void *scales, void *w_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOWBIT_HIP_H */

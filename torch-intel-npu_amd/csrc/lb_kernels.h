@@ -1,0 +1,319 @@
+// gfx950 kernels of the low-bit linear path.
+//
+//   gemv_kernel    decode regime (M <= 32): packed rows streamed with 16-byte loads,
+//                  dequantized in registers, multiplied on v_mfma_f32_16x16x32_f16 with
+//                  the activations as the (zero padded) A operand; optional split-K.
+//   gemm_kernel    prefill regime: 128x128x32 tiles, activations and dequantized weights
+//                  staged in LDS, v_mfma_f32_32x32x16_f16, fp32 accumulation.
+//   generic_kernel any shape / group size (odd K, rows starting mid-byte, groups < 32).
+//   unpack_kernel, dequant_kernel   bit-exact decode used by tests and by callers that
+//                  want the reference's dequantized fp16 weights on device.
+#pragma once
+#include "lb_common.h"
+
+namespace lb {
+
+constexpr int kGemvThreads = 256;  // 4 waves, 16 weight rows each
+
+template <int FMT, int MT, int U, bool SCALED>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(LinearParams p, int KC) {
+  constexpr int CPL = FormatTraits<FMT>::CPL;
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  constexpr int KSTEP = 4 * CPL;  // k covered by one wave-wide 16-byte load
+  constexpr int T8 = CPL / 8;     // MFMAs per lane load
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t *nf4_table = reinterpret_cast<uint32_t *>(smem);
+  f16 *xs = reinterpret_cast<f16 *>(smem + (FMT == FMT_NF4 ? 1024 : 0));
+  const int xs_ld = KC + 8;  // +16 bytes per row keeps the 16 A rows on distinct banks
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int n = blockIdx.x * 64 + wave * 16 + j;
+  const bool n_ok = n < p.N;
+  const int ks = blockIdx.y * p.kslice;
+  const int ke = min(p.K, ks + p.kslice);
+  const size_t row_bytes = BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * BITS / 8;
+  const uint8_t *wrow = p.codes + (n_ok ? (size_t)n * row_bytes : 0);
+  const f16 *srow = p.scales + (n_ok && SCALED ? (size_t)n * p.G : 0);
+
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+
+  f4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kc = ks; kc < ke; kc += KC) {
+    const int kend = min(ke, kc + KC);
+    const int blocks = (kend - kc) >> 3;
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < p.M * blocks; idx += kGemvThreads) {
+      const int m = idx / blocks, b = idx - m * blocks;
+      const h8 v = *reinterpret_cast<const h8 *>(p.x + (size_t)m * p.ldx + kc + b * 8);
+      *reinterpret_cast<h8 *>(xs + m * xs_ld + b * 8) = permute_block<FMT>(v);
+    }
+    __syncthreads();
+    for (int kb = kc; kb < kend; kb += KSTEP * U) {
+      u4 w[U];
+      h2 s2[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb + u * KSTEP + g * CPL;
+        const bool ok = n_ok && k < kend;
+        w[u] = ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k * BITS / 8) : u4{0u, 0u, 0u, 0u};
+        if constexpr (SCALED) {
+          const f16 s = ok ? srow[k / p.group] : (f16)0.0f;
+          s2[u] = h2{s, s};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb + u * KSTEP + g * CPL;
+        const bool kok = k < kend;
+#pragma unroll
+        for (int t = 0; t < T8; ++t) {
+          const h8 b = decode8<FMT, !SCALED>(w[u], t, s2[u], nf4_table);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + j;
+            h8 a = {};
+            if (m < p.M && kok) a = *reinterpret_cast<const h8 *>(xs + m * xs_ld + (k - kc) + 8 * t);
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mt], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // D layout of the 16x16 MFMA: lane (j, g) holds rows m = 4g + r of column j.
+  if (!n_ok) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mt * 16 + 4 * g + r;
+      if (m >= p.M) continue;
+      if (p.splits == 1) {
+        store_output(p, m, n, acc[mt][r]);
+      } else {
+        p.partial[((size_t)blockIdx.y * p.M + m) * p.N + n] = acc[mt][r];
+      }
+    }
+  }
+}
+
+// Sums split-K partials in a fixed order (deterministic) and applies the epilogue.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(LinearParams p) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)p.M * p.N) return;
+  const int m = (int)(idx / p.N), n = (int)(idx % p.N);
+  float s = 0.0f;
+  for (int sp = 0; sp < p.splits; ++sp) s += p.partial[((size_t)sp * p.M + m) * p.N + n];
+  store_output(p, m, n, s);
+}
+
+// Natural-order (k ascending) fp16 decode of one dword of codes for LDS staging.
+template <int FMT, bool SCALED>
+__device__ __forceinline__ h8 decode8_natural(uint32_t w0, uint32_t w1, h2 s2, const uint32_t *nf4_table) {
+  h2 p[4];
+  if constexpr (FMT == FMT_INT4) {
+    int4_pairs(w0, p);  // (c0,c4),(c1,c5),(c2,c6),(c3,c7)
+    h2 q0 = {p[0].x, p[1].x}, q1 = {p[2].x, p[3].x}, q2 = {p[0].y, p[1].y}, q3 = {p[2].y, p[3].y};
+    p[0] = q0; p[1] = q1; p[2] = q2; p[3] = q3;
+  } else if constexpr (FMT == FMT_NF4) {
+    p[0] = as_h2(nf4_table[w0 & 0xFFu]);
+    p[1] = as_h2(nf4_table[(w0 >> 8) & 0xFFu]);
+    p[2] = as_h2(nf4_table[(w0 >> 16) & 0xFFu]);
+    p[3] = as_h2(nf4_table[w0 >> 24]);
+  } else {  // INT8: two dwords
+    h2 a[2], b[2];
+    int8_pairs(w0, a);  // (b0,b2),(b1,b3)
+    int8_pairs(w1, b);
+    p[0] = h2{a[0].x, a[1].x}; p[1] = h2{a[0].y, a[1].y};
+    p[2] = h2{b[0].x, b[1].x}; p[3] = h2{b[0].y, b[1].y};
+  }
+  if (SCALED) { p[0] *= s2; p[1] *= s2; p[2] *= s2; p[3] *= s2; }
+  return __builtin_shufflevector(__builtin_shufflevector(p[0], p[1], 0, 1, 2, 3),
+                                 __builtin_shufflevector(p[2], p[3], 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 32, kGemmLd = kGemmBK + 8;
+
+template <int FMT, bool SCALED>
+__global__ __launch_bounds__(256) void gemm_kernel(LinearParams p) {
+  constexpr int BM = kGemmBM, BN = kGemmBN, BK = kGemmBK, LD = kGemmLd;
+  __shared__ __align__(16) f16 As[BM * LD];
+  __shared__ __align__(16) f16 Bs[BN * LD];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+
+  // A: 128 rows x 64 bytes -> two 16-byte chunks per thread.
+  const int a_row0 = tid >> 2, a_col = (tid & 3) * 8;  // chunk tid and tid + 256 (row + 64)
+  // B: weights for 128 rows x 32 k.  Each thread produces 16 k of one row.
+  const int b_row = tid >> 1, b_k = (tid & 1) * 16;
+  const int bn_row = bn + b_row;
+  const bool b_ok = bn_row < p.N;
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  const size_t row_bytes = BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * BITS / 8;
+  const uint8_t *wrow = p.codes + (b_ok ? (size_t)bn_row * row_bytes : 0);
+  const f16 *srow = p.scales + (b_ok && SCALED ? (size_t)bn_row * p.G : 0);
+
+  h8 a_reg[2];
+  u4 b_reg;  // up to 16 bytes: 16 codes (4-bit uses 8 bytes, int8 16 bytes, fp16 32 -> two loads)
+  u4 b_reg2;
+  f16 b_scale = (f16)0.0f;
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int m = bm + a_row0 + i * 64;
+      a_reg[i] = m < p.M ? *reinterpret_cast<const h8 *>(p.x + (size_t)m * p.ldx + k0 + a_col) : h8{};
+    }
+    const int k = k0 + b_k;
+    if constexpr (BITS == 4) {
+      const uint2 v = b_ok ? *reinterpret_cast<const uint2 *>(wrow + (size_t)k / 2) : uint2{0u, 0u};
+      b_reg = u4{v.x, v.y, 0u, 0u};
+    } else if constexpr (BITS == 8) {
+      b_reg = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k) : u4{0u, 0u, 0u, 0u};
+    } else {
+      b_reg = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k * 2) : u4{0u, 0u, 0u, 0u};
+      b_reg2 = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k * 2 + 16) : u4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (SCALED) b_scale = b_ok ? srow[k / p.group] : (f16)0.0f;
+  };
+
+  f16x acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
+
+  load_tile(0);
+  for (int k0 = 0; k0 < p.K; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<h8 *>(&As[(a_row0 + i * 64) * LD + a_col]) = a_reg[i];
+    {
+      const h2 s2 = {b_scale, b_scale};
+      h8 lo, hi;
+      if constexpr (BITS == 4) {
+        lo = decode8_natural<FMT, SCALED>(b_reg[0], 0u, s2, nf4_table);
+        hi = decode8_natural<FMT, SCALED>(b_reg[1], 0u, s2, nf4_table);
+      } else if constexpr (BITS == 8) {
+        lo = decode8_natural<FMT, SCALED>(b_reg[0], b_reg[1], s2, nf4_table);
+        hi = decode8_natural<FMT, SCALED>(b_reg[2], b_reg[3], s2, nf4_table);
+      } else {
+        lo = __builtin_bit_cast(h8, b_reg);
+        hi = __builtin_bit_cast(h8, b_reg2);
+      }
+      *reinterpret_cast<h8 *>(&Bs[b_row * LD + b_k]) = lo;
+      *reinterpret_cast<h8 *>(&Bs[b_row * LD + b_k + 8]) = hi;
+    }
+    __syncthreads();
+    if (k0 + BK < p.K) load_tile(k0 + BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      h8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const h8 *>(&As[(wm * 64 + i * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        b[jj] = *reinterpret_cast<const h8 *>(&Bs[(wn * 64 + jj * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[jj], acc[i][jj], 0, 0, 0);
+    }
+  }
+
+  // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int n = bn + wn * 64 + jj * 32 + (lane & 31);
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < p.M) store_output(p, m, n, acc[i][jj][r]);
+      }
+    }
+}
+
+// Decoded integer value of element (n, k) for the flat packed layout.
+__device__ __forceinline__ int decode_code(int fmt, const uint8_t *codes, size_t flat) {
+  if (fmt == FMT_INT8) return (int)(int8_t)codes[flat];
+  const uint8_t byte = codes[flat >> 1];
+  const int c = (flat & 1) ? (byte >> 4) : (byte & 15);
+  return fmt == FMT_INT4 ? ((c ^ 8) - 8) : c;
+}
+
+// Weight value used by the linear kernels: fp16(q*s) (or q for per-row int8, raw fp16).
+__device__ __forceinline__ float weight_value(int fmt, const LinearParams &p, int n, int k) {
+  if (fmt == FMT_FP16) return (float)reinterpret_cast<const f16 *>(p.codes)[(size_t)n * p.ldw + k];
+  const int q = decode_code(fmt, p.codes, (size_t)n * p.K + k);
+  f16 qh;
+  if (fmt == FMT_NF4) {
+    const float lit[16] = {LB_NF4_LITERALS};
+    qh = (f16)lit[q];
+  } else {
+    qh = (f16)(float)q;
+  }
+  if (p.per_row) return (float)qh;
+  return (float)(f16)(qh * p.scales[(size_t)n * p.G + k / p.group]);
+}
+
+// One wave per (row n, 8 activation rows): any shape and group size.
+__global__ __launch_bounds__(64) void generic_kernel(LinearParams p, int fmt) {
+  const int n = blockIdx.x, m0 = blockIdx.y * 8, lane = threadIdx.x;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int k = lane; k < p.K; k += 64) {
+    const float w = weight_value(fmt, p, n, k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (m0 + i < p.M) acc[i] += (float)p.x[(size_t)(m0 + i) * p.ldx + k] * w;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, 64);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (m0 + i < p.M) store_output(p, m0 + i, n, acc[i]);
+  }
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(int fmt, const uint8_t *codes, size_t count, int8_t *out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) out[i] = (int8_t)decode_code(fmt, codes, i);
+}
+
+__global__ __launch_bounds__(256) void dequant_kernel(int fmt, const uint8_t *codes, const f16 *scales,
+                                                      int K, int group, int G, size_t count, f16 *out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const int q = decode_code(fmt, codes, i);
+  f16 qh;
+  if (fmt == FMT_NF4) {
+    const float lit[16] = {LB_NF4_LITERALS};
+    qh = (f16)lit[q];
+  } else {
+    qh = (f16)(float)q;
+  }
+  const size_t n = i / K;
+  const int k = (int)(i - n * K);
+  out[i] = qh * scales[n * G + k / group];
+}
+
+}  // namespace lb

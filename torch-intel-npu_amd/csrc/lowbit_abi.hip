@@ -1,0 +1,394 @@
+// C-ABI of liblowbit_hip.so: argument validation, regime dispatch and launches.
+// Declarations and contracts: include/lowbit_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/lowbit_hip.h"
+#include "lb_kernels.h"
+
+using namespace lb;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+lb_status fail(lb_status status, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+lb_status ok() {
+  g_last_error.clear();
+  return LB_OK;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+struct Range {
+  uintptr_t lo = 0, hi = 0;  // [lo, hi)
+  const char *name = "";
+};
+
+Range range_of(const void *p, size_t bytes, const char *name) {
+  Range r;
+  r.lo = reinterpret_cast<uintptr_t>(p);
+  r.hi = r.lo + bytes;
+  r.name = name;
+  return r;
+}
+
+bool overlaps(const Range &a, const Range &b) {
+  return a.lo != a.hi && b.lo != b.hi && a.lo < b.hi && b.lo < a.hi;
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2 };
+
+constexpr int kGemvMaxM = 32;
+constexpr size_t kGemvLdsBudget = 48 * 1024;
+
+int codes_per_load(int fmt) { return fmt == FMT_FP16 ? 8 : fmt == FMT_INT8 ? 16 : 32; }
+
+struct Plan {
+  int path = PATH_GENERIC;
+  int splits = 1, kslice = 0, kc = 0;
+  size_t z_off = 0, z_bytes = 0;
+  size_t d_off = 0, d_bytes = 0;
+  size_t part_off = 0, part_bytes = 0;
+  size_t total = 0;
+};
+
+// Whether the MFMA fast paths can run these arguments.
+bool fast_eligible(int fmt, int64_t K, int64_t group, const void *codes, const void *x, int64_t ldx, int64_t ldw) {
+  if (K % 32 != 0) return false;
+  if (fmt != FMT_FP16 && !(group == K || group % 32 == 0)) return false;
+  if (!aligned(codes, 16) || !aligned(x, 16) || ldx % 8 != 0) return false;
+  if (fmt == FMT_FP16 && ldw % 8 != 0) return false;
+  return true;
+}
+
+void gemv_split(int fmt, int64_t M, int64_t N, int64_t K, int *splits, int *kslice, int *kc) {
+  const int kstep = 4 * codes_per_load(fmt);
+  const int64_t wgs = (N + 63) / 64;
+  int64_t s = 1;
+  if (wgs < 512) s = std::min<int64_t>((512 + wgs - 1) / wgs, K / (4 * kstep));
+  s = std::max<int64_t>(s, 1);
+  int64_t ks = round_up((K + s - 1) / s, kstep);
+  s = (K + ks - 1) / ks;
+  *splits = (int)s;
+  *kslice = (int)ks;
+  const int64_t budget = (int64_t)(kGemvLdsBudget / 2 / std::max<int64_t>(M, 1)) - 8;
+  int64_t c = std::max<int64_t>(kstep, budget / kstep * kstep);
+  *kc = (int)std::min<int64_t>(c, ks);
+}
+
+Plan make_plan(const lb_linear_args *a, bool eligible) {
+  Plan pl;
+  const int fmt = (int)a->format;
+  if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) {
+    pl.path = PATH_GENERIC;
+  } else if (a->flags & LB_FLAG_FORCE_GEMM) {
+    pl.path = PATH_GEMM;
+  } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) {
+    pl.path = PATH_GEMV;
+  } else {
+    pl.path = PATH_GEMM;
+  }
+  size_t off = 0;
+  if (a->rank > 0) {
+    pl.z_off = off;
+    pl.z_bytes = (size_t)a->M * a->rank * 2;
+    off = round_up(off + pl.z_bytes, 256);
+    if (pl.path != PATH_GEMV) {
+      pl.d_off = off;
+      pl.d_bytes = (size_t)a->M * a->N * 2;
+      off = round_up(off + pl.d_bytes, 256);
+    }
+  }
+  if (pl.path == PATH_GEMV) {
+    gemv_split(fmt, a->M, a->N, a->K, &pl.splits, &pl.kslice, &pl.kc);
+    if (pl.splits > 1) {
+      pl.part_off = off;
+      pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
+      off = round_up(off + pl.part_bytes, 256);
+    }
+  }
+  pl.total = off;
+  return pl;
+}
+
+lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_linear: args is NULL");
+  if (a->struct_size < sizeof(lb_linear_args))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: struct_size %u < %zu", a->struct_size, sizeof(lb_linear_args));
+  if (a->format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "lb_linear: unknown format %u", a->format);
+  if (a->M <= 0 || a->N <= 0 || a->K <= 0)
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: M, N, K must be positive (got %lld, %lld, %lld)",
+                (long long)a->M, (long long)a->N, (long long)a->K);
+  if (a->M > INT32_MAX || a->N > INT32_MAX || a->K > INT32_MAX || a->M * a->N > (int64_t)1 << 40 ||
+      a->N * a->K > (int64_t)1 << 40)
+    return fail(LB_UNSUPPORTED, "lb_linear: extents exceed the supported range");
+  const bool dense = a->format == LB_FORMAT_FP16;
+  if (!dense && (a->group_size < 1 || a->group_size > a->K || a->K % a->group_size != 0))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: group_size %lld must divide K=%lld", (long long)a->group_size,
+                (long long)a->K);
+  if (!a->codes || !a->x || !a->y || (!dense && !a->scales))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: codes, scales, x and y must be non-NULL");
+  if (a->ldx < a->K || a->ldy < a->N)
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: ldx >= K and ldy >= N required");
+  if (a->rank < 0 || a->rank > std::min(a->N, a->K))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: rank %lld outside 0..min(N,K)", (long long)a->rank);
+  const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;
+  if (a->rank > 0 && (!a->down || !a->up || up_ld < a->rank))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: correction needs down, up and up_ld >= rank");
+  if (!aligned(a->x, 2) || !aligned(a->y, 2) || (a->scales && !aligned(a->scales, 2)) ||
+      (a->bias && !aligned(a->bias, 2)) || (dense && !aligned(a->codes, 2)) ||
+      (a->rank > 0 && (!aligned(a->down, 2) || !aligned(a->up, 2))))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: fp16 buffers must be 2-byte aligned");
+
+  const int64_t code_bytes = dense ? a->N * a->K * 2
+                             : a->format == LB_FORMAT_INT8 ? a->N * a->K
+                                                           : (a->N * a->K + 1) / 2;
+  const Range y = range_of(a->y, (size_t)((a->M - 1) * a->ldy + a->N) * 2, "y");
+  const Range inputs[] = {
+      range_of(a->x, (size_t)((a->M - 1) * a->ldx + a->K) * 2, "x"),
+      range_of(a->codes, (size_t)code_bytes, "codes"),
+      range_of(a->scales, dense ? 0 : (size_t)(a->N * (a->K / a->group_size) * 2), "scales"),
+      range_of(a->bias, a->bias ? (size_t)a->N * 2 : 0, "bias"),
+      range_of(a->down, a->rank > 0 ? (size_t)(a->rank * a->K * 2) : 0, "down"),
+      range_of(a->up, a->rank > 0 ? (size_t)(((a->N - 1) * up_ld + a->rank) * 2) : 0, "up"),
+      range_of(a->workspace, a->workspace ? a->workspace_bytes : 0, "workspace"),
+  };
+  for (const Range &r : inputs)
+    if (overlaps(y, r)) return fail(LB_INVALID_ARGUMENT, "lb_linear: y overlaps %s", r.name);
+  for (int i = 0; i < 6; ++i)
+    if (overlaps(inputs[6], inputs[i]))
+      return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace overlaps %s", inputs[i].name);
+
+  const bool eligible = fast_eligible((int)a->format, a->K, dense ? a->K : a->group_size, a->codes, a->x, a->ldx, a->K);
+  if ((a->flags & LB_FLAG_FORCE_GEMV) && a->M > kGemvMaxM)
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: LB_FLAG_FORCE_GEMV needs M <= %d", kGemvMaxM);
+  if ((a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM)) && !(a->flags & LB_FLAG_FORCE_GENERIC) && !eligible)
+    return fail(LB_UNSUPPORTED,
+                "lb_linear: forced MFMA path needs K %% 32 == 0, group == K or group %% 32 == 0, "
+                "16-byte aligned codes/x and ldx %% 8 == 0");
+  if (__builtin_popcount(a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC)) > 1)
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: at most one LB_FLAG_FORCE_* flag");
+  *plan = make_plan(a, eligible);
+  if (check_workspace && plan->total > 0) {
+    if (!a->workspace || a->workspace_bytes < plan->total)
+      return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace of %zu bytes required (got %zu)", plan->total,
+                  a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace must be 256-byte aligned");
+  }
+  return ok();
+}
+
+template <int FMT, int MT, bool SCALED>
+void launch_gemv_t(const LinearParams &p, int kc, hipStream_t s) {
+  const dim3 grid((p.N + 63) / 64, p.splits);
+  const size_t lds = (FMT == FMT_NF4 ? 1024 : 0) + (size_t)p.M * (kc + 8) * 2;
+  hipLaunchKernelGGL((gemv_kernel<FMT, MT, 2, SCALED>), grid, dim3(kGemvThreads), lds, s, p, kc);
+}
+
+template <int FMT, bool SCALED>
+void launch_gemv_m(const LinearParams &p, int kc, hipStream_t s) {
+  if (p.M <= 16)
+    launch_gemv_t<FMT, 1, SCALED>(p, kc, s);
+  else
+    launch_gemv_t<FMT, 2, SCALED>(p, kc, s);
+}
+
+void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kc, hipStream_t s) {
+  switch (fmt) {
+    case FMT_INT8: scaled ? launch_gemv_m<FMT_INT8, true>(p, kc, s) : launch_gemv_m<FMT_INT8, false>(p, kc, s); break;
+    case FMT_INT4: launch_gemv_m<FMT_INT4, true>(p, kc, s); break;
+    case FMT_NF4: launch_gemv_m<FMT_NF4, true>(p, kc, s); break;
+    default: launch_gemv_m<FMT_FP16, false>(p, kc, s); break;
+  }
+  if (p.splits > 1) {
+    const size_t count = (size_t)p.M * p.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p);
+  }
+}
+
+template <int FMT, bool SCALED>
+void launch_gemm_t(const LinearParams &p, hipStream_t s) {
+  const dim3 grid((p.N + kGemmBN - 1) / kGemmBN, (p.M + kGemmBM - 1) / kGemmBM);
+  hipLaunchKernelGGL((gemm_kernel<FMT, SCALED>), grid, dim3(256), 0, s, p);
+}
+
+void launch_gemm(int fmt, bool scaled, const LinearParams &p, hipStream_t s) {
+  switch (fmt) {
+    case FMT_INT8: scaled ? launch_gemm_t<FMT_INT8, true>(p, s) : launch_gemm_t<FMT_INT8, false>(p, s); break;
+    case FMT_INT4: launch_gemm_t<FMT_INT4, true>(p, s); break;
+    case FMT_NF4: launch_gemm_t<FMT_NF4, true>(p, s); break;
+    default: launch_gemm_t<FMT_FP16, false>(p, s); break;
+  }
+}
+
+void launch_generic(int fmt, const LinearParams &p, hipStream_t s) {
+  hipLaunchKernelGGL(generic_kernel, dim3(p.N, (p.M + 7) / 8), dim3(64), 0, s, p, fmt);
+}
+
+LinearParams base_params(int fmt, int64_t M, int64_t N, int64_t K, int64_t group, const void *codes,
+                         const void *scales, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t ldw) {
+  LinearParams p{};
+  p.codes = static_cast<const uint8_t *>(codes);
+  p.scales = static_cast<const f16 *>(scales);
+  p.x = static_cast<const f16 *>(x);
+  p.y = static_cast<f16 *>(y);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.group = (int)group;
+  p.G = (int)(K / group);
+  p.ldx = (int)ldx;
+  p.ldy = (int)ldy;
+  p.ldw = (int)ldw;
+  p.per_row = fmt == FMT_INT8 && group == K;
+  p.splits = 1;
+  p.kslice = (int)K;
+  return p;
+}
+
+// Dense fp16 product out[M, N] = fp16(in[M, K] . W[N, K]^T), used for the correction stages.
+void dense_fp16(int64_t M, int64_t N, int64_t K, const void *w, int64_t ldw, const void *in, int64_t ld_in,
+                void *out, hipStream_t s) {
+  LinearParams p = base_params(FMT_FP16, M, N, K, K, w, nullptr, in, ld_in, out, N, ldw);
+  const bool eligible = fast_eligible(FMT_FP16, K, K, w, in, ld_in, ldw);
+  if (!eligible) {
+    launch_generic(FMT_FP16, p, s);
+  } else if (M <= kGemvMaxM) {
+    int splits, kslice, kc;
+    gemv_split(FMT_FP16, M, N, K, &splits, &kslice, &kc);
+    p.splits = 1;
+    p.kslice = (int)K;
+    kc = std::min<int>(kc, (int)K);
+    launch_gemv(FMT_FP16, false, p, kc, s);
+  } else {
+    launch_gemm(FMT_FP16, false, p, s);
+  }
+}
+
+lb_status launch_status(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LB_DEVICE_FAILED, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int lb_abi_version(void) { return LB_ABI_VERSION; }
+
+const char *lb_status_name(lb_status status) {
+  switch (status) {
+    case LB_OK: return "LB_OK";
+    case LB_INVALID_ARGUMENT: return "LB_INVALID_ARGUMENT";
+    case LB_OUT_OF_MEMORY: return "LB_OUT_OF_MEMORY";
+    case LB_UNSUPPORTED: return "LB_UNSUPPORTED";
+    case LB_DEVICE_FAILED: return "LB_DEVICE_FAILED";
+    case LB_INTERNAL: return "LB_INTERNAL";
+  }
+  return "LB_UNKNOWN_STATUS";
+}
+
+const char *lb_last_error(void) { return g_last_error.c_str(); }
+
+lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes) {
+  if (!bytes) return fail(LB_INVALID_ARGUMENT, "lb_workspace_bytes: bytes is NULL");
+  Plan plan;
+  const lb_status st = validate(args, false, &plan);
+  if (st != LB_OK) return st;
+  *bytes = plan.total;
+  return ok();
+}
+
+lb_status lb_linear(const lb_linear_args *a, void *stream) {
+  Plan plan;
+  lb_status st = validate(a, true, &plan);
+  if (st != LB_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int fmt = (int)a->format;
+  const bool dense = fmt == FMT_FP16;
+  LinearParams p = base_params(fmt, a->M, a->N, a->K, dense ? a->K : a->group_size, a->codes, a->scales, a->x,
+                               a->ldx, a->y, a->ldy, a->K);
+  p.bias = static_cast<const f16 *>(a->bias);
+  uint8_t *ws = static_cast<uint8_t *>(a->workspace);
+  if (a->rank > 0) {
+    const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;
+    f16 *z = reinterpret_cast<f16 *>(ws + plan.z_off);
+    // z = fp16(x . V^T)  (reference torch_npu_smollm.py:162, first MatMul of :256)
+    dense_fp16(a->M, a->rank, a->K, a->down, a->K, a->x, a->ldx, z, s);
+    if (plan.path == PATH_GEMV) {
+      p.z = z;
+      p.up = static_cast<const f16 *>(a->up);
+      p.rank = (int)a->rank;
+      p.up_ld = (int)up_ld;
+    } else {
+      // d = fp16(z . U^T)  (second MatMul of torch_npu_smollm.py:257)
+      f16 *d = reinterpret_cast<f16 *>(ws + plan.d_off);
+      dense_fp16(a->M, a->N, a->rank, a->up, up_ld, z, a->rank, d, s);
+      p.delta = d;
+    }
+  }
+  const bool scaled = !dense && !p.per_row;
+  if (plan.path == PATH_GEMV) {
+    p.splits = plan.splits;
+    p.kslice = plan.kslice;
+    p.partial = reinterpret_cast<float *>(ws + plan.part_off);
+    launch_gemv(fmt, scaled, p, plan.kc, s);
+  } else if (plan.path == PATH_GEMM) {
+    launch_gemm(fmt, scaled, p, s);
+  } else {
+    launch_generic(fmt, p, s);
+  }
+  return launch_status("lb_linear");
+}
+
+lb_status lb_unpack_codes(uint32_t format, int64_t N, int64_t K, const void *codes, int8_t *out, void *stream) {
+  if (format > LB_FORMAT_NF4) return fail(LB_INVALID_ARGUMENT, "lb_unpack_codes: format must be int8/int4/nf4");
+  if (N <= 0 || K <= 0 || !codes || !out) return fail(LB_INVALID_ARGUMENT, "lb_unpack_codes: bad arguments");
+  const size_t count = (size_t)N * (size_t)K;
+  const size_t code_bytes = format == LB_FORMAT_INT8 ? count : (count + 1) / 2;
+  if (overlaps(range_of(out, count, "out"), range_of(codes, code_bytes, "codes")))
+    return fail(LB_INVALID_ARGUMENT, "lb_unpack_codes: out overlaps codes");
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), (int)format, static_cast<const uint8_t *>(codes), count, out);
+  return launch_status("lb_unpack_codes");
+}
+
+lb_status lb_dequantize(uint32_t format, int64_t N, int64_t K, int64_t group_size, const void *codes,
+                        const void *scales, void *w_out, void *stream) {
+  if (format > LB_FORMAT_NF4) return fail(LB_INVALID_ARGUMENT, "lb_dequantize: format must be int8/int4/nf4");
+  if (N <= 0 || K <= 0 || K > INT32_MAX || !codes || !scales || !w_out || group_size < 1 || group_size > K ||
+      K % group_size != 0)
+    return fail(LB_INVALID_ARGUMENT, "lb_dequantize: bad arguments");
+  if (!aligned(scales, 2) || !aligned(w_out, 2))
+    return fail(LB_INVALID_ARGUMENT, "lb_dequantize: fp16 buffers must be 2-byte aligned");
+  const size_t count = (size_t)N * (size_t)K;
+  const size_t code_bytes = format == LB_FORMAT_INT8 ? count : (count + 1) / 2;
+  const Range out = range_of(w_out, count * 2, "w_out");
+  if (overlaps(out, range_of(codes, code_bytes, "codes")) ||
+      overlaps(out, range_of(scales, (size_t)N * (K / group_size) * 2, "scales")))
+    return fail(LB_INVALID_ARGUMENT, "lb_dequantize: w_out overlaps an input");
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), (int)format, static_cast<const uint8_t *>(codes),
+                     static_cast<const f16 *>(scales), (int)K, (int)group_size, (int)(K / group_size), count,
+                     static_cast<f16 *>(w_out));
+  return launch_status("lb_dequantize");
+}
+
+}  // extern "C"

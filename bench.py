@@ -1,0 +1,297 @@
+"""Benchmark of the MI355X low-bit linear path (one JSON line on stdout).
+
+Headline workload: INT4 group-wise dequant-GEMV at M=1 over
+every SmolLM-135M linear shape -- q/o 576x576, k/v 192x576, gate/up 1536x576,
+down 576x1536, lm_head 49152x576.  The reference requires K % group == 0, so K=576
+shapes use group 64 and K=1536 uses group 128.  One step = one pass over the eight
+linears, each reading a distinct weight replica from a pool larger than the 256 MB
+MALL, so the bandwidth is HBM bandwidth.  Launches are replayed from HIP graphs so
+host launch cost is not in the timed region; inputs are resident in HBM beforehand.
+
+Also reported: the same pass at M=4 and M=16, per-kernel GB/s, the config-5 roofline
+sweep, prefill GEMM TFLOP/s (configs 3 and 5), and the CPU baseline (the reference's
+CPU path: fp32 torch matmul on pre-dequantized weights) timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cpu]
+       python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / 'torch-intel-npu_amd'):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = 'dequant-GEMV HBM GB/s (% of peak) at M=1; decode tokens/sec SmolLM-135M W8'
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+POOL_BYTES = 1.1 * 2 ** 30
+
+# (name, N, K, group) -- config 2 shapes with the group substitution for K=576.
+SMOL_SHAPES = [('q_proj', 576, 576, 64), ('k_proj', 192, 576, 64), ('v_proj', 192, 576, 64),
+               ('o_proj', 576, 576, 64), ('gate_proj', 1536, 576, 64), ('up_proj', 1536, 576, 64),
+               ('down_proj', 576, 1536, 128), ('lm_head', 49152, 576, 64)]
+LLAMA_SHAPES = [('4096x4096', 4096, 4096, 128), ('1024x4096', 1024, 4096, 128),
+                ('14336x4096', 14336, 4096, 128), ('4096x14336', 4096, 14336, 128),
+                ('128256x4096', 128256, 4096, 128)]
+
+
+def log(*parts):
+    print('[bench]', *parts, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(fmt, m, n, k, group):
+    code = n * k if fmt == 'int8' else n * k // 2
+    return code + 2 * n * (k // group) + 2 * m * k + 2 * m * n + (32 if fmt == 'nf4' else 0)
+
+
+def make_weight(fmt, n, k, group, seed):
+    from torch_npu_lowbit import quantize_weight
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(n, k, generator=g) * 0.02
+    return quantize_weight(w, format=fmt, group_size=group)
+
+
+class Linear:
+    """A packed weight replicated `copies` times on the device, plus fixed x / y buffers."""
+
+    def __init__(self, packed, m, copies, device, seed):
+        import lowbit_hip
+        self.packed = packed
+        self.fmt = packed.format
+        self.n, self.k = packed.shape
+        self.group = packed.group_size
+        self.m = m
+        codes, scales = packed.device_tensors(device)
+        self.replicas = [(codes.clone(), scales.clone()) for _ in range(copies)]
+        g = torch.Generator().manual_seed(seed)
+        self.x = torch.randn(m, self.k, generator=g).half().to(device)
+        self.y = torch.empty(m, self.n, dtype=torch.float16, device=device)
+        self.calls = [lowbit_hip.PreparedLinear(self.x, c, s, format=self.fmt, N=self.n, K=self.k,
+                                                group_size=self.group, out=self.y) for c, s in self.replicas]
+        self.bytes = algorithmic_bytes(self.fmt, m, self.n, self.k, self.group)
+        self.flops = 2 * m * self.n * self.k
+
+
+def copies_for(bytes_per_copy, cap=64):
+    return int(max(2, min(cap, np.ceil(POOL_BYTES / bytes_per_copy))))
+
+
+def capture(fns, stream):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for fn in fns:
+            fn()
+    return graph
+
+
+def time_graphs(graphs, count, stream):
+    """Replay graphs[i % len] for i < count between two events on `stream`; returns ms."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for i in range(count):
+            graphs[i % len(graphs)].replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop)
+
+
+def kernel_time_us(linear, stream, replays=8):
+    """Average duration of one launch of `linear`, over a graph of all its replicas."""
+    for call in linear.calls[:2]:
+        call.run()
+    graph = capture([c.run for c in linear.calls], stream)
+    time_graphs([graph], 2, stream)
+    ms = time_graphs([graph], replays, stream)
+    return 1000.0 * ms / (replays * len(linear.calls))
+
+
+def smol_pass(m, device, stream, steps, warmup):
+    linears = []
+    total = sum(algorithmic_bytes('int4', m, n, k, g) for _, n, k, g in SMOL_SHAPES)
+    copies = copies_for(total)
+    for i, (name, n, k, g) in enumerate(SMOL_SHAPES):
+        linears.append(Linear(make_weight('int4', n, k, g, 100 + i), m, copies, device, 200 + i))
+    for lin in linears:
+        lin.calls[0].run()
+    graphs = [capture([lin.calls[r].run for lin in linears], stream) for r in range(copies)]
+    time_graphs(graphs, warmup, stream)
+    ms = time_graphs(graphs, steps, stream)
+    per_kernel = {}
+    for (name, *_), lin in zip(SMOL_SHAPES, linears):
+        us = kernel_time_us(lin, stream)
+        per_kernel[name] = dict(us=round(us, 3), gbs=round(lin.bytes / us / 1e3, 1))
+    return dict(ms_per_step=ms / steps, bytes_per_step=total, copies=copies,
+                gbs=total / (ms / steps) / 1e6, per_kernel=per_kernel, linears=linears)
+
+
+def sweep(device, stream, quick):
+    rows = []
+    specs = []
+    for m in ((1, 32) if quick else (1, 8, 32)):
+        for name, n, k, g in LLAMA_SHAPES:
+            specs.append(('int4', m, n, k, g, name))
+    gemm = [('nf4', 512, 2560, 960, 64, 'smol360m_gate'), ('nf4', 2048, 2560, 960, 64, 'smol360m_gate'),
+            ('nf4', 512, 960, 2560, 64, 'smol360m_down'), ('int4', 1024, 14336, 4096, 128, '14336x4096'),
+            ('int4', 1024, 4096, 4096, 128, '4096x4096')]
+    if not quick:
+        gemm += [('nf4', 128, 2560, 960, 64, 'smol360m_gate'), ('int4', 256, 14336, 4096, 128, '14336x4096'),
+                 ('int8', 256, 576, 576, 576, 'smol135m_q_prefill')]
+    specs += gemm
+    for i, (fmt, m, n, k, g, name) in enumerate(specs):
+        packed = make_weight(fmt, n, k, g, 300 + i)
+        bytes_w = algorithmic_bytes(fmt, 0, n, k, g)
+        lin = Linear(packed, m, copies_for(bytes_w, cap=32), device, 400 + i)
+        us = kernel_time_us(lin, stream, replays=4)
+        row = dict(fmt=fmt, M=m, N=n, K=k, group=g, shape=name, us=round(us, 2),
+                   gbs=round(lin.bytes / us / 1e3, 1), tflops=round(lin.flops / us / 1e6, 2))
+        row['hbm_frac' if m <= 32 else 'mfma_frac'] = round(
+            row['gbs'] / HBM_PEAK_GBS if m <= 32 else row['tflops'] / FP16_MFMA_PEAK_TFLOPS, 4)
+        rows.append(row)
+        log('sweep', json.dumps(row))
+        del lin
+        torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_leg(budget_s):
+    from oracle import cpu_baseline
+    problems = []
+    for i, (name, n, k, g) in enumerate(SMOL_SHAPES):
+        packed = make_weight('int4', n, k, g, 100 + i)
+        x = torch.randn(1, k, generator=torch.Generator().manual_seed(200 + i)).half().numpy()
+        problems.append((x, 'int4', (n, k), g, packed.data, packed.scales))
+    cpu = cpu_baseline.CpuPass(problems)
+    pre, deq, rounds = cpu_baseline.time_pass(cpu, budget_s=budget_s)
+    total = sum(algorithmic_bytes('int4', 1, n, k, g) for _, n, k, g in SMOL_SHAPES)
+    return dict(value=round(total / pre / 1e9, 3), unit='GB/s', cores=cpu.threads, kind='port',
+                sample=(f'{rounds} interleaved rounds (median) of one M=1 pass over the 8 SmolLM-135M '
+                        f'INT4 shapes: fp32 torch CPU matmul on pre-dequantized weights, fp16 out '
+                        f'(reference timing method, torch_npu_lowbit_demo.py:65,71); host {cpu_baseline.cpu_model()}'),
+                ms_per_pass=round(pre * 1e3, 3), dequant_inclusive_ms_per_pass=round(deq * 1e3, 3),
+                dequant_inclusive_gbs=round(total / deq / 1e9, 3))
+
+
+def profile_kernel(device, stream):
+    """Dominant kernel (lm_head INT4 GEMV, M=1) over its replica pool, then a known-size copy."""
+    name, n, k, g = SMOL_SHAPES[-1]
+    lin = Linear(make_weight('int4', n, k, g, 107), 1, copies_for(algorithmic_bytes('int4', 0, n, k, g)),
+                 device, 207)
+    for _ in range(4):
+        for call in lin.calls:
+            call.run()
+    src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(profile='lm_head int4 g64 M=1', launches=4 * len(lin.calls),
+                          algorithmic_bytes=lin.bytes, copy_bytes=src.numel())), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=256)
+    ap.add_argument('--warmup', type=int, default=32)
+    ap.add_argument('--quick', action='store_true', help='shorter sweep')
+    ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--no-sweep', action='store_true')
+    ap.add_argument('--cpu-seconds', type=float, default=15.0)
+    ap.add_argument('--profile-kernel', action='store_true')
+    args = ap.parse_args()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps(dict(error='single-GPU build: the low-bit linear path is measured on one MI355X; '
+                                    'multi-GPU sharding is design-only (see DESIGN.md)', n_gpus=args.gpus)))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps(dict(error='no ROCm device visible')))
+        sys.exit(1)
+    import lowbit_hip
+    lowbit_hip.library()
+    device = torch.device('cuda:0')
+    stream = torch.cuda.Stream(device)
+    torch.manual_seed(0)
+    if args.profile_kernel:
+        profile_kernel(device, stream)
+        return
+
+    t0 = time.time()
+    log('config-2 pass, M=1')
+    head = smol_pass(1, device, stream, args.steps, args.warmup)
+    log(f"M=1: {head['gbs']:.1f} GB/s per pass, {head['ms_per_step'] * 1e3:.2f} us/step")
+    dominant = head['per_kernel']['lm_head']
+    lm = head['linears'][-1]
+    del head['linears']
+    others = {}
+    for m in (4, 16):
+        log(f'config-2 pass, M={m}')
+        r = smol_pass(m, device, stream, max(32, args.steps // 4), 8)
+        del r['linears']
+        others[f'M={m}'] = dict(gbs=round(r['gbs'], 1), us_per_step=round(r['ms_per_step'] * 1e3, 2),
+                                per_kernel=r['per_kernel'])
+        torch.cuda.empty_cache()
+    rows = [] if args.no_sweep else sweep(device, stream, args.quick)
+    cpu = None if args.no_cpu else cpu_leg(args.cpu_seconds)
+    achieved = lm.bytes / dominant['us'] / 1e3
+    result = {
+        'metric': METRIC,
+        'value': round(head['gbs'], 1),
+        'unit': 'GB/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(head['ms_per_step'], 5),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'int4 codes -> fp16 weights, fp32 accumulate',
+        'data': 'synthetic: seeded N(0,0.02) weights quantized by quantize_weight, N(0,1) fp16 activations',
+        'config': {
+            'workload': 'configs[1]: INT4 group-wise dequant-GEMV, M=1, all SmolLM-135M linear shapes '
+                        '(q,k,v,o 576/192x576 g64; gate,up 1536x576 g64; down 576x1536 g128; lm_head 49152x576 g64)',
+            'step': 'one pass over the 8 linears (8 kernel launches replayed from a HIP graph)',
+            'weight_pool_bytes': int(head['bytes_per_step'] * head['copies']),
+            'replicas': head['copies'],
+            'hbm_frac_of_pass': round(head['gbs'] / HBM_PEAK_GBS, 4),
+        },
+        'roofline': {
+            'kernel': 'gemv_kernel<INT4> lm_head 49152x576 g64, M=1',
+            'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+            'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_per_launch(),
+            'algorithmic_bytes_per_launch': lm.bytes, 'avg_launch_us': dominant['us'],
+        },
+        'cpu_baseline': cpu,
+        'per_kernel_M1': head['per_kernel'],
+        'passes': others,
+        'sweep': rows,
+        'wall_s': round(time.time() - t0, 1),
+    }
+    print(json.dumps(result), flush=True)
+
+
+def traffic_per_launch():
+    """HBM bytes per dominant-kernel launch from the committed rocprofv3 --pmc summary, if any."""
+    path = ROOT / 'profiles' / 'traffic_lm_head_int4_m1.json'
+    if path.exists():
+        try:
+            return json.loads(path.read_text()).get('traffic_bytes_per_launch')
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+if __name__ == '__main__':
+    main()

@@ -24,7 +24,7 @@ REL_L2 = 1e-3
 
 
 def to_dev(array, device):
-    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+    return torch.from_numpy(np.array(array, copy=True)).to(device)
 
 
 def problem(rng, fmt, m, n, k, group, rank=0, bias=False, xscale=1.0):
@@ -101,7 +101,7 @@ def test_dequantize_bit_exact_all_codes_and_scales(device, fmt):
 
 
 @pytest.mark.parametrize('fmt', ['int8', 'int4', 'nf4'])
-@pytest.mark.parametrize('shape', [(5, 64, 32), (11, 200, 96), (3, 17, 17)])
+@pytest.mark.parametrize('shape', [(5, 64, 32), (11, 192, 96), (3, 17, 17)])
 def test_dequantize_bit_exact_quantized(device, fmt, shape):
     n, k, group = shape
     announce('dequantize-q', fmt, shape)
@@ -235,7 +235,8 @@ def test_noncontiguous_and_strided_activations(device):
     view = wide[:, 8:136]                          # row stride 200, 16-byte aligned start
     transposed = to_dev(np.ascontiguousarray(p['x'].T), device).t()   # column-major view
     want = expected(p)
-    misaligned = wide[:, 1:129]                    # 2-byte aligned start: generic kernel
+    other = torch.zeros(6, 200, dtype=torch.float16, device=device)
+    misaligned = other[:, 1:129]                   # 2-byte aligned start: generic kernel
     misaligned.copy_(view)
     for x in (view, transposed, misaligned):
         y = lowbit_hip.linear(x, codes, scales, format='int4', N=64, K=128, group_size=32)

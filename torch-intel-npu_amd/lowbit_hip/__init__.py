@@ -170,3 +170,42 @@ def dequantize(codes, scales, *, format, N, K, group_size):
     _check(library().lb_dequantize(FORMATS[format], N, K, group_size, _ptr(codes), _ptr(scales), _ptr(out),
                                    _stream(codes.device)), 'lb_dequantize')
     return out
+
+
+class PreparedLinear:
+    """A fixed lb_linear call (shapes, buffers and workspace bound once) for hot loops.
+
+    Holds references to every tensor it points at, so the device memory stays alive.
+    run() enqueues on the current stream of the output's device (or `stream`), so it can be
+    captured into a HIP graph with torch.cuda.graph.
+    """
+
+    def __init__(self, x, codes, scales, *, format, N, K, group_size, out, bias=None, down=None, up=None,
+                 rank=0, flags=0, workspace=None):
+        _device_tensor(x, 'x', torch.float16)
+        _device_tensor(out, 'out', torch.float16)
+        if x.ndim != 2 or x.shape[1] != K or (K > 1 and x.stride(1) != 1):
+            raise ValueError('PreparedLinear needs x [M, K] with unit column stride')
+        if out.shape != (x.shape[0], N) or (N > 1 and out.stride(1) != 1):
+            raise ValueError('PreparedLinear needs out [M, N] with unit column stride')
+        self._keep = [x, codes, scales, out, bias, down, up]
+        self.args = make_args(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out,
+                              bias=bias, down=down, up=up, rank=rank, flags=flags)
+        need = workspace_bytes(self.args)
+        if need:
+            if workspace is None or workspace.numel() < need:
+                workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+            self.args.workspace, self.args.workspace_bytes = _ptr(workspace), workspace.numel()
+            self._keep.append(workspace)
+        self.workspace_bytes = need
+        self.out = out
+        self._ref = ctypes.byref(self.args)
+        self._fn = library().lb_linear
+        self._device = x.device
+
+    def run(self, stream=None):
+        handle = torch.cuda.current_stream(self._device).cuda_stream if stream is None else stream
+        status = self._fn(self._ref, ctypes.c_void_p(handle))
+        if status != OK:
+            _check(status, 'lb_linear')
+        return self.out

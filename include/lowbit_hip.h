@@ -15,7 +15,8 @@
  *   - Outputs may not alias inputs (reference: backend.cpp:265-272).
  *   - Calls are asynchronous and ordered on `stream` (a hipStream_t; NULL is
  *     the default stream).  No entry point allocates device memory; scratch
- *     comes from a caller workspace sized by lb_workspace_bytes().
+ *     comes from a caller workspace sized by lb_workspace_bytes().  Calls that
+ *     share one workspace must be ordered (same stream); concurrent calls race.
  *   - On any status other than LB_OK, lb_last_error() returns a thread-local
  *     message describing the failure, valid until the next call on the same
  *     thread.  Argument errors are detected before anything is launched.

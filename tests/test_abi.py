@@ -83,9 +83,9 @@ def test_workspace_sizes():
     status, size, _ = workspace(args(rank=32, down=0x50000, up=0x60000, up_ld=32))
     assert status == 0 and size == 256
     # split-K decode of a tall K needs fp32 partials
-    status, size, _ = workspace(args(N=4096, K=4096, ldx=4096, ldy=4096, group_size=128,
+    status, size, _ = workspace(args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128,
                                      x=0x1000000, y=0x2000000, scales=0x3000000, codes=0x4000000))
-    assert status == 0 and size == 8 * 4096 * 4
+    assert status == 0 and size > 0 and size % (1024 * 4) == 0  # fp32 split-K partials [splits, M, N]
     # prefill with correction needs z and the fp16 delta
     status, size, _ = workspace(args(M=256, rank=32, down=0x5000000, up=0x6000000, up_ld=32,
                                      x=0x1000000, y=0x2000000))
@@ -93,7 +93,7 @@ def test_workspace_sizes():
 
 
 def test_missing_workspace_is_rejected_by_lb_linear():
-    a = args(N=4096, K=4096, ldx=4096, ldy=4096, group_size=128, x=0x1000000, y=0x2000000,
+    a = args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128, x=0x1000000, y=0x2000000,
              scales=0x3000000, codes=0x4000000)
     status = lowbit_hip.library().lb_linear(ctypes.byref(a), None)
     assert status == lowbit_hip.INVALID_ARGUMENT

@@ -241,3 +241,28 @@ def test_noncontiguous_and_strided_activations(device):
     for x in (view, transposed, misaligned):
         y = lowbit_hip.linear(x, codes, scales, format='int4', N=64, K=128, group_size=32)
         assert o.rel_l2(y.cpu().numpy(), want) <= REL_L2
+
+
+@pytest.mark.parametrize('spec', [('int4', 1, 1024, 14336, 128), ('int8', 8, 256, 4096, 4096),
+                                  ('nf4', 32, 520, 8192, 64)], ids=lambda s: '-'.join(map(str, s)))
+def test_split_k_repeated_calls_reuse_workspace(device, spec):
+    """Split-K partials: repeated calls on one workspace agree bit-for-bit."""
+    fmt, m, n, k, group = spec
+    announce('split-k repeat', spec)
+    rng = np.random.default_rng(5 + n)
+    p = problem(rng, fmt, m, n, k, group)
+    codes = to_dev(np.frombuffer(p['data'], np.uint8), device)
+    scales = to_dev(np.frombuffer(p['scales'], np.float16), device)
+    x = to_dev(p['x'], device)
+    out = torch.empty(m, n, dtype=torch.float16, device=device)
+    call = lowbit_hip.PreparedLinear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, out=out)
+    assert call.workspace_bytes > 0  # this shape is split along K
+    want = expected(p)
+    first = None
+    for _ in range(3):
+        got = call.run().cpu().numpy()
+        torch.cuda.synchronize()
+        assert o.rel_l2(got, want) <= REL_L2
+        if first is None:
+            first = got.copy()
+        np.testing.assert_array_equal(got.view(np.uint16), first.view(np.uint16))  # deterministic

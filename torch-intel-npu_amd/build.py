@@ -24,17 +24,20 @@ def hipcc():
     raise RuntimeError('hipcc not found; the low-bit HIP library cannot be built')
 
 
-def command(output=LIBRARY):
+def command(output=LIBRARY, defines=()):
     return [hipcc(), f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-shared',
+            *(f'-D{d}' for d in defines),
             # Packed fp32 VALU forms are kept out of the generated code on purpose.
             '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
             '-Wall', '-Wno-unused-function', '-Wno-unused-variable',
             '-o', str(output), *map(str, SOURCES)]
 
 
-def build(verbose=False):
-    tmp = LIBRARY.with_suffix('.so.tmp')
-    cmd = command(tmp)
+def build(verbose=False, output=LIBRARY, defines=()):
+    """Compile to `output` (default: the in-tree library); `defines` are extra -D macros."""
+    output = Path(output)
+    tmp = output.with_name(output.name + '.tmp')
+    cmd = command(tmp, defines)
     if verbose:
         print(' '.join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,8 +48,8 @@ def build(verbose=False):
         raise RuntimeError('hipcc failed:\n' + '\n'.join(messages))
     if verbose and messages:
         print('\n'.join(messages), flush=True)
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, output)
+    return output
 
 
 if __name__ == '__main__':

@@ -47,18 +47,21 @@ template <> struct FormatTraits<FMT_INT8> { static constexpr int CPL = 16, BITS 
 template <> struct FormatTraits<FMT_FP16> { static constexpr int CPL = 8,  BITS = 16; };
 
 // INT4: one dword (8 nibbles c0..c7, c_i at bits 4i) -> four fp16 pairs holding
-// q = (c^8)-8 exactly, in slot order (c0,c4),(c1,c5),(c2,c6),(c3,c7).
-// (c^8) | 0x6400 is the fp16 value 1024 + (c^8); subtracting 1032 is exact.
+// q = (c^8)-8 exactly, in slot order (c0,c2),(c4,c6),(c1,c3),(c5,c7).
+// Even / odd nibbles are split into bytes (xor 8 folded in), then v_perm_b32 places each
+// byte under the magic 0x64: 0x64bb is the fp16 value 1024 + b, and subtracting 1032 is exact.
 __device__ __forceinline__ void int4_pairs(uint32_t w, h2 out[4]) {
-  const uint32_t t = w ^ 0x88888888u;
+  const uint32_t lo = (w & 0x0F0F0F0Fu) ^ 0x08080808u;         // c0 c2 c4 c6
+  const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // c1 c3 c5 c7
   const h2 bias = {(f16)-1032.0f, (f16)-1032.0f};
-  out[0] = as_h2((t & 0x000F000Fu) | 0x64006400u) + bias;
-  out[1] = as_h2(((t >> 4) & 0x000F000Fu) | 0x64006400u) + bias;
-  out[2] = as_h2(((t >> 8) & 0x000F000Fu) | 0x64006400u) + bias;
-  out[3] = as_h2(((t >> 12) & 0x000F000Fu) | 0x64006400u) + bias;
+  // v_perm_b32: selector bytes 0-3 pick from the second operand, 4-7 from the first.
+  out[0] = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + bias;
+  out[1] = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + bias;
+  out[2] = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + bias;
+  out[3] = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + bias;
 }
 // Slot e of an INT4 8-group holds code kPermInt4[e].
-__device__ constexpr int kPermInt4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+__device__ constexpr int kPermInt4[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 
 // INT8: one dword (4 signed bytes b0..b3) -> two fp16 pairs (b0,b2),(b1,b3), exact.
 // (b ^ 0x80) in the low mantissa byte of 0x64xx is 1024 + b + 128; subtract 1152.
@@ -76,7 +79,7 @@ __device__ constexpr int kPermInt8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 template <int FMT>
 __device__ __forceinline__ h8 permute_block(h8 v) {
   if constexpr (FMT == FMT_INT4) {
-    return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
+    return __builtin_shufflevector(v, v, 0, 2, 4, 6, 1, 3, 5, 7);
   } else if constexpr (FMT == FMT_INT8) {
     return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
   } else {
@@ -149,6 +152,8 @@ struct LinearParams {
   int rank, up_ld;
   int kslice, splits;
   int per_row;            // int8 with one scale per row: scale applied to the fp32 sum
+  int group_shift;        // scale index = k >> group_shift (31 when group == K)
+  int scales_aligned;     // scales pointer is 16-byte aligned
 };
 
 // Epilogue with the reference's staging (torch_npu_lowbit.py:262-266,

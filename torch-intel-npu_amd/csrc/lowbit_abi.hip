@@ -61,35 +61,72 @@ int codes_per_load(int fmt) { return fmt == FMT_FP16 ? 8 : fmt == FMT_INT8 ? 16 
 
 struct Plan {
   int path = PATH_GENERIC;
-  int splits = 1, kslice = 0, kc = 0;
+  int kg = 1, splits = 1, kslice = 0, kc = 0;
   size_t z_off = 0, z_bytes = 0;
   size_t d_off = 0, d_bytes = 0;
   size_t part_off = 0, part_bytes = 0;
   size_t total = 0;
 };
 
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int group_shift(int64_t group, int64_t K) {
+  if (group == K) return 31;  // one scale per row: index k >> 31 == 0
+  int sh = 0;
+  while ((int64_t)1 << sh < group) ++sh;
+  return sh;
+}
+
 // Whether the MFMA fast paths can run these arguments.
 bool fast_eligible(int fmt, int64_t K, int64_t group, const void *codes, const void *x, int64_t ldx, int64_t ldw) {
   if (K % 32 != 0) return false;
-  if (fmt != FMT_FP16 && !(group == K || group % 32 == 0)) return false;
+  if (fmt != FMT_FP16 && !(group == K || (group % 32 == 0 && is_pow2(group)))) return false;
   if (!aligned(codes, 16) || !aligned(x, 16) || ldx % 8 != 0) return false;
   if (fmt == FMT_FP16 && ldw % 8 != 0) return false;
   return true;
 }
 
-void gemv_split(int fmt, int64_t M, int64_t N, int64_t K, int *splits, int *kslice, int *kc) {
+#ifndef LB_GEMV_TARGET_WAVES
+#define LB_GEMV_TARGET_WAVES 4096
+#endif
+#ifndef LB_GEMV_SPLIT_BELOW
+#define LB_GEMV_SPLIT_BELOW 1024  // split K across workgroups only when fewer waves than this
+#endif
+#ifndef LB_GEMV_MAX_KG
+#define LB_GEMV_MAX_KG 4
+#endif
+#ifndef LB_GEMV_SPLIT
+#define LB_GEMV_SPLIT 1
+#endif
+constexpr int64_t kGemvTargetWaves = LB_GEMV_TARGET_WAVES;
+
+struct GemvShape {
+  int kg = 1, splits = 1, kslice = 0, kc = 0;
+};
+
+// In-workgroup K groups (KG) and cross-workgroup splits so the grid holds ~kGemvTargetWaves
+// waves while each wave keeps at least one full batch of loads per split.
+GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split) {
+  GemvShape gs;
   const int kstep = 4 * codes_per_load(fmt);
-  const int64_t wgs = (N + 63) / 64;
+  const int64_t tiles = (N + 15) / 16;
+  const int64_t ksteps = (K + kstep - 1) / kstep;
+  int kg = 1;
+  const int max_kg = std::min(LB_GEMV_MAX_KG, kGemvWaves);
+  while (kg < max_kg && tiles * kg * 2 <= kGemvTargetWaves && ksteps >= 4 * kg) kg *= 2;
   int64_t s = 1;
-  if (wgs < 512) s = std::min<int64_t>((512 + wgs - 1) / wgs, K / (4 * kstep));
-  s = std::max<int64_t>(s, 1);
-  int64_t ks = round_up((K + s - 1) / s, kstep);
+  if (LB_GEMV_SPLIT && allow_split && tiles * kg < LB_GEMV_SPLIT_BELOW)
+    s = std::max<int64_t>(1, std::min<int64_t>((kGemvTargetWaves + tiles * kg - 1) / (tiles * kg),
+                                               ksteps / ((int64_t)kg * kGemvBatch)));
+  const int64_t ks = round_up((K + s - 1) / s, kstep);
   s = (K + ks - 1) / ks;
-  *splits = (int)s;
-  *kslice = (int)ks;
-  const int64_t budget = (int64_t)(kGemvLdsBudget / 2 / std::max<int64_t>(M, 1)) - 8;
-  int64_t c = std::max<int64_t>(kstep, budget / kstep * kstep);
-  *kc = (int)std::min<int64_t>(c, ks);
+  gs.kg = kg;
+  gs.splits = (int)s;
+  gs.kslice = (int)ks;
+  const int64_t budget = (int64_t)(kGemvLdsBudget / 2 / (M + 1)) - 4 * codes_per_load(fmt) - 8;
+  const int64_t c = std::max<int64_t>(kstep, budget / kstep * kstep);
+  gs.kc = (int)std::min<int64_t>(c, ks);
+  return gs;
 }
 
 Plan make_plan(const lb_linear_args *a, bool eligible) {
@@ -116,7 +153,11 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     }
   }
   if (pl.path == PATH_GEMV) {
-    gemv_split(fmt, a->M, a->N, a->K, &pl.splits, &pl.kslice, &pl.kc);
+    const GemvShape gs = gemv_shape(fmt, a->M, a->N, a->K, true);
+    pl.kg = gs.kg;
+    pl.splits = gs.splits;
+    pl.kslice = gs.kslice;
+    pl.kc = gs.kc;
     if (pl.splits > 1) {
       pl.part_off = off;
       pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
@@ -194,27 +235,47 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
   return ok();
 }
 
-template <int FMT, int MT, bool SCALED>
+template <int FMT, int MT, int KG, bool SCALED>
 void launch_gemv_t(const LinearParams &p, int kc, hipStream_t s) {
-  const dim3 grid((p.N + 63) / 64, p.splits);
-  const size_t lds = (FMT == FMT_NF4 ? 1024 : 0) + (size_t)p.M * (kc + 8) * 2;
-  hipLaunchKernelGGL((gemv_kernel<FMT, MT, 2, SCALED>), grid, dim3(kGemvThreads), lds, s, p, kc);
+  constexpr int rows = 16 * (kGemvWaves / KG);
+  const dim3 grid((p.N + rows - 1) / rows, p.splits);
+  // Staged scales per row: the chunk's groups plus 4 zero entries for tail lanes.
+  const int sc_ld = SCALED ? (p.group_shift >= 31 ? 1 : (kc >> p.group_shift) + 2) + 4 : 0;
+  const size_t stage = (size_t)(p.M + 1) * (kc + 4 * codes_per_load(FMT) + 8) * 2 + (size_t)rows * sc_ld * 2;
+  const size_t reduce = (size_t)(KG - 1) * (kGemvWaves / KG) * MT * 64 * 4 * sizeof(float);
+  const size_t lds = (FMT == FMT_NF4 ? 1024 : 0) + std::max(stage, reduce);
+  hipLaunchKernelGGL((gemv_kernel<FMT, MT, KG, SCALED>), grid, dim3(kGemvThreads), lds, s, p, kc, sc_ld);
+}
+
+template <int FMT, int MT, bool SCALED>
+void launch_gemv_kg(const LinearParams &p, int kg, int kc, hipStream_t s) {
+  if constexpr (kGemvWaves >= 8) {
+    if (kg == 8) return launch_gemv_t<FMT, MT, 8, SCALED>(p, kc, s);
+  }
+  if (kg == 4)
+    launch_gemv_t<FMT, MT, 4, SCALED>(p, kc, s);
+  else if (kg == 2)
+    launch_gemv_t<FMT, MT, 2, SCALED>(p, kc, s);
+  else
+    launch_gemv_t<FMT, MT, 1, SCALED>(p, kc, s);
 }
 
 template <int FMT, bool SCALED>
-void launch_gemv_m(const LinearParams &p, int kc, hipStream_t s) {
+void launch_gemv_m(const LinearParams &p, int kg, int kc, hipStream_t s) {
   if (p.M <= 16)
-    launch_gemv_t<FMT, 1, SCALED>(p, kc, s);
+    launch_gemv_kg<FMT, 1, SCALED>(p, kg, kc, s);
   else
-    launch_gemv_t<FMT, 2, SCALED>(p, kc, s);
+    launch_gemv_kg<FMT, 2, SCALED>(p, kg, kc, s);
 }
 
-void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kc, hipStream_t s) {
+void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kg, int kc, hipStream_t s) {
   switch (fmt) {
-    case FMT_INT8: scaled ? launch_gemv_m<FMT_INT8, true>(p, kc, s) : launch_gemv_m<FMT_INT8, false>(p, kc, s); break;
-    case FMT_INT4: launch_gemv_m<FMT_INT4, true>(p, kc, s); break;
-    case FMT_NF4: launch_gemv_m<FMT_NF4, true>(p, kc, s); break;
-    default: launch_gemv_m<FMT_FP16, false>(p, kc, s); break;
+    case FMT_INT8:
+      scaled ? launch_gemv_m<FMT_INT8, true>(p, kg, kc, s) : launch_gemv_m<FMT_INT8, false>(p, kg, kc, s);
+      break;
+    case FMT_INT4: launch_gemv_m<FMT_INT4, true>(p, kg, kc, s); break;
+    case FMT_NF4: launch_gemv_m<FMT_NF4, true>(p, kg, kc, s); break;
+    default: launch_gemv_m<FMT_FP16, false>(p, kg, kc, s); break;
   }
   if (p.splits > 1) {
     const size_t count = (size_t)p.M * p.N;
@@ -257,6 +318,8 @@ LinearParams base_params(int fmt, int64_t M, int64_t N, int64_t K, int64_t group
   p.ldy = (int)ldy;
   p.ldw = (int)ldw;
   p.per_row = fmt == FMT_INT8 && group == K;
+  p.group_shift = group_shift(group, K);
+  p.scales_aligned = aligned(scales, 16);
   p.splits = 1;
   p.kslice = (int)K;
   return p;
@@ -270,12 +333,8 @@ void dense_fp16(int64_t M, int64_t N, int64_t K, const void *w, int64_t ldw, con
   if (!eligible) {
     launch_generic(FMT_FP16, p, s);
   } else if (M <= kGemvMaxM) {
-    int splits, kslice, kc;
-    gemv_split(FMT_FP16, M, N, K, &splits, &kslice, &kc);
-    p.splits = 1;
-    p.kslice = (int)K;
-    kc = std::min<int>(kc, (int)K);
-    launch_gemv(FMT_FP16, false, p, kc, s);
+    const GemvShape gs = gemv_shape(FMT_FP16, M, N, K, false);
+    launch_gemv(FMT_FP16, false, p, gs.kg, gs.kc, s);
   } else {
     launch_gemm(FMT_FP16, false, p, s);
   }
@@ -349,7 +408,7 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     p.splits = plan.splits;
     p.kslice = plan.kslice;
     p.partial = reinterpret_cast<float *>(ws + plan.part_off);
-    launch_gemv(fmt, scaled, p, plan.kc, s);
+    launch_gemv(fmt, scaled, p, plan.kg, plan.kc, s);
   } else if (plan.path == PATH_GEMM) {
     launch_gemm(fmt, scaled, p, s);
   } else {

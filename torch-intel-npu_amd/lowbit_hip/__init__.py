@@ -147,7 +147,7 @@ def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, 
     need = workspace_bytes(args)
     if need:
         if workspace is None or workspace.numel() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+            workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
         args.workspace, args.workspace_bytes = _ptr(workspace), workspace.numel()
     _check(library().lb_linear(ctypes.byref(args), _stream(x.device)), 'lb_linear')
     return y
@@ -194,7 +194,7 @@ class PreparedLinear:
         need = workspace_bytes(self.args)
         if need:
             if workspace is None or workspace.numel() < need:
-                workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+                workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
             self.args.workspace, self.args.workspace_bytes = _ptr(workspace), workspace.numel()
             self._keep.append(workspace)
         self.workspace_bytes = need

@@ -1,0 +1,123 @@
+"""GPU parity of the SmolLM decoder path against the CPU oracle.
+
+Bars: decoder logits rel-L2 <= 1e-2 and greedy tokens identical for
+the first 32 steps (config 4: random-init SmolLM-135M, W8 per-row + rank-32 corrections,
+theta 1e4, 256-token prompt).  Layer outputs are compared at the same bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+import smollm_random
+from conftest import announce
+from oracle import smollm_oracle as so
+from torch_npu_lowbit import quantize_weight
+from torch_npu_lowbit_correction import LowRankCorrection
+from torch_npu_smollm import FrozenSmolLayer, FrozenSmolStack, generate_greedy, _SHAPES
+
+pytestmark = pytest.mark.gpu
+CONFIG = smollm_random.config(theta=100000.0, layers=1)
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def packed_of(layer):
+    return {n: (q.format, q.shape, q.group_size, q.data, q.scales) for n, q in layer._packed.items()}
+
+
+def corr_of(layer):
+    return {n: c.tensors() for n, c in layer._corrections.items()}
+
+
+@pytest.fixture(scope='module')
+def weights():
+    g = torch.Generator().manual_seed(414)
+    w = {n: (torch.randn(s, generator=g) * .015).half() if len(s) == 2 else (1 + torch.randn(s, generator=g) * .1).half()
+         for n, s in _SHAPES.items()}
+    x = (torch.randn(2, 7, 576, generator=g) * .1).half()
+    return w, x
+
+
+@pytest.mark.parametrize('mode', ['w8a16', 'w4a16', 'nf4a16', 'fp16'])
+def test_layer_forward_matches_oracle(device, weights, mode):
+    announce('smollm layer', mode)
+    w, x = weights
+    layer = FrozenSmolLayer(CONFIG, w, mode=mode)
+    oracle = so.OracleLayer(w, packed_of(layer) if mode != 'fp16' else None)
+    want = oracle.forward(x)[0]
+    got = layer(x.to(device)).cpu()
+    assert rel_l2(got, want) <= 1e-2
+    assert rel_l2(got, layer.reference_cpu(x)[0]) <= 1e-2
+
+
+def test_prefill_decode_with_corrections(device, weights):
+    announce('smollm prefill/decode')
+    w, x = weights
+    g = torch.Generator().manual_seed(7)
+    packed = {n: quantize_weight(t, format='int8') for n, t in w.items() if t.ndim == 2}
+    corr = {n: LowRankCorrection(_SHAPES[n], 16, (torch.randn(16, _SHAPES[n][1], generator=g) * .01).half().numpy().tobytes(),
+                                 (torch.randn(_SHAPES[n][0], 16, generator=g) * .01).half().numpy().tobytes())
+            for n in packed}
+    layers = [FrozenSmolLayer(CONFIG, w, packed_weights=packed, corrections=corr, capacity=16) for _ in range(2)]
+    stack = FrozenSmolStack.from_layers(layers)
+    oracles = [so.OracleLayer(w, packed_of(layer), corr_of(layer), capacity=16) for layer in layers]
+    h, caches = stack.prefill(x[:, :4].to(device))
+    ref, kv = x[:, :4], []
+    for o in oracles:
+        ref, _, k, v = o.forward(ref)
+        kv.append((k, v))
+    assert rel_l2(h.cpu(), ref) <= 1e-2
+    for pos in range(4, 7):
+        h, caches = stack.decode(x[:, pos:pos + 1].to(device), caches)
+        ref, new = x[:, pos:pos + 1], []
+        for o, (k, v) in zip(oracles, kv):
+            ref, k, v = o.decode(ref, k, v, pos)
+            new.append((k, v))
+        kv = new
+        assert rel_l2(h.cpu(), ref) <= 1e-2, pos
+        assert caches[0].length == pos + 1
+    keys = caches[0].keys[:, :, :7].cpu()
+    assert rel_l2(keys, kv[0][0]) <= 1e-2
+
+
+def test_snapshots_are_not_mutated(device, weights):
+    announce('smollm snapshots')
+    w, x = weights
+    layer = FrozenSmolLayer(CONFIG, w, capacity=8)
+    xd = x[:1].to(device)
+    _, c3 = layer.prefill(xd[:, :3])
+    y1, c4 = layer.decode(xd[:, 3:4], c3)
+    k4 = c4.keys[:, :, :4].clone()
+    y2, c4b = layer.decode(xd[:, 4:5], c3)       # branch from the older snapshot: copy on write
+    assert torch.equal(c4.keys[:, :, :4], k4)   # the first branch is untouched
+    y3, _ = layer.decode(xd[:, 3:4], c3)
+    assert torch.equal(y1, y3)
+    with pytest.raises(ValueError):
+        layer.decode(xd[:, :2], c3)
+    other = FrozenSmolLayer(CONFIG, w, capacity=8)
+    with pytest.raises(ValueError):
+        other.decode(xd[:, 3:4], c3)
+
+
+def test_config4_greedy_tokens_and_logits(device):
+    """Config 4: 30 layers, W8 + rank-32, theta 1e4, 256-token prompt; 32 greedy steps."""
+    announce('config4 decoder parity')
+    steps = 32
+    stack, io, packed, corr = smollm_random.build(seed=0, layers=30, rank=32, theta=10000.0, capacity=384)
+    ids = smollm_random.prompt(seed=0, length=256)
+    io = io.to(device)
+    tokens, logits = generate_greedy(stack, io, ids, steps)
+    layers = []
+    for layer in stack.layers:
+        layers.append(so.OracleLayer(layer._weights, packed_of(layer), corr_of(layer), theta=10000.0, capacity=384))
+    oracle = so.OracleModel(layers, io.embedding.cpu(), io.norm.cpu())
+    ref_tokens, ref_logits = oracle.generate(ids, steps)
+    errs = [rel_l2(logits[i], ref_logits[i]) for i in range(steps)]
+    top2 = torch.topk(ref_logits.float(), 2, dim=-1).values
+    margin = float((top2[:, 0] - top2[:, 1]).min())
+    print(f'[config4] max logits rel-L2 {max(errs):.3e}, min top-2 margin {margin:.4f}', flush=True)
+    assert max(errs) <= 1e-2
+    assert tokens == ref_tokens

@@ -183,6 +183,75 @@ def cpu_leg(budget_s):
                 dequant_inclusive_gbs=round(total / deq / 1e9, 3))
 
 
+def decode_leg(device, steps, cpu_steps):
+    """Config 4: 30-layer random-init SmolLM-135M, W8 per-row + rank-32 corrections, theta 1e4,
+    256-token prompt, then greedy decode with the fp16 KV cache (GraphDecoder replays)."""
+    import smollm_random
+    from torch_npu_smollm import GraphDecoder
+    stack, io, _, _ = smollm_random.build(seed=0, layers=30, rank=32, theta=10000.0, capacity=384)
+    io = io.to(device)
+    ids = smollm_random.prompt(seed=0, length=256).to(device)
+    out = {}
+    with torch.no_grad():
+        for _ in range(2):  # warm (device copies of weights, allocator)
+            h, caches = stack.prefill(io.embed_tokens(ids))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        h, caches = stack.prefill(io.embed_tokens(ids))
+        first = int(io.logits(h[:, -1:])[0, 0].float().argmax())
+        out['prefill_ms'] = round((time.perf_counter() - t0) * 1e3, 3)
+        out['prefill_tokens_per_s'] = round(256 / (time.perf_counter() - t0), 1)
+        # eager decode (one Python-driven step per token)
+        x = io.embed_tokens(torch.tensor([[first]], device=device))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eager_caches = caches
+        for _ in range(8):
+            h2, eager_caches = stack.decode(x, eager_caches)
+            x = io.embed_tokens(io.logits(h2)[0, 0].float().argmax().view(1, 1))
+        torch.cuda.synchronize()
+        out['eager_decode_tokens_per_s'] = round(8 / (time.perf_counter() - t0), 1)
+        decoder = GraphDecoder(stack, io)
+        decoder.load(caches, first)
+        decoder.capture()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            decoder.graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop)
+        out.update(decode_steps=steps, decode_ms_per_token=round(ms / steps, 4),
+                   decode_tokens_per_s=round(steps * 1000.0 / ms, 1),
+                   first_tokens=decoder.tokens[256:256 + 8].tolist())
+    if cpu_steps:
+        from oracle import smollm_oracle as so
+        packed = lambda l: {n: (q.format, q.shape, q.group_size, q.data, q.scales) for n, q in l._packed.items()}
+        layers = [so.OracleLayer(l._weights, packed(l), {n: c.tensors() for n, c in l._corrections.items()},
+                                 theta=10000.0, capacity=384) for l in stack.layers]
+        model = so.OracleModel(layers, io.embedding.cpu(), io.norm.cpu())
+        t0 = time.perf_counter()
+        x, kv = model.prefill(ids.cpu())
+        prefill_s = time.perf_counter() - t0
+        h = model.embed(torch.tensor([[first]]))
+        t0 = time.perf_counter()
+        pos = 256
+        for _ in range(cpu_steps):
+            new = []
+            for layer, (k, v) in zip(model.layers, kv):
+                h, k, v = layer.decode(h, k, v, pos)
+                new.append((k, v))
+            kv, pos = new, pos + 1
+            h = model.embed(model.logits(h)[:, 0].float().argmax(-1).view(1, 1))
+        dt = time.perf_counter() - t0
+        out['cpu_baseline'] = dict(decode_tokens_per_s=round(cpu_steps / dt, 2), prefill_s=round(prefill_s, 2),
+                                   cores=torch.get_num_threads(), kind='port',
+                                   sample=f'oracle staged decoder on the host: 256-token prefill + {cpu_steps} greedy steps')
+    return out
+
+
 def profile_kernel(device, stream):
     """Dominant kernel (lm_head INT4 GEMV, M=1) over its replica pool, then a known-size copy."""
     name, n, k, g = SMOL_SHAPES[-1]
@@ -210,6 +279,8 @@ def main():
     ap.add_argument('--no-sweep', action='store_true')
     ap.add_argument('--cpu-seconds', type=float, default=15.0)
     ap.add_argument('--profile-kernel', action='store_true')
+    ap.add_argument('--no-decode', action='store_true')
+    ap.add_argument('--decode-steps', type=int, default=128)
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -245,6 +316,11 @@ def main():
         torch.cuda.empty_cache()
     rows = [] if args.no_sweep else sweep(device, stream, args.quick)
     cpu = None if args.no_cpu else cpu_leg(args.cpu_seconds)
+    decode = None
+    if not args.no_decode:
+        log('config-4 decode')
+        decode = decode_leg(device, args.decode_steps, 0 if args.no_cpu else 6)
+        log('decode', json.dumps(decode))
     achieved = lm.bytes / dominant['us'] / 1e3
     result = {
         'metric': METRIC,
@@ -275,6 +351,7 @@ def main():
         },
         'cpu_baseline': cpu,
         'per_kernel_M1': head['per_kernel'],
+        'decode_smollm135m_w8_rank32': decode,
         'passes': others,
         'sweep': rows,
         'wall_s': round(time.time() - t0, 1),

@@ -121,3 +121,20 @@ def test_config4_greedy_tokens_and_logits(device):
     print(f'[config4] max logits rel-L2 {max(errs):.3e}, min top-2 margin {margin:.4f}', flush=True)
     assert max(errs) <= 1e-2
     assert tokens == ref_tokens
+
+
+def test_graph_decoder_matches_eager_and_oracle(device):
+    """The captured decode step reproduces the eager decode tokens (small stack, 24 steps)."""
+    announce('graph decoder')
+    from torch_npu_smollm import GraphDecoder
+    stack, io, _, _ = smollm_random.build(seed=5, layers=4, rank=32, theta=10000.0, capacity=96)
+    io = io.to(device)
+    ids = smollm_random.prompt(seed=5, length=40)
+    tokens, _ = generate_greedy(stack, io, ids, 24)
+    x = io.embed_tokens(ids.to(device))
+    h, caches = stack.prefill(x)
+    first = int(io.logits(h[:, -1:])[0, 0].float().argmax())
+    decoder = GraphDecoder(stack, io)
+    decoder.load(caches, first)
+    rest = decoder.generate(23)
+    assert [first] + rest == tokens

@@ -538,3 +538,133 @@ def generate_greedy(stack, io, ids, steps):
         h, caches = stack.decode(io.embed_tokens(torch.tensor([[tok]], device=device)), caches)
         logits = io.logits(h)[0, 0]
     return tokens, torch.stack(history)
+
+
+class GraphDecoder:
+    """Greedy decode of one sequence (B=1) as a replayable HIP graph.
+
+    The per-token work of FrozenSmolStack.decode plus FrozenSmolIO.logits and the argmax is
+    captured once: activations live in static buffers, every projection is a
+    PreparedLinear bound to them, and the position is a device tensor (RoPE rows are
+    gathered by it, K/V rows are written at it, and attention runs over the whole capacity
+    with positions > p masked to -inf, which contributes exact zeros).  One replay embeds
+    the current token, runs every layer, writes the greedy next token and advances the
+    position, so generation needs no host synchronization.  Staging matches
+    FrozenSmolLayer.decode (reference torch_npu_smollm.py:142-193).
+    """
+
+    def __init__(self, stack, io):
+        import lowbit_hip as lb
+        self.device = io.embedding.device
+        if self.device.type != 'cuda':
+            raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
+        self.stack, self.io = stack, io
+        dev = self.device
+        cap = stack.layers[0].capacity
+        self.capacity = cap
+        z = lambda *shape, dtype=torch.float16: torch.zeros(shape, dtype=dtype, device=dev)
+        self.pos = z(1, dtype=torch.int64)
+        self.token = z(1, dtype=torch.int64)
+        self.tokens = z(cap + 1, dtype=torch.int64)
+        self.h = z(1, HIDDEN)
+        self.n1, self.att, self.o, self.n2, self.down = (z(1, HIDDEN) for _ in range(5))
+        self.q, self.k, self.v = z(1, 576), z(1, 192), z(1, 192)
+        self.gate, self.up, self.hidden = z(1, 1536), z(1, 1536), z(1, 1536)
+        self.normed = z(1, HIDDEN)
+        self.logits = z(1, io.vocab_size)
+        self.slots = torch.arange(cap, device=dev)
+        self.keys = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
+        self.values = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
+        self.states = [layer._dev(dev) for layer in stack.layers]
+        plan = (('self_attn.q_proj.weight', 'n1', 'q'), ('self_attn.k_proj.weight', 'n1', 'k'),
+                ('self_attn.v_proj.weight', 'n1', 'v'), ('self_attn.o_proj.weight', 'att', 'o'),
+                ('mlp.gate_proj.weight', 'n2', 'gate'), ('mlp.up_proj.weight', 'n2', 'up'),
+                ('mlp.down_proj.weight', 'hidden', 'down'))
+        self.calls = []
+        for state in self.states:
+            calls = {}
+            for name, src, dst in plan:
+                e = state['lin'][name]
+                calls[name] = lb.PreparedLinear(getattr(self, src), e['codes'], e['scales'], format=e['format'],
+                                                N=e['N'], K=e['K'], group_size=e['group'], out=getattr(self, dst),
+                                                down=e.get('down'), up=e.get('up'), rank=e.get('rank', 0))
+            self.calls.append(calls)
+        self.head = lb.PreparedLinear(self.normed, io.embedding, None, format='fp16', N=io.vocab_size, K=HIDDEN,
+                                      group_size=HIDDEN, out=self.logits)
+        self.graph = None
+
+    def load(self, caches, next_token):
+        """Start from a prefill snapshot: copy its K/V, set the position and the next input token."""
+        length = caches[0].length
+        for dst_k, dst_v, cache in zip(self.keys, self.values, caches):
+            dst_k[:, :, :length].copy_(cache.keys[:, :, :length])
+            dst_v[:, :, :length].copy_(cache.values[:, :, :length])
+        self.pos.fill_(length)
+        self.token.fill_(int(next_token))
+
+    @staticmethod
+    def _norm_into(out, x, gamma):
+        f = x.float()
+        torch.mul((f * torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)).half(), gamma, out=out)
+
+    def step(self):
+        """One greedy token (eager; this is what capture() records)."""
+        torch.index_select(self.io.embedding, 0, self.token, out=self.h)
+        mask = torch.where(self.slots > self.pos, float('-inf'), 0.0)
+        for layer_index, (state, calls) in enumerate(zip(self.states, self.calls)):
+            self._norm_into(self.n1, self.h, state['norm1'])
+            calls['self_attn.q_proj.weight'].run()
+            calls['self_attn.k_proj.weight'].run()
+            calls['self_attn.v_proj.weight'].run()
+            cos = state['cos'].index_select(0, self.pos)[None]
+            sin = state['sin'].index_select(0, self.pos)[None]
+            q = FrozenSmolLayer._rotate(self.q.view(1, HEADS, 1, HEAD_DIM), cos, sin)
+            k = FrozenSmolLayer._rotate(self.k.view(1, KV_HEADS, 1, HEAD_DIM), cos, sin)
+            keys, values = self.keys[layer_index], self.values[layer_index]
+            keys.index_copy_(2, self.pos, k)
+            values.index_copy_(2, self.pos, self.v.view(1, KV_HEADS, 1, HEAD_DIM))
+            att = FrozenSmolLayer._attend(q, keys, values, mask)
+            self.att.copy_(att.view(1, HIDDEN))
+            calls['self_attn.o_proj.weight'].run()
+            torch.add(self.h, self.o, out=self.h)
+            self._norm_into(self.n2, self.h, state['norm2'])
+            calls['mlp.gate_proj.weight'].run()
+            calls['mlp.up_proj.weight'].run()
+            torch.mul(F.silu(self.gate.float()).half(), self.up, out=self.hidden)
+            calls['mlp.down_proj.weight'].run()
+            torch.add(self.h, self.down, out=self.h)
+        f = self.h.float()
+        torch.mul((f * torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)).half(), self.io.norm, out=self.normed)
+        self.head.run()
+        nxt = self.logits.float().argmax(-1)
+        self.tokens.index_copy_(0, self.pos, nxt)
+        self.token.copy_(nxt)
+        self.pos.add_(1)
+
+    def capture(self):
+        """Record step() into a HIP graph (warm-up runs first on a side stream, as torch requires)."""
+        pos, token = self.pos.clone(), self.token.clone()
+        keys = [k.clone() for k in self.keys]
+        values = [v.clone() for v in self.values]
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+        self.pos.copy_(pos)  # the warm-up and capture advanced state; restore it
+        self.token.copy_(token)
+        for dst, src in zip(self.keys + self.values, keys + values):
+            dst.copy_(src)
+        return self.graph
+
+    def generate(self, steps):
+        """Replay `steps` tokens; returns the generated token ids (one host sync at the end)."""
+        if self.graph is None:
+            self.capture()
+        start = int(self.pos.item())
+        for _ in range(steps):
+            self.graph.replay()
+        return self.tokens[start:start + steps].tolist()

@@ -16,7 +16,7 @@ Every fp16 rounding point of the reference is kept:
   logits     fp16(fp32 RMS) * gamma, then F.linear with the tied fp16 embedding (io :57-61)
 
 The decode step is the KV-cached row of the same computation: at position p it reads
-keys/values 0..p and uses the RoPE row p.  Pinning: tests/test_smollm_oracle.py checks
+keys/values 0..p and uses the RoPE row p.  Pinning: tests/test_smollm_cpu.py checks
 the decode rows against the full-sequence forward, zero-factor corrections against no
 correction (bitwise), the correction delta at one projection, the 4-bit trace against
 F.linear(norm1, dequantize()), and the tied logits against F.rms_norm.

@@ -1,0 +1,116 @@
+/*
+ * lowbit_decode_hip.h -- C-ABI of the decode-step entry points of liblowbit_hip.so
+ * (MI355X, gfx950): one SmolLM-style decoder token for one sequence, built from a few
+ * fused launches instead of one launch per operator.
+ *
+ * The reference compiles each decoder layer into one NPU graph
+ * (torch_npu_smollm.py:195-340, FrozenSmolLayer.graph) and submits 30 of them per token in
+ * fenced chains (torch_npu_smollm.py:644-654, torch_intel_npu.py:560-570); its RMSNorm and
+ * KV-select steps ran as SHAVE kernels inside that graph
+ * (npunlock/tests/fixtures/npu4000/rmsnorm.c, kv_select.c).  These entry points are the
+ * pieces of such a layer on the GPU; a caller enqueues them on one stream (and may capture
+ * them into a HIP graph -- none of them calls hipMemsetAsync or allocates).
+ *
+ * Conventions are those of lowbit_hip.h: device pointers, caller-owned buffers,
+ * asynchronous stream-ordered calls, lb_status results with lb_last_error().
+ * Every activation here is one fp16 row (batch 1, one token).
+ */
+#ifndef LOWBIT_DECODE_HIP_H
+#define LOWBIT_DECODE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lowbit_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LB_FUSED_MAX_PROBLEMS 3
+#define LB_FUSED_MAX_RANK 32
+#define LB_FUSED_MAX_K 1536
+
+/* lb_fused_linear_args.prologue: what is applied to the activation row before the product */
+#define LB_PROLOGUE_NONE 0u     /* x as given */
+#define LB_PROLOGUE_RMSNORM 1u  /* fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) (torch_npu_smollm.py:166-168) */
+#define LB_PROLOGUE_SILU_MUL 2u /* fp16(fp16(silu(x)) * x2), x = gate row, x2 = up row (torch_npu_smollm.py:188-190) */
+
+typedef struct lb_fused_problem {
+  const void *codes;        /* PackedWeight.data bytes, or fp16 [N,K] for LB_FORMAT_FP16; 16-byte aligned */
+  const void *scales;       /* fp16 [N, K/group_size] */
+  int64_t N;
+  void *y;                  /* fp16 [N] */
+  const void *bias;         /* fp16 [N] or NULL */
+  const void *residual;     /* fp16 [N] or NULL; y = fp16(residual + y) last. May be y itself. */
+  int64_t rank;             /* 0..32; 0: no correction */
+  const void *down;         /* V fp16 [rank, K], 16-byte aligned */
+  const void *up;           /* U fp16 [N, up_ld], 16-byte aligned, up_ld % 8 == 0, up_ld >= rank */
+  int64_t up_ld;
+} lb_fused_problem;
+
+typedef struct lb_fused_linear_args {
+  uint32_t struct_size;     /* sizeof(lb_fused_linear_args) */
+  uint32_t format;          /* lb_format, shared by every problem */
+  int64_t K;                /* K % 32 == 0, K <= LB_FUSED_MAX_K */
+  int64_t group_size;       /* int8: K (per row) or a power of two >= 32; int4/nf4: power of two >= 32 */
+  uint32_t prologue;        /* LB_PROLOGUE_* */
+  uint32_t count;           /* problems, 1..LB_FUSED_MAX_PROBLEMS */
+  const void *x;            /* fp16 [K], 16-byte aligned (SILU_MUL: the gate row) */
+  const void *x2;           /* SILU_MUL: the up row fp16 [K] */
+  const void *gamma;        /* RMSNORM: fp16 [K] */
+  float eps;                /* RMSNORM epsilon */
+  uint32_t reserved;
+  lb_fused_problem problems[LB_FUSED_MAX_PROBLEMS];
+} lb_fused_linear_args;
+
+/*
+ * For each problem i: y_i = epilogue(x' . dequant(W_i)^T), x' = prologue(x), one launch for
+ * all problems.  The epilogue is lb_linear's (scale, fp16, + bias, + fp16(fp16(x'.V^T).U^T))
+ * followed by the residual add.  Replaces the per-projection linear() of
+ * FrozenSmolLayer.graph with its neighbouring RMSNorm / SiLU-multiply / residual Add
+ * (torch_npu_smollm.py:237-259, with the fused RMSNorm of :195-340), for one token.
+ * Outputs may not overlap any input except a problem's own residual (same pointer).
+ */
+lb_status lb_fused_linear(const lb_fused_linear_args *args, void *stream);
+
+typedef struct lb_decode_attention_args {
+  uint32_t struct_size;     /* sizeof(lb_decode_attention_args) */
+  uint32_t reserved;
+  int64_t heads, kv_heads;  /* heads % kv_heads == 0; query head h uses KV head h / (heads / kv_heads) */
+  int64_t head_dim;         /* 64 */
+  int64_t capacity;         /* KV slots, 1..4096 */
+  const void *q;            /* fp16 [heads, 64] new query row (before RoPE) */
+  const void *k;            /* fp16 [kv_heads, 64] new key row (before RoPE) */
+  const void *v;            /* fp16 [kv_heads, 64] new value row */
+  const void *cos, *sin;    /* fp16 [capacity, 64] RoPE tables */
+  const int64_t *position;  /* device scalar p: the slot of the new token; the call is a no-op unless 0 <= p < capacity */
+  void *keys, *values;      /* fp16 [kv_heads, capacity, 64]; slot p is written */
+  void *out;                /* fp16 [heads, 64] */
+  float scale;              /* score scale, applied after the fp16 rounding of q.k (0.125 for head_dim 64) */
+  uint32_t reserved2;
+} lb_decode_attention_args;
+
+/*
+ * RoPE of q and k at row p, append (k, v) at slot p, causal GQA attention over slots 0..p with
+ * the reference staging: scores fp16(q.k) -> fp16(* scale), softmax fp32 -> fp16,
+ * out = fp16(P.V) (CPU staging torch_npu_smollm.py:174-182; the device graph's RoPE gather,
+ * GQA attention and KV Select, :262-303, :325-329).
+ */
+lb_status lb_decode_attention(const lb_decode_attention_args *args, void *stream);
+
+/*
+ * Greedy step: t = first index of the largest logit (NaN logits are never chosen);
+ * token[0] = t; if 0 <= position[0] < limit: tokens[position[0]] = t and position[0] += 1;
+ * h_next = embedding[t] (fp16 [hidden]).  Replaces the host argmax and the next step's embedding
+ * lookup of the reference generation loop (torch_npu_smollm_kv_demo.py:229-245,
+ * torch_npu_smollm_io.py:45-50).
+ */
+lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embedding, int64_t hidden, void *h_next,
+                         int64_t *tokens, int64_t *token, int64_t *position, int64_t limit, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOWBIT_DECODE_HIP_H */

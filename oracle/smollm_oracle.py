@@ -80,11 +80,13 @@ class OracleLayer:
         n = (f * torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)).half()
         return (n * self.w[name]).half()
 
-    def _rotate(self, v, cos, sin):
+    @staticmethod
+    def _rotate(v, cos, sin):
         rot = torch.cat((-v[..., 32:], v[..., :32]), -1)
         return (v * cos + rot * sin).half()
 
-    def _attend(self, q, k, v, mask):
+    @staticmethod
+    def _attend(q, k, v, mask):
         k = k.repeat_interleave(3, dim=1)
         v = v.repeat_interleave(3, dim=1)
         scores = (q.float() @ k.float().transpose(-1, -2)).half()

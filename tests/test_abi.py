@@ -8,18 +8,22 @@ import pytest
 
 import lowbit_hip
 
-HEADER = Path(__file__).resolve().parents[1] / 'include' / 'lowbit_hip.h'
+HEADERS = sorted((Path(__file__).resolve().parents[1] / 'include').glob('*.h'))
 
 
 def declared_functions():
-    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r'\b(lb_[a-z_]+)\s*\(', text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r'/\*.*?\*/', '', header.read_text(), flags=re.S)
+        names |= set(re.findall(r'\b(lb_[a-z_]+)\s*\(', text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     lib = lowbit_hip.library()
     names = declared_functions()
-    assert set(names) == set(lowbit_hip.EXPORTS), names
+    assert len(HEADERS) == 2
+    assert set(names) == set(lowbit_hip.EXPORTS) | set(lowbit_hip.DECODE_EXPORTS), names
     for name in names:
         assert hasattr(lib, name), name
     assert lib.lb_abi_version() == lowbit_hip.ABI_VERSION
@@ -30,6 +34,9 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_matches_header():
     # struct_size is checked by the library: a wrong Python mirror is rejected as too small.
     assert ctypes.sizeof(lowbit_hip.LinearArgs) == 8 + 8 * 4 + 8 * 2 + 8 * 2 + 8 * 2 + 8 + 8 * 3 + 8 + 8 + 8 + 8
+    assert ctypes.sizeof(lowbit_hip.FusedProblem) == 10 * 8
+    assert ctypes.sizeof(lowbit_hip.FusedLinearArgs) == 8 + 8 + 8 + 8 + 3 * 8 + 8 + 3 * 80
+    assert ctypes.sizeof(lowbit_hip.DecodeAttentionArgs) == 8 + 4 * 8 + 9 * 8 + 8
 
 
 def args(**over):
@@ -107,3 +114,89 @@ def test_unpack_and_dequantize_argument_errors():
     assert lib.lb_unpack_codes(1, 4, 4, 0x1000, 0x1004, None) == lowbit_hip.INVALID_ARGUMENT  # overlap
     assert lib.lb_dequantize(1, 4, 6, 4, 0x1000, 0x2000, 0x3000, None) == lowbit_hip.INVALID_ARGUMENT
     assert lib.lb_dequantize(3, 4, 8, 4, 0x1000, 0x2000, 0x3000, None) == lowbit_hip.INVALID_ARGUMENT
+
+
+def fused(**over):
+    a = lowbit_hip.FusedLinearArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.format, a.K, a.group_size, a.prologue, a.count = 0, 576, 576, 1, 1
+    a.x, a.gamma, a.eps = 0x10000, 0x20000, 1e-5
+    p = a.problems[0]
+    p.codes, p.scales, p.N, p.y = 0x100000, 0x30000, 64, 0x40000
+    for key, value in over.items():
+        target = p if key.startswith('p_') else a
+        setattr(target, key[2:] if key.startswith('p_') else key, value)
+    return a
+
+
+@pytest.mark.parametrize('over,needle', [
+    (dict(struct_size=16), 'struct_size'),
+    (dict(format=7), 'format'),
+    (dict(K=600), 'multiple of 32'),
+    (dict(K=2048), 'multiple of 32'),
+    (dict(format=1, group_size=48), 'group_size'),
+    (dict(prologue=5), 'prologue'),
+    (dict(count=0), 'count'),
+    (dict(count=4), 'count'),
+    (dict(x=0x10008), 'x must be'),
+    (dict(gamma=0), 'gamma'),
+    (dict(prologue=2), 'x2'),
+    (dict(p_N=0), 'N='),
+    (dict(p_codes=0x100008), 'codes'),
+    (dict(p_rank=33), 'rank'),
+    (dict(p_rank=8, p_down=0x50000, p_up=0x60000, p_up_ld=12), 'up_ld'),
+    (dict(p_y=0x10010), 'overlaps x'),
+    (dict(p_y=0x100010), 'overlaps codes'),
+    (dict(p_residual=0x40002), 'overlaps residual'),
+])
+def test_fused_linear_argument_errors(over, needle):
+    lib = lowbit_hip.library()
+    status = lib.lb_fused_linear(ctypes.byref(fused(**over)), None)
+    message = lib.lb_last_error().decode()
+    assert status == lowbit_hip.INVALID_ARGUMENT, message
+    assert needle in message
+
+
+def test_fused_linear_outputs_may_not_overlap_each_other():
+    a = fused(count=2)
+    p = a.problems[1]
+    p.codes, p.scales, p.N, p.y = 0x200000, 0x70000, 64, 0x40040
+    lib = lowbit_hip.library()
+    assert lib.lb_fused_linear(ctypes.byref(a), None) == lowbit_hip.INVALID_ARGUMENT
+    assert 'outputs of problems 0 and 1' in lib.lb_last_error().decode()
+
+
+def attention(**over):
+    a = lowbit_hip.DecodeAttentionArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.heads, a.kv_heads, a.head_dim, a.capacity = 9, 3, 64, 64
+    a.q, a.k, a.v, a.cos, a.sin, a.position = 0x10000, 0x11000, 0x12000, 0x20000, 0x30000, 0x40000
+    a.keys, a.values, a.out, a.scale = 0x100000, 0x200000, 0x50000, 0.125
+    for key, value in over.items():
+        setattr(a, key, value)
+    return a
+
+
+@pytest.mark.parametrize('over,needle,status', [
+    (dict(head_dim=128), 'head_dim', lowbit_hip.UNSUPPORTED),
+    (dict(kv_heads=4), 'multiple of kv_heads', lowbit_hip.INVALID_ARGUMENT),
+    (dict(capacity=5000), 'capacity', lowbit_hip.INVALID_ARGUMENT),
+    (dict(keys=0), 'NULL', lowbit_hip.INVALID_ARGUMENT),
+    (dict(keys=0x100008), 'misaligned', lowbit_hip.INVALID_ARGUMENT),
+    (dict(values=0x100000 + 3 * 64 * 128 - 16), 'keys overlap values', lowbit_hip.INVALID_ARGUMENT),
+    (dict(out=0x10040), 'overlaps q', lowbit_hip.INVALID_ARGUMENT),
+    (dict(scale=float('inf')), 'scale', lowbit_hip.INVALID_ARGUMENT),
+])
+def test_decode_attention_argument_errors(over, needle, status):
+    lib = lowbit_hip.library()
+    assert lib.lb_decode_attention(ctypes.byref(attention(**over)), None) == status
+    assert needle in lib.lb_last_error().decode()
+
+
+def test_argmax_next_argument_errors():
+    lib = lowbit_hip.library()
+    ok = (0x10000, 1000, 0x100000, 64, 0x20000, 0x30000, 0x31000, 0x32000, 8)
+    for index, value in ((0, 0), (1, 0), (3, 12), (4, 0x20008), (5, 0x30004), (8, -1), (4, 0x100000 + 640)):
+        bad = list(ok)
+        bad[index] = value
+        assert lib.lb_argmax_next(*bad, None) == lowbit_hip.INVALID_ARGUMENT, (index, value)

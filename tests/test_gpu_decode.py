@@ -1,0 +1,258 @@
+"""GPU parity of the decode-step entry points (include/lowbit_decode_hip.h) against the CPU oracle.
+
+lb_fused_linear: the prologue is applied on the CPU with the reference staging (RMSNorm
+torch_npu_smollm.py:166-168, SiLU * up :188-190), then oracle.lowbit_oracle.linear gives each
+projection (with its correction) and the residual is added in fp16; rel-L2 <= 1e-3.
+lb_decode_attention: RoPE/attention from oracle.smollm_oracle (the restated reference_cpu);
+the appended key/value rows are bit-exact, attention output rel-L2 <= 1e-3.
+lb_argmax_next: torch.argmax order (first maximal index), bit-exact embedding row.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import lowbit_hip as lb
+from conftest import announce
+from oracle import lowbit_oracle as lo
+from oracle import smollm_oracle as so
+from torch_npu_lowbit import quantize_weight
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a, b = torch.as_tensor(a).double().cpu(), torch.as_tensor(b).double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def prologue_cpu(kind, x, x2=None, gamma=None):
+    if kind == 'rmsnorm':
+        f = x.float()
+        return ((f * torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)).half() * gamma).half()
+    if kind == 'silu_mul':
+        return (F.silu(x.float()).half() * x2).half()
+    return x
+
+
+# (format, group (None = per row), K, prologue, output sizes, rank, residual, bias)
+CASES = [
+    ('int8', None, 576, 'rmsnorm', (576, 192, 192), 32, False, False),   # SmolLM q|k|v, W8 + rank 32
+    ('int8', None, 576, 'none', (576,), 32, True, False),                # o_proj + residual
+    ('int8', None, 576, 'rmsnorm', (1536, 1536), 32, False, False),      # gate|up
+    ('int8', None, 1536, 'silu_mul', (576,), 32, True, False),           # down + residual
+    ('int4', 32, 576, 'rmsnorm', (576, 192, 192), 0, False, False),      # w4a16 policy
+    ('nf4', 32, 1536, 'silu_mul', (200,), 0, True, False),               # partial last tile
+    ('int8', 64, 576, 'none', (40, 8, 100), 8, False, True),             # grouped int8, rank 8, bias
+    ('int4', 576, 576, 'none', (33,), 16, True, True),                   # one group per row
+    ('nf4', 64, 1024, 'rmsnorm', (40, 300), 24, False, True),
+    ('fp16', None, 576, 'rmsnorm', (4096,), 0, False, False),            # tied-head shape (smaller N)
+    ('fp16', None, 1536, 'silu_mul', (64, 64), 8, True, False),
+]
+
+
+def make_case(case, seed):
+    fmt, group, K, prologue, sizes, rank, residual, bias = case
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(K, generator=g).half()
+    x2 = torch.randn(K, generator=g).half() if prologue == 'silu_mul' else None
+    gamma = (1 + 0.1 * torch.randn(K, generator=g)).half() if prologue == 'rmsnorm' else None
+    problems = []
+    for n in sizes:
+        w = torch.randn(n, K, generator=g) * 0.02
+        pr = dict(N=n, w=w.half())
+        if fmt != 'fp16':
+            pr['packed'] = quantize_weight(w, format=fmt, group_size=group)
+        if rank:
+            pr['down'] = (torch.randn(rank, K, generator=g) * 0.01).half()
+            pr['up'] = (torch.randn(n, rank, generator=g) * 0.01).half()
+        if residual:
+            pr['residual'] = torch.randn(n, generator=g).half()
+        if bias:
+            pr['bias'] = (0.1 * torch.randn(n, generator=g)).half()
+        problems.append(pr)
+    return x, x2, gamma, problems
+
+
+def expected(case, x, x2, gamma, problems):
+    fmt, group, K, prologue = case[:4]
+    xp = prologue_cpu(prologue, x, x2, gamma)[None].numpy()
+    outs = []
+    for pr in problems:
+        n = pr['N']
+        down = pr['down'].numpy() if 'down' in pr else None
+        up = pr['up'].numpy() if 'up' in pr else None
+        b = pr['bias'].numpy() if 'bias' in pr else None
+        if fmt == 'fp16':
+            y = lo.dense_linear(xp, pr['w'].numpy())
+            if b is not None:
+                y = (y.astype(np.float64) + b.astype(np.float64)).astype(np.float16)
+            if down is not None:
+                z = lo.dense_linear(xp, down)
+                y = (y.astype(np.float64) + lo.dense_linear(z, up).astype(np.float64)).astype(np.float16)
+        else:
+            q = pr['packed']
+            y = lo.linear(xp, fmt, (n, K), q.group_size, q.data, q.scales, bias=b, down=down, up=up)
+        if 'residual' in pr:
+            y = (pr['residual'].numpy().astype(np.float64) + y.astype(np.float64)).astype(np.float16)
+        outs.append(torch.from_numpy(y[0]))
+    return outs
+
+
+def device_problems(case, problems, device, in_place):
+    fmt = case[0]
+    out = []
+    for pr in problems:
+        if fmt == 'fp16':
+            codes, scales = pr['w'].to(device), None
+        else:
+            codes, scales = pr['packed'].device_tensors(device)
+        d = dict(codes=codes, scales=scales, N=pr['N'])
+        if 'residual' in pr:
+            res = pr['residual'].to(device)
+            d['residual'] = res
+            d['y'] = res if in_place else torch.full((pr['N'],), float('nan'), dtype=torch.float16, device=device)
+        else:
+            d['y'] = torch.full((pr['N'],), float('nan'), dtype=torch.float16, device=device)
+        for key in ('down', 'up', 'bias'):
+            if key in pr:
+                d[key] = pr[key].to(device)
+        out.append(d)
+    return out
+
+
+@pytest.mark.parametrize('index', range(len(CASES)))
+def test_fused_linear_matches_oracle(device, index):
+    case = CASES[index]
+    announce('fused linear', case)
+    fmt, group, K, prologue = case[:4]
+    x, x2, gamma, problems = make_case(case, 100 + index)
+    want = expected(case, x, x2, gamma, problems)
+    for in_place in (False, True):
+        dev = device_problems(case, problems, device, in_place)
+        call = lb.PreparedFused(x.to(device), dev, format=fmt, K=K,
+                                group_size=K if group is None or fmt == 'fp16' else group, prologue=prologue,
+                                x2=None if x2 is None else x2.to(device),
+                                gamma=None if gamma is None else gamma.to(device), eps=1e-5)
+        call.run()
+        torch.cuda.synchronize()
+        got = [d['y'].cpu() for d in dev]
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert torch.isfinite(a).all(), (i, in_place)
+            err = rel_l2(a, b)
+            assert err <= 1e-3, (i, in_place, err)
+        if not in_place:  # a second call on the same buffers gives the same bits
+            call.run()
+            torch.cuda.synchronize()
+            for d, a in zip(dev, got):
+                assert torch.equal(d['y'].cpu(), a)
+
+
+def test_fused_linear_agrees_with_lb_linear(device):
+    """Same W8 + correction projection through lb_linear (prologue done on the CPU) and fused."""
+    announce('fused vs lb_linear')
+    case = CASES[0]
+    x, _, gamma, problems = make_case(case, 7)
+    xp = prologue_cpu('rmsnorm', x, gamma=gamma).to(device)[None]
+    dev = device_problems(case, problems, device, False)
+    lb.PreparedFused(x.to(device), dev, format='int8', K=576, group_size=576, prologue='rmsnorm',
+                     gamma=gamma.to(device)).run()
+    for d in dev:
+        ref = lb.linear(xp, d['codes'], d['scales'], format='int8', N=d['N'], K=576, group_size=576,
+                        down=d['down'], up=d['up'], rank=d['down'].shape[0])
+        torch.cuda.synchronize()
+        assert rel_l2(d['y'].cpu(), ref[0].cpu()) <= 1e-3
+
+
+def test_fused_linear_rejects_bad_arguments(device):
+    x = torch.zeros(576, dtype=torch.float16, device=device)
+    w = quantize_weight(torch.randn(64, 576), format='int8')
+    codes, scales = w.device_tensors(device)
+    y = torch.zeros(64, dtype=torch.float16, device=device)
+    up5 = torch.zeros(64, 5, dtype=torch.float16, device=device)
+    down5 = torch.zeros(5, 576, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError, match='up_ld'):
+        lb.fused_linear(x, [dict(codes=codes, scales=scales, N=64, y=y, down=down5, up=up5)], format='int8', K=576,
+                        group_size=576)
+    with pytest.raises(ValueError, match='overlaps'):
+        lb.fused_linear(x, [dict(codes=codes, scales=scales, N=64, y=x[:64])], format='int8', K=576, group_size=576)
+    with pytest.raises(ValueError, match='K='):
+        lb.fused_linear(torch.zeros(1600, dtype=torch.float16, device=device),
+                        [dict(codes=codes, scales=scales, N=64, y=y)], format='int8', K=1600, group_size=1600)
+
+
+def attention_case(pos, cap, seed):
+    g = torch.Generator().manual_seed(seed)
+    keys = (torch.randn(1, 3, cap, 64, generator=g) * 0.7).half()
+    values = torch.randn(1, 3, cap, 64, generator=g).half()
+    q = (torch.randn(576, generator=g) * 0.7).half()
+    k = (torch.randn(192, generator=g) * 0.7).half()
+    v = torch.randn(192, generator=g).half()
+    cos, sin = so.rope_tables(10000.0, cap)
+    return keys, values, q, k, v, cos, sin
+
+
+@pytest.mark.parametrize('pos', [0, 1, 37, 255, 383])
+def test_decode_attention_matches_oracle(device, pos):
+    announce('decode attention', pos)
+    cap = 384
+    keys, values, q, k, v, cos, sin = attention_case(pos, cap, pos)
+    c, s = cos[pos:pos + 1][None, None], sin[pos:pos + 1][None, None]
+    qr = so.OracleLayer._rotate(q.view(1, 1, 9, 64).transpose(1, 2), c, s)
+    kr = so.OracleLayer._rotate(k.view(1, 1, 3, 64).transpose(1, 2), c, s)
+    ks = torch.cat((keys[:, :, :pos], kr), dim=2)
+    vs = torch.cat((values[:, :, :pos], v.view(1, 1, 3, 64).transpose(1, 2)), dim=2)
+    want = so.OracleLayer._attend(qr, ks, vs, torch.zeros(1, pos + 1)).reshape(576)
+    dk, dv = keys.to(device), values.to(device)
+    out = torch.full((576,), float('nan'), dtype=torch.float16, device=device)
+    position = torch.tensor([pos], dtype=torch.int64, device=device)
+    lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
+                         out, heads=9, kv_heads=3).run()
+    torch.cuda.synchronize()
+    assert rel_l2(out.cpu(), want) <= 1e-3
+    assert torch.equal(dk[:, :, pos].cpu(), kr[:, :, 0])
+    assert torch.equal(dv[:, :, pos].cpu(), v.view(3, 64)[None])
+    others = [i for i in range(cap) if i != pos]
+    assert torch.equal(dk[:, :, others].cpu(), keys[:, :, others])
+    assert torch.equal(dv[:, :, others].cpu(), values[:, :, others])
+
+
+def test_decode_attention_full_cache_is_a_no_op(device):
+    cap = 16
+    keys, values, q, k, v, cos, sin = attention_case(0, cap, 3)
+    dk, dv = keys.to(device), values.to(device)
+    out = torch.full((576,), 7.0, dtype=torch.float16, device=device)
+    position = torch.tensor([cap], dtype=torch.int64, device=device)
+    lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
+                         out, heads=9, kv_heads=3).run()
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), keys) and torch.equal(dv.cpu(), values)
+    assert bool((out.cpu() == 7.0).all())
+
+
+def test_argmax_next_order_position_and_embedding(device):
+    announce('argmax next')
+    vocab, hidden = 1003, 64
+    g = torch.Generator().manual_seed(11)
+    emb = torch.randn(vocab, hidden, generator=g).half().to(device)
+    logits = torch.randn(vocab, generator=g).half()
+    logits[700] = logits[300] = 9.0           # tie: the first index wins (torch.argmax)
+    logits[1001] = float('nan')               # never chosen
+    assert int(logits[:1001].float().argmax()) == 300
+    tokens = torch.full((10,), -1, dtype=torch.int64, device=device)
+    token = torch.zeros(1, dtype=torch.int64, device=device)
+    position = torch.tensor([5], dtype=torch.int64, device=device)
+    h = torch.zeros(hidden, dtype=torch.float16, device=device)
+    call = lb.PreparedArgmax(logits.to(device), emb, h, tokens, token, position, limit=10)
+    call.run()
+    torch.cuda.synchronize()
+    assert int(token) == 300 and int(position) == 6 and int(tokens[5]) == 300
+    assert torch.equal(h, emb[300])
+    position.fill_(10)                        # at the limit: token and h still update, nothing else
+    call.run()
+    torch.cuda.synchronize()
+    assert int(position) == 10 and int((tokens >= 0).sum()) == 1
+    ninf = torch.full((vocab,), float('-inf'), dtype=torch.float16, device=device)
+    lb.PreparedArgmax(ninf, emb, h, tokens, token, position, limit=10).run()
+    torch.cuda.synchronize()
+    assert int(token) == 0 and torch.equal(h, emb[0])

@@ -123,18 +123,42 @@ def test_config4_greedy_tokens_and_logits(device):
     assert tokens == ref_tokens
 
 
-def test_graph_decoder_matches_eager_and_oracle(device):
-    """The captured decode step reproduces the eager decode tokens (small stack, 24 steps)."""
-    announce('graph decoder')
+@pytest.mark.parametrize('fused', [True, False])
+def test_graph_decoder_matches_eager(device, fused):
+    """The captured decode step reproduces the eager decode tokens and logits (4 layers, 24 steps)."""
+    announce('graph decoder', 'fused' if fused else 'staged')
     from torch_npu_smollm import GraphDecoder
     stack, io, _, _ = smollm_random.build(seed=5, layers=4, rank=32, theta=10000.0, capacity=96)
     io = io.to(device)
     ids = smollm_random.prompt(seed=5, length=40)
-    tokens, _ = generate_greedy(stack, io, ids, 24)
+    tokens, logits = generate_greedy(stack, io, ids, 24)
     x = io.embed_tokens(ids.to(device))
     h, caches = stack.prefill(x)
     first = int(io.logits(h[:, -1:])[0, 0].float().argmax())
-    decoder = GraphDecoder(stack, io)
+    decoder = GraphDecoder(stack, io, fused=fused)
     decoder.load(caches, first)
     rest = decoder.generate(23)
     assert [first] + rest == tokens
+    assert rel_l2(decoder.logits.view(-1), logits[23]) <= 1e-2
+    with pytest.raises(ValueError):
+        decoder.generate(96)
+
+
+def test_config4_graph_decoder_matches_oracle(device):
+    """Config 4 through the fused, graph-replayed decode step: 32 greedy tokens equal the oracle's."""
+    announce('config4 graph decoder parity')
+    from torch_npu_smollm import GraphDecoder
+    steps = 32
+    stack, io, packed, corr = smollm_random.build(seed=0, layers=30, rank=32, theta=10000.0, capacity=384)
+    ids = smollm_random.prompt(seed=0, length=256)
+    io = io.to(device)
+    layers = [so.OracleLayer(layer._weights, packed_of(layer), corr_of(layer), theta=10000.0, capacity=384)
+              for layer in stack.layers]
+    oracle = so.OracleModel(layers, io.embedding.cpu(), io.norm.cpu())
+    ref_tokens, ref_logits = oracle.generate(ids, steps)
+    h, caches = stack.prefill(io.embed_tokens(ids.to(device)))
+    decoder = GraphDecoder(stack, io)
+    decoder.load(caches, ref_tokens[0])
+    rest = decoder.generate(steps - 1)
+    assert [ref_tokens[0]] + rest == ref_tokens
+    assert rel_l2(decoder.logits.view(-1), ref_logits[steps - 1]) <= 1e-2

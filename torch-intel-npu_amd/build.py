@@ -12,8 +12,9 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / 'csrc'
 LIBRARY = HERE / 'liblowbit_hip.so'
-SOURCES = [CSRC / 'lowbit_abi.hip']
-HEADERS = [CSRC / 'lb_common.h', CSRC / 'lb_kernels.h', HERE.parent / 'include' / 'lowbit_hip.h']
+SOURCES = [CSRC / 'lowbit_abi.hip', CSRC / 'decode_abi.hip']
+HEADERS = [CSRC / 'lb_common.h', CSRC / 'lb_kernels.h', CSRC / 'lb_decode.h', CSRC / 'abi_util.h',
+           HERE.parent / 'include' / 'lowbit_hip.h', HERE.parent / 'include' / 'lowbit_decode_hip.h']
 ARCH = 'gfx950'
 
 

@@ -1,0 +1,243 @@
+// C-ABI of the decode-step entry points (include/lowbit_decode_hip.h): validation and launches.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "../../include/lowbit_decode_hip.h"
+#include "abi_util.h"
+#include "lb_decode.h"
+
+using namespace lb;
+using namespace lb::abi;
+
+namespace {
+
+bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int shift_of(int64_t group, int64_t K) {
+  if (group == K) return 31;
+  int sh = 0;
+  while ((int64_t)1 << sh < group) ++sh;
+  return sh;
+}
+
+size_t code_bytes(uint32_t format, int64_t N, int64_t K) {
+  const int64_t count = N * K;
+  return format == LB_FORMAT_FP16 ? (size_t)count * 2 : format == LB_FORMAT_INT8 ? (size_t)count : (size_t)(count + 1) / 2;
+}
+
+lb_status check_fused(const lb_fused_linear_args *a) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: args is NULL");
+  if (a->struct_size < sizeof(lb_fused_linear_args))
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: struct_size %u < %zu", a->struct_size,
+                sizeof(lb_fused_linear_args));
+  if (a->format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: unknown format %u", a->format);
+  if (a->K <= 0 || a->K % 32 != 0 || a->K > LB_FUSED_MAX_K)
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: K=%lld must be a positive multiple of 32 <= %d",
+                (long long)a->K, LB_FUSED_MAX_K);
+  const bool dense = a->format == LB_FORMAT_FP16;
+  if (!dense) {
+    const int64_t g = a->group_size;
+    if (!(g == a->K || (pow2(g) && g >= 32 && a->K % g == 0)))
+      return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: group_size %lld must be K or a power of two >= 32 dividing K",
+                  (long long)g);
+  }
+  if (a->prologue > LB_PROLOGUE_SILU_MUL) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: unknown prologue %u", a->prologue);
+  if (a->count < 1 || a->count > LB_FUSED_MAX_PROBLEMS)
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: count %u outside 1..%d", a->count, LB_FUSED_MAX_PROBLEMS);
+  if (!a->x || !aligned(a->x, 16)) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: x must be non-NULL and 16-byte aligned");
+  if (a->prologue == LB_PROLOGUE_SILU_MUL && (!a->x2 || !aligned(a->x2, 16)))
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: SILU_MUL needs a 16-byte aligned x2");
+  if (a->prologue == LB_PROLOGUE_RMSNORM && (!a->gamma || !aligned(a->gamma, 16) || !std::isfinite(a->eps) || a->eps < 0))
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: RMSNORM needs a 16-byte aligned gamma and a finite eps >= 0");
+
+  const size_t kb = (size_t)a->K * 2;
+  Range in[4 + 6 * LB_FUSED_MAX_PROBLEMS];
+  int nin = 0;
+  in[nin++] = range_of(a->x, kb, "x");
+  in[nin++] = range_of(a->prologue == LB_PROLOGUE_SILU_MUL ? a->x2 : nullptr, a->prologue == LB_PROLOGUE_SILU_MUL ? kb : 0, "x2");
+  in[nin++] = range_of(a->prologue == LB_PROLOGUE_RMSNORM ? a->gamma : nullptr, a->prologue == LB_PROLOGUE_RMSNORM ? kb : 0, "gamma");
+  int64_t tiles = 0;
+  for (uint32_t i = 0; i < a->count; ++i) {
+    const lb_fused_problem &q = a->problems[i];
+    if (q.N <= 0 || q.N > ((int64_t)1 << 30))
+      return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: problem %u: N=%lld outside 1..2^30", i, (long long)q.N);
+    if (!q.codes || !aligned(q.codes, 16) || !q.y || !aligned(q.y, 2) || (!dense && (!q.scales || !aligned(q.scales, 2))))
+      return fail(LB_INVALID_ARGUMENT,
+                  "lb_fused_linear: problem %u: codes (16-byte aligned), scales and y (2-byte aligned) required", i);
+    if ((q.bias && !aligned(q.bias, 2)) || (q.residual && !aligned(q.residual, 2)))
+      return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: problem %u: bias/residual must be 2-byte aligned", i);
+    if (q.rank < 0 || q.rank > LB_FUSED_MAX_RANK || q.rank > std::min(q.N, a->K))
+      return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: problem %u: rank %lld outside 0..%d", i, (long long)q.rank,
+                  LB_FUSED_MAX_RANK);
+    if (q.rank > 0 && (!q.down || !q.up || !aligned(q.down, 16) || !aligned(q.up, 16) || q.up_ld < q.rank ||
+                       q.up_ld % 8 != 0))
+      return fail(LB_INVALID_ARGUMENT,
+                  "lb_fused_linear: problem %u: correction needs 16-byte aligned down/up and up_ld %% 8 == 0, >= rank", i);
+    tiles += (q.N + 15) / 16;
+    const int64_t G = dense ? 1 : a->K / a->group_size;
+    in[nin++] = range_of(q.codes, code_bytes(a->format, q.N, a->K), "codes");
+    in[nin++] = range_of(dense ? nullptr : q.scales, dense ? 0 : (size_t)(q.N * G * 2), "scales");
+    in[nin++] = range_of(q.bias, q.bias ? (size_t)q.N * 2 : 0, "bias");
+    in[nin++] = range_of(q.rank ? q.down : nullptr, q.rank ? (size_t)(q.rank * a->K * 2) : 0, "down");
+    in[nin++] = range_of(q.rank ? q.up : nullptr, q.rank ? (size_t)((q.N - 1) * q.up_ld + q.rank) * 2 : 0, "up");
+    in[nin++] = range_of(q.residual != q.y ? q.residual : nullptr, q.residual && q.residual != q.y ? (size_t)q.N * 2 : 0,
+                         "residual");
+  }
+  if (tiles > INT32_MAX) return fail(LB_UNSUPPORTED, "lb_fused_linear: too many rows");
+  for (uint32_t i = 0; i < a->count; ++i) {
+    const Range y = range_of(a->problems[i].y, (size_t)a->problems[i].N * 2, "y");
+    for (int r = 0; r < nin; ++r)
+      if (overlaps(y, in[r])) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: y of problem %u overlaps %s", i, in[r].name);
+    for (uint32_t k = i + 1; k < a->count; ++k)
+      if (overlaps(y, range_of(a->problems[k].y, (size_t)a->problems[k].N * 2, "y")))
+        return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: outputs of problems %u and %u overlap", i, k);
+  }
+  return ok();
+}
+
+template <int FMT, bool SCALED>
+void launch_fused_t(const FusedParams &p, int tiles, hipStream_t s) {
+  if (p.K <= 640)
+    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, 640>), dim3(tiles), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, LB_FUSED_MAX_K>), dim3(tiles), dim3(256), 0, s, p);
+}
+
+lb_status launch_status(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LB_DEVICE_FAILED, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
+  const lb_status st = check_fused(a);
+  if (st != LB_OK) return st;
+  FusedParams p{};
+  const bool dense = a->format == LB_FORMAT_FP16;
+  p.x = static_cast<const f16 *>(a->x);
+  p.x2 = static_cast<const f16 *>(a->x2);
+  p.gamma = static_cast<const f16 *>(a->gamma);
+  p.eps = a->eps;
+  p.K = (int)a->K;
+  const int64_t group = dense ? a->K : a->group_size;
+  p.G = (int)(a->K / group);
+  p.group_shift = shift_of(group, a->K);
+  p.per_row = a->format == LB_FORMAT_INT8 && group == a->K;
+  p.prologue = (int)a->prologue;
+  int tiles = 0;
+  for (int i = 0; i < LB_FUSED_MAX_PROBLEMS; ++i) {
+    FusedProblem &q = p.prob[i];
+    if (i < (int)a->count) {
+      const lb_fused_problem &s = a->problems[i];
+      q.codes = static_cast<const uint8_t *>(s.codes);
+      q.scales = static_cast<const f16 *>(s.scales);
+      q.y = static_cast<f16 *>(s.y);
+      q.bias = static_cast<const f16 *>(s.bias);
+      q.residual = static_cast<const f16 *>(s.residual);
+      q.rank = (int)s.rank;
+      q.down = s.rank ? static_cast<const f16 *>(s.down) : nullptr;
+      q.up = s.rank ? static_cast<const f16 *>(s.up) : nullptr;
+      q.up_ld = (int)s.up_ld;
+      q.N = (int)s.N;
+      tiles += (int)((s.N + 15) / 16);
+    }
+    q.tiles_end = tiles;  // absent problems own no tiles
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool scaled = !dense && !p.per_row;
+  switch (a->format) {
+    case LB_FORMAT_INT8:
+      scaled ? launch_fused_t<FMT_INT8, true>(p, tiles, s) : launch_fused_t<FMT_INT8, false>(p, tiles, s);
+      break;
+    case LB_FORMAT_INT4: launch_fused_t<FMT_INT4, true>(p, tiles, s); break;
+    case LB_FORMAT_NF4: launch_fused_t<FMT_NF4, true>(p, tiles, s); break;
+    default: launch_fused_t<FMT_FP16, false>(p, tiles, s); break;
+  }
+  return launch_status("lb_fused_linear");
+}
+
+lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: args is NULL");
+  if (a->struct_size < sizeof(lb_decode_attention_args))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: struct_size %u < %zu", a->struct_size,
+                sizeof(lb_decode_attention_args));
+  if (a->head_dim != kHeadDim) return fail(LB_UNSUPPORTED, "lb_decode_attention: head_dim must be %d", kHeadDim);
+  if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0 || a->heads > 1024)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: heads must be a multiple of kv_heads (<= 1024)");
+  if (a->capacity < 1 || a->capacity > 4096)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: capacity %lld outside 1..4096", (long long)a->capacity);
+  if (!a->q || !a->k || !a->v || !a->cos || !a->sin || !a->position || !a->keys || !a->values || !a->out)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: NULL pointer");
+  if (!aligned(a->q, 2) || !aligned(a->k, 2) || !aligned(a->v, 2) || !aligned(a->cos, 2) || !aligned(a->sin, 2) ||
+      !aligned(a->out, 2) || !aligned(a->position, 8) || !aligned(a->keys, 16) || !aligned(a->values, 16))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: misaligned buffer (keys/values need 16 bytes)");
+  if (!std::isfinite(a->scale)) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: scale must be finite");
+  const size_t row = kHeadDim * 2;
+  const size_t cache = (size_t)a->kv_heads * a->capacity * row;
+  const Range keys = range_of(a->keys, cache, "keys"), values = range_of(a->values, cache, "values");
+  const Range out = range_of(a->out, (size_t)a->heads * row, "out");
+  const Range in[] = {range_of(a->q, (size_t)a->heads * row, "q"), range_of(a->k, (size_t)a->kv_heads * row, "k"),
+                      range_of(a->v, (size_t)a->kv_heads * row, "v"), range_of(a->cos, (size_t)a->capacity * row, "cos"),
+                      range_of(a->sin, (size_t)a->capacity * row, "sin"),
+                      range_of(a->position, sizeof(int64_t), "position")};
+  if (overlaps(keys, values)) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: keys overlap values");
+  for (const Range &r : in) {
+    if (overlaps(out, r) || overlaps(keys, r) || overlaps(values, r))
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: an output overlaps %s", r.name);
+  }
+  if (overlaps(out, keys) || overlaps(out, values))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: out overlaps the cache");
+  AttnParams p{};
+  p.q = static_cast<const f16 *>(a->q);
+  p.k = static_cast<const f16 *>(a->k);
+  p.v = static_cast<const f16 *>(a->v);
+  p.cos = static_cast<const f16 *>(a->cos);
+  p.sin = static_cast<const f16 *>(a->sin);
+  p.position = a->position;
+  p.keys = static_cast<f16 *>(a->keys);
+  p.values = static_cast<f16 *>(a->values);
+  p.out = static_cast<f16 *>(a->out);
+  p.heads = (int)a->heads;
+  p.kv_heads = (int)a->kv_heads;
+  p.capacity = (int)a->capacity;
+  p.scale = a->scale;
+  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)a->heads), dim3(256), (size_t)a->capacity * sizeof(float),
+                     static_cast<hipStream_t>(stream), p);
+  return launch_status("lb_decode_attention");
+}
+
+lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embedding, int64_t hidden, void *h_next,
+                         int64_t *tokens, int64_t *token, int64_t *position, int64_t limit, void *stream) {
+  if (!logits || !embedding || !h_next || !tokens || !token || !position)
+    return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: NULL pointer");
+  if (vocab < 1 || vocab > INT32_MAX / 2 || hidden < 8 || hidden % 8 != 0 || hidden > 65536 || limit < 0 ||
+      limit > INT32_MAX)
+    return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: vocab >= 1, hidden a positive multiple of 8, limit >= 0");
+  if (!aligned(logits, 16) || !aligned(embedding, 16) || !aligned(h_next, 16) || !aligned(tokens, 8) ||
+      !aligned(token, 8) || !aligned(position, 8))
+    return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: logits/embedding/h_next need 16-byte, indices 8-byte alignment");
+  const Range h = range_of(h_next, (size_t)hidden * 2, "h_next");
+  const Range outs[] = {h, range_of(tokens, (size_t)limit * 8, "tokens"), range_of(token, 8, "token"),
+                        range_of(position, 8, "position")};
+  const Range ins[] = {range_of(logits, (size_t)vocab * 2, "logits"),
+                       range_of(embedding, (size_t)vocab * hidden * 2, "embedding")};
+  for (int i = 0; i < 4; ++i) {
+    for (const Range &r : ins)
+      if (overlaps(outs[i], r)) return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: %s overlaps %s", outs[i].name, r.name);
+    for (int k = i + 1; k < 4; ++k)
+      if (overlaps(outs[i], outs[k]))
+        return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: %s overlaps %s", outs[i].name, outs[k].name);
+  }
+  hipLaunchKernelGGL(argmax_next_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const f16 *>(logits), (int)vocab, static_cast<const f16 *>(embedding), (int)hidden,
+                     static_cast<f16 *>(h_next), tokens, token, position, (int)limit);
+  return launch_status("lb_argmax_next");
+}
+
+}  // extern "C"

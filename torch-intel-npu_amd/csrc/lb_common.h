@@ -135,6 +135,12 @@ __device__ __forceinline__ h8 decode8(const u4 &w, int t8, h2 s2, const uint32_t
   return out;
 }
 
+// Raw buffer resource over [base, base + bytes): loads at or beyond `bytes` return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, size_t bytes) {
+  const int records = bytes > 0x7FFFFFF0ull ? 0x7FFFFFF0 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, records, 0x00020000);
+}
+
 // Arguments shared by the linear kernels (device pointers, element strides).
 struct LinearParams {
   const uint8_t *codes;   // packed codes, or fp16 weights for FMT_FP16

@@ -1,0 +1,418 @@
+// gfx950 kernels of one SmolLM decode step (one sequence, one token).
+//
+//   fused_gemv_kernel     up to three low-bit linears that share one activation row, in one
+//                         launch, with the layer's neighbouring element-wise work folded in:
+//                         a prologue (RMSNorm, or SiLU(gate) * up) that every workgroup
+//                         applies to the row it stages, the rank-r correction z = fp16(x.V^T)
+//                         computed inside each workgroup while its weights are in flight, and
+//                         an epilogue that adds fp16(z.U^T) and, optionally, a residual.
+//   decode_attention_kernel  RoPE of the new query/key row, KV append at the device-held
+//                         position, scores, softmax and P.V for one query head.
+//   argmax_next_kernel    greedy token of the logits row; writes it, advances the position and
+//                         gathers the next input embedding.
+//
+// Staging (fp16 rounding points) is that of the reference CPU layer, torch_npu_smollm.py:142-193:
+// RMSNorm fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma); RoPE fp16(fp16(t cos) + fp16(rot(t) sin));
+// scores fp16(q.k), fp16(* scale); softmax in fp32 rounded to fp16; P.V fp32 -> fp16;
+// MLP fp16(fp16(silu(gate)) * up); residual fp16(x + delta).
+#pragma once
+#include "lb_common.h"
+
+namespace lb {
+
+constexpr int kFusedMaxProblems = 3;
+constexpr int kFusedMaxRank = 32;
+enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
+
+struct FusedProblem {
+  const uint8_t *codes;   // packed codes (fp16 weights for FMT_FP16), rows [N, K]
+  const f16 *scales;      // [N, G]
+  f16 *y;                 // [N]
+  const f16 *bias;        // [N] or null
+  const f16 *residual;    // [N] or null (may equal y: each element is read and written by one lane)
+  const f16 *down;        // V [rank, K] or null
+  const f16 *up;          // U [N, up_ld] or null
+  int N, rank, up_ld;
+  int tiles_end;          // exclusive prefix sum of 16-row tiles over the problems
+};
+
+struct FusedParams {
+  const f16 *x;           // [K] activation (PRO_SILU_MUL: the gate row)
+  const f16 *x2;          // PRO_SILU_MUL: the up row [K]
+  const f16 *gamma;       // PRO_RMSNORM: [K]
+  float eps;
+  int K, G, group_shift, per_row, prologue;
+  FusedProblem prob[kFusedMaxProblems];
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// One rotate-half RoPE element with the reference's three fp16 roundings,
+// fp16(fp16(x * c) + fp16(r * s)).  Contraction stays off: once x * c is narrowed to an fp16
+// multiply (exact, as both factors are fp16) the compiler would otherwise fuse it with the add
+// and drop the first rounding.
+__device__ __forceinline__ f16 rope_element(float x, float r, float c, float s) {
+#pragma clang fp contract(off)
+  const f16 a = (f16)(x * c);
+  const f16 b = (f16)(r * s);
+  return (f16)((float)a + (float)b);
+}
+
+// One workgroup = 4 waves = one 16-row tile of one problem; the waves split K (wave w takes
+// k-steps w, w + 4, ...) and are reduced through LDS.  K <= KMAX, so every lane issues all
+// of its weight loads (D of them) up front and the activation row is staged once.
+template <int FMT, bool SCALED, int KMAX>
+__global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
+  constexpr int CPL = FormatTraits<FMT>::CPL;
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  constexpr int KSTEP = 4 * CPL;
+  constexpr int KG = 4;
+  constexpr int WSTEP = KG * KSTEP;
+  constexpr int D = (KMAX + WSTEP - 1) / WSTEP;  // weight loads per lane
+  constexpr int T8 = CPL / 8;
+  constexpr int XLD = KMAX + KSTEP + 8;           // staged row, zero beyond K
+  constexpr int VB = KMAX / 64;                   // 16-byte V loads per thread (8 threads per rank row)
+  constexpr int GMAX = KMAX / 32;                 // groups per row (group >= 32)
+  constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;  // staged scales per thread
+  __shared__ __align__(16) f16 xs[2 * XLD];       // row 0: the activation, row 1: zeros
+  __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
+  __shared__ float zs[kFusedMaxRank];
+  __shared__ float red[(KG - 1) * 16];
+  __shared__ float wsum[4];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int K = p.K;
+
+  // Problem and tile of this workgroup (wave-uniform selects; no dynamic kernarg indexing).
+  const int bid = blockIdx.x;
+  const int pi = bid < p.prob[0].tiles_end ? 0 : (bid < p.prob[1].tiles_end ? 1 : 2);
+  FusedProblem P = p.prob[0];
+  int first = 0;
+  if (pi == 1) { P = p.prob[1]; first = p.prob[0].tiles_end; }
+  if (pi == 2) { P = p.prob[2]; first = p.prob[1].tiles_end; }
+  const int n0 = (bid - first) * 16;
+  const int rows = min(16, P.N - n0);
+  const int row_bytes = K * BITS / 8;
+  constexpr int kOutOfRange = (int)0x80000000u;
+
+  // ---- issue every global load: activation, scales, V, epilogue operands, then weights ----
+  const int blocks = K >> 3;
+  h8 xv = {}, x2v = {}, gv = {};
+  if (t < blocks) {
+    xv = *reinterpret_cast<const h8 *>(p.x + t * 8);
+    if (p.prologue == PRO_SILU_MUL) x2v = *reinterpret_cast<const h8 *>(p.x2 + t * 8);
+    if (p.prologue == PRO_RMSNORM) gv = *reinterpret_cast<const h8 *>(p.gamma + t * 8);
+  }
+  f16 sreg[SC > 0 ? SC : 1];
+  if constexpr (SCALED) {
+    const int valid = rows * p.G;
+#pragma unroll
+    for (int i = 0; i < SC; ++i) {
+      const int idx = t + i * 256;
+      sreg[i] = idx < valid ? P.scales[(size_t)n0 * p.G + idx] : (f16)0.0f;
+    }
+  }
+  const int rank = P.rank;
+  u4 vreg[VB];
+  const int vr = t >> 3, vpart = t & 7;
+  if (rank > 0) {
+    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(P.down, (size_t)rank * K * 2);
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int k = (vpart + 8 * i) * 8;
+      const int off = (vr < rank && k < K) ? (vr * K + k) * 2 : kOutOfRange;
+      vreg[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
+    }
+  }
+  // Epilogue operands of lane (j, g == 0) of wave 0: row n0 + j.
+  const bool writer = wave == 0 && g == 0 && j < rows;
+  const int n = n0 + j;
+  u4 ureg[kFusedMaxRank / 8];
+  f16 res = (f16)0.0f, bia = (f16)0.0f, rsc = (f16)1.0f;
+  if (writer) {
+    if (P.residual) res = P.residual[n];
+    if (P.bias) bia = P.bias[n];
+    if (p.per_row) rsc = P.scales[n];
+    if (rank > 0) {
+#pragma unroll
+      for (int q = 0; q < kFusedMaxRank / 8; ++q)
+        ureg[q] = q * 8 < rank ? *reinterpret_cast<const u4 *>(P.up + (size_t)n * P.up_ld + q * 8) : u4{};
+    }
+  }
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(P.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  u4 w[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int k = (wave + KG * u) * KSTEP + g * CPL;
+    const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
+    w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
+  }
+
+  // ---- prologue: stage the activation row (fp16, in the format's slot order) ----
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  float inv = 1.0f;
+  if (p.prologue == PRO_RMSNORM) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)xv[e] * (float)xv[e];
+    s = wave_sum(s);
+    if (lane == 0) wsum[wave] = s;
+    __syncthreads();
+    const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    inv = 1.0f / sqrtf(total / (float)K + p.eps);
+  }
+  if (t < blocks) {
+    h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (p.prologue == PRO_RMSNORM)
+        v[e] = (f16)((float)(f16)((float)xv[e] * inv) * (float)gv[e]);
+      else if (p.prologue == PRO_SILU_MUL)
+        v[e] = (f16)((float)(f16)silu((float)xv[e]) * (float)x2v[e]);
+      else
+        v[e] = xv[e];
+    }
+    *reinterpret_cast<h8 *>(xs + t * 8) = permute_block<FMT>(v);
+  }
+  for (int b = blocks + t; b < 2 * XLD / 8; b += 256)  // zeros: tail of row 0, all of row 1
+    *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      if (t + i * 256 < 16 * GMAX) ss[t + i * 256] = sreg[i];
+    if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;  // lanes past K of the last row index up to 4 beyond
+  }
+  __syncthreads();
+
+  // ---- correction activations z = fp16(x . V^T), 8 threads per rank row ----
+  if (rank > 0) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
+      const h8 xx = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)xx[e] * (float)vv[e];
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 4, 64);
+    if (vpart == 0 && vr < kFusedMaxRank) zs[vr] = (float)(f16)acc;
+  }
+
+  // ---- the product on MFMA: A = activation row (row 0) or zeros, B = decoded weights ----
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const f16 *a0 = xs + (j == 0 ? 0 : XLD) + g * CPL;
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int kb = (wave + KG * u) * KSTEP;
+    if (kb >= K) break;  // wave-uniform
+    h2 s2 = {(f16)1.0f, (f16)1.0f};
+    if constexpr (SCALED) {
+      const f16 sc = ss[j * p.G + ((kb + g * CPL) >> p.group_shift)];
+      s2 = h2{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < T8; ++q) {
+      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
+      const h8 b = decode8<FMT, !SCALED>(w[u], q, s2, nf4_table);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+  // Lane (j, g) holds D rows 4g..4g+3 of column j; the activation is row 0 (g == 0, r == 0).
+  if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
+  __syncthreads();
+  if (!writer) return;
+  float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
+
+  // ---- epilogue (reference torch_npu_lowbit.py:262-266, torch_npu_smollm.py:160-163) ----
+  if (p.per_row) sum *= (float)rsc;
+  f16 h = (f16)sum;
+  if (P.bias) h = (f16)((float)h + (float)bia);
+  if (rank > 0) {
+    float d = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kFusedMaxRank / 8; ++q) {
+      const h8 uu = __builtin_bit_cast(h8, ureg[q]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (q * 8 + e < rank) d += zs[q * 8 + e] * (float)uu[e];
+    }
+    h = (f16)((float)h + (float)(f16)d);
+  }
+  if (P.residual) h = (f16)((float)res + (float)h);
+  P.y[n] = h;
+}
+
+struct AttnParams {
+  const f16 *q, *k, *v;      // new rows: q [heads, 64], k and v [kv_heads, 64]
+  const f16 *cos, *sin;      // [capacity, 64]
+  const int64_t *position;   // device scalar: the slot of the new token
+  f16 *keys, *values;        // [kv_heads, capacity, 64]
+  f16 *out;                  // [heads, 64]
+  int heads, kv_heads, capacity;
+  float scale;
+};
+
+constexpr int kHeadDim = 64;
+constexpr int kAttnParts = 32;  // position partitions of the P.V product
+
+// One workgroup per query head.  The first query head of each KV group writes the rotated key
+// and the value into the cache; every workgroup uses its own copy of that new row, so no
+// workgroup reads a cache slot another one writes.
+__global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
+  extern __shared__ float sc[];  // [capacity] scores, then probabilities
+  __shared__ __align__(16) f16 qs[kHeadDim], kn[kHeadDim], vn[kHeadDim];
+  __shared__ float wred[4];
+  __shared__ float pv[kAttnParts * kHeadDim];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = blockIdx.x;
+  const int group = p.heads / p.kv_heads;
+  const int kvh = h / group;
+  const int pos = (int)p.position[0];
+  if (pos < 0 || pos >= p.capacity) return;  // host guarantees; never index outside the cache
+
+  if (t < 3 * kHeadDim) {
+    const int which = t >> 6, d = t & 63;
+    const f16 *src = which == 0 ? p.q + h * kHeadDim : (which == 1 ? p.k : p.v) + kvh * kHeadDim;
+    if (which == 2) {
+      vn[d] = src[d];
+    } else {
+      const float c = (float)p.cos[(size_t)pos * kHeadDim + d];
+      const float s = (float)p.sin[(size_t)pos * kHeadDim + d];
+      const float rot = d < 32 ? -(float)src[d + 32] : (float)src[d - 32];
+      const f16 r = rope_element((float)src[d], rot, c, s);
+      if (which == 0) qs[d] = r; else kn[d] = r;
+    }
+  }
+  __syncthreads();
+  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
+  if (h % group == 0 && t < 2 * kHeadDim) {
+    const int d = t & 63;
+    f16 *dst = (t < kHeadDim ? p.keys : p.values) + head_base + (size_t)pos * kHeadDim + d;
+    *dst = t < kHeadDim ? kn[d] : vn[d];
+  }
+
+  // scores = fp16(fp16(q . k) * scale) over slots 0..pos
+  float lmax = -INFINITY;
+  for (int s = t; s <= pos; s += 256) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < kHeadDim / 8; ++b) {
+      const h8 qq = *reinterpret_cast<const h8 *>(qs + 8 * b);
+      const h8 kk = s < pos ? *reinterpret_cast<const h8 *>(p.keys + head_base + (size_t)s * kHeadDim + 8 * b)
+                            : *reinterpret_cast<const h8 *>(kn + 8 * b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)qq[e] * (float)kk[e];
+    }
+    const float v = (float)(f16)((float)(f16)acc * p.scale);
+    sc[s] = v;
+    lmax = fmaxf(lmax, v);
+  }
+  lmax = wave_max(lmax);
+  if (lane == 0) wred[wave] = lmax;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float lsum = 0.0f;
+  for (int s = t; s <= pos; s += 256) {
+    const float e = expf(sc[s] - m);
+    sc[s] = e;
+    lsum += e;
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();  // every wave has read wred
+  if (lane == 0) wred[wave] = lsum;
+  __syncthreads();
+  const float total = ((wred[0] + wred[1]) + wred[2]) + wred[3];
+  for (int s = t; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
+  __syncthreads();
+
+  // out = fp16(P . V): thread (blk, part) sums 8 dims over slots part, part + 32, ...
+  const int blk = t & 7, part = t >> 3;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = part; s <= pos; s += kAttnParts) {
+    const float pr = sc[s];
+    const h8 vv = s < pos ? *reinterpret_cast<const h8 *>(p.values + head_base + (size_t)s * kHeadDim + 8 * blk)
+                          : *reinterpret_cast<const h8 *>(vn + 8 * blk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pv[part * kHeadDim + blk * 8 + e] = o[e];
+  __syncthreads();
+  if (t < kHeadDim) {
+    float r = 0.0f;
+    for (int q = 0; q < kAttnParts; ++q) r += pv[q * kHeadDim + t];
+    p.out[h * kHeadDim + t] = (f16)r;
+  }
+}
+
+// Greedy next token: first index of the largest logit (torch.argmax order), written to
+// tokens[position] and token; the position advances by one and h receives the token's
+// embedding row.  One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void argmax_next_kernel(const f16 *logits, int vocab, const f16 *embedding,
+                                                           int hidden, f16 *h, int64_t *tokens, int64_t *token,
+                                                           int64_t *position, int limit) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  __shared__ int chosen;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int b = t; b * 8 < vocab; b += 1024) {
+    if (b * 8 + 8 <= vocab) {
+      const h8 v = *reinterpret_cast<const h8 *>(logits + b * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if ((float)v[e] > best) { best = (float)v[e]; idx = b * 8 + e; }
+    } else {
+      for (int i = b * 8; i < vocab; ++i)
+        if ((float)logits[i] > best) { best = (float)logits[i]; idx = i; }
+    }
+  }
+  if (idx == 0x7fffffff) idx = vocab;  // a thread with no element (or only -inf) loses every tie below
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(idx, off, 64);
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+  }
+  if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+  __syncthreads();
+  if (t == 0) {
+    float b0 = bv[0];
+    int i0 = bi[0];
+    for (int w = 1; w < 16; ++w)
+      if (bv[w] > b0 || (bv[w] == b0 && bi[w] < i0)) { b0 = bv[w]; i0 = bi[w]; }
+    if (i0 >= vocab) i0 = 0;  // every logit -inf: torch.argmax returns 0
+    chosen = i0;
+    const int64_t pos = position[0];
+    if (pos >= 0 && pos < limit) {
+      tokens[pos] = i0;
+      position[0] = pos + 1;
+    }
+    token[0] = i0;
+  }
+  __syncthreads();
+  const int tok = chosen;
+  for (int b = t; b * 8 < hidden; b += 1024)
+    *reinterpret_cast<h8 *>(h + b * 8) = *reinterpret_cast<const h8 *>(embedding + (size_t)tok * hidden + b * 8);
+}
+
+}  // namespace lb

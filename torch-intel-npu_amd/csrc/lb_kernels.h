@@ -34,12 +34,6 @@ struct GemvBatch {
   h2 s[kGemvBatch];
 };
 
-// Raw buffer resource over [base, base + bytes): loads at or beyond `bytes` return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, size_t bytes) {
-  const int records = bytes > 0x7FFFFFF0ull ? 0x7FFFFFF0 : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, records, 0x00020000);
-}
-
 // Decode-regime GEMV.  The waves of a workgroup form RG row groups x KG k groups:
 // wave (rg, kg) owns weight rows n0 + 16 rg .. +15 (the MFMA N dimension) and every KG-th
 // k-step of the workgroup's K range; lane (j, g) streams row n0 + 16 rg + j at

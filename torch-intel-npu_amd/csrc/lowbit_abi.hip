@@ -8,49 +8,13 @@
 #include <string>
 
 #include "../../include/lowbit_hip.h"
+#include "abi_util.h"
 #include "lb_kernels.h"
 
 using namespace lb;
+using namespace lb::abi;
 
 namespace {
-
-thread_local std::string g_last_error;
-
-lb_status fail(lb_status status, const char *fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return status;
-}
-
-lb_status ok() {
-  g_last_error.clear();
-  return LB_OK;
-}
-
-bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
-struct Range {
-  uintptr_t lo = 0, hi = 0;  // [lo, hi)
-  const char *name = "";
-};
-
-Range range_of(const void *p, size_t bytes, const char *name) {
-  Range r;
-  r.lo = reinterpret_cast<uintptr_t>(p);
-  r.hi = r.lo + bytes;
-  r.name = name;
-  return r;
-}
-
-bool overlaps(const Range &a, const Range &b) {
-  return a.lo != a.hi && b.lo != b.hi && a.lo < b.hi && b.lo < a.hi;
-}
-
-size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2 };
 
@@ -364,7 +328,7 @@ const char *lb_status_name(lb_status status) {
   return "LB_UNKNOWN_STATUS";
 }
 
-const char *lb_last_error(void) { return g_last_error.c_str(); }
+const char *lb_last_error(void) { return last_error().c_str(); }
 
 lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes) {
   if (!bytes) return fail(LB_INVALID_ARGUMENT, "lb_workspace_bytes: bytes is NULL");

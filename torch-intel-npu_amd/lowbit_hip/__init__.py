@@ -22,6 +22,9 @@ FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC = 0x1, 0x2, 0x4
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_workspace_bytes', 'lb_linear',
            'lb_unpack_codes', 'lb_dequantize')
+DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
+PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
+MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
 
 
 class LinearArgs(ctypes.Structure):
@@ -37,6 +40,35 @@ class LinearArgs(ctypes.Structure):
                 ('up_ld', ctypes.c_int64),
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t),
                 ('flags', ctypes.c_uint32), ('reserved', ctypes.c_uint32)]
+
+
+class FusedProblem(ctypes.Structure):
+    """Mirror of lb_fused_problem (include/lowbit_decode_hip.h)."""
+    _fields_ = [('codes', ctypes.c_void_p), ('scales', ctypes.c_void_p), ('N', ctypes.c_int64),
+                ('y', ctypes.c_void_p), ('bias', ctypes.c_void_p), ('residual', ctypes.c_void_p),
+                ('rank', ctypes.c_int64), ('down', ctypes.c_void_p), ('up', ctypes.c_void_p),
+                ('up_ld', ctypes.c_int64)]
+
+
+class FusedLinearArgs(ctypes.Structure):
+    """Mirror of lb_fused_linear_args."""
+    _fields_ = [('struct_size', ctypes.c_uint32), ('format', ctypes.c_uint32),
+                ('K', ctypes.c_int64), ('group_size', ctypes.c_int64),
+                ('prologue', ctypes.c_uint32), ('count', ctypes.c_uint32),
+                ('x', ctypes.c_void_p), ('x2', ctypes.c_void_p), ('gamma', ctypes.c_void_p),
+                ('eps', ctypes.c_float), ('reserved', ctypes.c_uint32),
+                ('problems', FusedProblem * 3)]
+
+
+class DecodeAttentionArgs(ctypes.Structure):
+    """Mirror of lb_decode_attention_args."""
+    _fields_ = [('struct_size', ctypes.c_uint32), ('reserved', ctypes.c_uint32),
+                ('heads', ctypes.c_int64), ('kv_heads', ctypes.c_int64), ('head_dim', ctypes.c_int64),
+                ('capacity', ctypes.c_int64),
+                ('q', ctypes.c_void_p), ('k', ctypes.c_void_p), ('v', ctypes.c_void_p),
+                ('cos', ctypes.c_void_p), ('sin', ctypes.c_void_p), ('position', ctypes.c_void_p),
+                ('keys', ctypes.c_void_p), ('values', ctypes.c_void_p), ('out', ctypes.c_void_p),
+                ('scale', ctypes.c_float), ('reserved2', ctypes.c_uint32)]
 
 
 _lib = None
@@ -64,6 +96,14 @@ def library():
         lib.lb_dequantize.restype = ctypes.c_int
         lib.lb_dequantize.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.lb_fused_linear.restype = ctypes.c_int
+        lib.lb_fused_linear.argtypes = [ctypes.POINTER(FusedLinearArgs), ctypes.c_void_p]
+        lib.lb_decode_attention.restype = ctypes.c_int
+        lib.lb_decode_attention.argtypes = [ctypes.POINTER(DecodeAttentionArgs), ctypes.c_void_p]
+        lib.lb_argmax_next.restype = ctypes.c_int
+        lib.lb_argmax_next.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_void_p]
         if lib.lb_abi_version() != ABI_VERSION:
             raise RuntimeError(f'liblowbit_hip ABI {lib.lb_abi_version()} != expected {ABI_VERSION}')
         _lib = lib
@@ -209,3 +249,128 @@ class PreparedLinear:
         if status != OK:
             _check(status, 'lb_linear')
         return self.out
+
+
+# ---------------------------------------------------------------- decode-step entry points
+def _row(t, name, count, dtype=torch.float16):
+    """A contiguous device row of at least `count` elements (views into larger buffers are fine)."""
+    _device_tensor(t, name, dtype)
+    if not t.is_contiguous() or t.numel() < count:
+        raise ValueError(f'{name} must be contiguous with at least {count} elements')
+    return t
+
+
+class _Prepared:
+    """A fixed call of one decode-step entry point; run() enqueues it on the current stream."""
+
+    def _bind(self, fn, what, args, device, keep):
+        self.args, self._keep, self._device, self._what = args, keep, device, what
+        self._fn = getattr(library(), fn)
+        self._ref = ctypes.byref(args)
+
+    def run(self, stream=None):
+        handle = torch.cuda.current_stream(self._device).cuda_stream if stream is None else stream
+        status = self._fn(self._ref, ctypes.c_void_p(handle))
+        if status != OK:
+            _check(status, self._what)
+
+
+class PreparedFused(_Prepared):
+    """One lb_fused_linear call: up to three linears sharing the activation row `x` (K fp16).
+
+    problems: sequence of dicts with keys codes, scales (None for fp16), N, y (fp16 row of N),
+    and optionally bias, residual (may be y itself), down [rank,K], up [N,rank] (rank = down rows).
+    prologue: 'none', 'rmsnorm' (gamma, eps) or 'silu_mul' (x = gate row, x2 = up row).
+    """
+
+    def __init__(self, x, problems, *, format, K, group_size, prologue='none', x2=None, gamma=None, eps=1e-5):
+        if prologue not in PROLOGUES:
+            raise ValueError(f'unknown prologue {prologue!r}')
+        if not 1 <= len(problems) <= MAX_PROBLEMS:
+            raise ValueError(f'1..{MAX_PROBLEMS} problems per fused call')
+        a = FusedLinearArgs()
+        a.struct_size = ctypes.sizeof(FusedLinearArgs)
+        a.format = FORMATS[format]
+        a.K, a.group_size = K, group_size
+        a.prologue, a.count = PROLOGUES[prologue], len(problems)
+        keep = [_row(x, 'x', K)]
+        a.x = _ptr(x)
+        if prologue == 'silu_mul':
+            keep.append(_row(x2, 'x2', K))
+            a.x2 = _ptr(x2)
+        if prologue == 'rmsnorm':
+            keep.append(_row(gamma, 'gamma', K))
+            a.gamma = _ptr(gamma)
+        a.eps = eps
+        for i, pr in enumerate(problems):
+            q = a.problems[i]
+            n = pr['N']
+            q.N = n
+            q.codes = _ptr(pr['codes'])
+            q.scales = _ptr(pr.get('scales'))
+            q.y = _ptr(_row(pr['y'], 'y', n))
+            q.bias = _ptr(pr.get('bias'))
+            q.residual = _ptr(pr.get('residual'))
+            down, up = pr.get('down'), pr.get('up')
+            if down is not None:
+                q.rank = down.shape[0]
+                q.down, q.up, q.up_ld = _ptr(down.contiguous()), _ptr(up), up.stride(0)
+                keep += [down, up]
+            keep += [pr['codes'], pr.get('scales'), pr['y'], pr.get('bias'), pr.get('residual')]
+        self._bind('lb_fused_linear', 'lb_fused_linear', a, x.device, keep)
+        self.outputs = [pr['y'] for pr in problems]
+
+
+def fused_linear(x, problems, **options):
+    """Run one lb_fused_linear on the current stream; returns the problems' y tensors."""
+    call = PreparedFused(x, problems, **options)
+    call.run()
+    return call.outputs
+
+
+class PreparedAttention(_Prepared):
+    """lb_decode_attention for one token: q [heads*64], k, v [kv_heads*64], position int64 [1]."""
+
+    def __init__(self, q, k, v, cos, sin, position, keys, values, out, *, heads, kv_heads, scale=0.125):
+        capacity = keys.shape[-2]
+        a = DecodeAttentionArgs()
+        a.struct_size = ctypes.sizeof(DecodeAttentionArgs)
+        a.heads, a.kv_heads, a.head_dim, a.capacity = heads, kv_heads, 64, capacity
+        rows = ((q, 'q', heads * 64), (k, 'k', kv_heads * 64), (v, 'v', kv_heads * 64),
+                (cos, 'cos', capacity * 64), (sin, 'sin', capacity * 64), (keys, 'keys', kv_heads * capacity * 64),
+                (values, 'values', kv_heads * capacity * 64), (out, 'out', heads * 64))
+        for t, name, count in rows:
+            _row(t, name, count)
+        _row(position, 'position', 1, torch.int64)
+        a.q, a.k, a.v, a.cos, a.sin = _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin)
+        a.position, a.keys, a.values, a.out = _ptr(position), _ptr(keys), _ptr(values), _ptr(out)
+        a.scale = scale
+        self._bind('lb_decode_attention', 'lb_decode_attention', a, q.device,
+                   [q, k, v, cos, sin, position, keys, values, out])
+        self.out = out
+
+
+class PreparedArgmax:
+    """lb_argmax_next: greedy token of `logits`, recorded at tokens[position], position += 1,
+    h_next = embedding[token]."""
+
+    def __init__(self, logits, embedding, h_next, tokens, token, position, *, limit):
+        vocab, hidden = embedding.shape
+        _row(logits, 'logits', vocab)
+        _row(embedding, 'embedding', vocab * hidden)
+        _row(h_next, 'h_next', hidden)
+        for t, name in ((tokens, 'tokens'), (token, 'token'), (position, 'position')):
+            _row(t, name, 1, torch.int64)
+        if tokens.numel() < limit:
+            raise ValueError('tokens must hold `limit` entries')
+        self._keep = [logits, embedding, h_next, tokens, token, position]
+        self._call = (_ptr(logits), vocab, _ptr(embedding), hidden, _ptr(h_next), _ptr(tokens), _ptr(token),
+                      _ptr(position), limit)
+        self._fn = library().lb_argmax_next
+        self._device = logits.device
+
+    def run(self, stream=None):
+        handle = torch.cuda.current_stream(self._device).cuda_stream if stream is None else stream
+        status = self._fn(*self._call, ctypes.c_void_p(handle))
+        if status != OK:
+            _check(status, 'lb_argmax_next')

@@ -544,21 +544,29 @@ class GraphDecoder:
     """Greedy decode of one sequence (B=1) as a replayable HIP graph.
 
     The per-token work of FrozenSmolStack.decode plus FrozenSmolIO.logits and the argmax is
-    captured once: activations live in static buffers, every projection is a
-    PreparedLinear bound to them, and the position is a device tensor (RoPE rows are
-    gathered by it, K/V rows are written at it, and attention runs over the whole capacity
-    with positions > p masked to -inf, which contributes exact zeros).  One replay embeds
-    the current token, runs every layer, writes the greedy next token and advances the
-    position, so generation needs no host synchronization.  Staging matches
-    FrozenSmolLayer.decode (reference torch_npu_smollm.py:142-193).
+    captured once; activations live in static buffers and the position is a device tensor,
+    so generation needs no host synchronization.  Staging matches FrozenSmolLayer.decode
+    (reference torch_npu_smollm.py:142-193).
+
+    fused=True (default) issues five launches per layer from liblowbit_hip's decode-step
+    entry points, the GPU counterpart of the reference's one-graph-per-layer decode
+    (:195-340, chained per fence at :644-654):
+      1. RMSNorm -> q | k | v projections (+ corrections)          lb_fused_linear
+      2. RoPE, KV append at the position, GQA attention            lb_decode_attention
+      3. o projection (+ correction) + residual                     lb_fused_linear
+      4. RMSNorm -> gate | up projections (+ corrections)           lb_fused_linear
+      5. SiLU(gate) * up -> down projection (+ correction) + residual  lb_fused_linear
+    then RMSNorm -> tied fp16 lm_head (lb_fused_linear) and the greedy token with the next
+    embedding (lb_argmax_next).  Projections of different formats (fp16-protected ones)
+    get separate launches.  fused=False runs the same step as staged PyTorch-ROCm glue
+    around one lb_linear per projection.
     """
 
-    def __init__(self, stack, io):
-        import lowbit_hip as lb
+    def __init__(self, stack, io, *, fused=True):
         self.device = io.embedding.device
         if self.device.type != 'cuda':
             raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
-        self.stack, self.io = stack, io
+        self.stack, self.io, self.fused = stack, io, fused
         dev = self.device
         cap = stack.layers[0].capacity
         self.capacity = cap
@@ -566,16 +574,91 @@ class GraphDecoder:
         self.pos = z(1, dtype=torch.int64)
         self.token = z(1, dtype=torch.int64)
         self.tokens = z(cap + 1, dtype=torch.int64)
+        self.logits = z(1, io.vocab_size)
+        self.keys = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
+        self.values = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
+        self.states = [layer._dev(dev) for layer in stack.layers]
+        if fused:
+            self._build_fused(z)
+        else:
+            self._build_staged(z)
+        self.graph = None
+
+    # ---------------------------------------------------------------- fused launches
+    @staticmethod
+    def _problem(entry, y, **extra):
+        problem = dict(codes=entry['codes'], scales=entry['scales'], N=entry['N'], y=y, **extra)
+        if entry.get('rank', 0):
+            down, up = entry['down'], entry['up']
+            rank = down.shape[0]
+            if rank % 8:  # the fused kernel reads U rows in 8-wide pieces: pad columns with zeros
+                padded = torch.zeros((up.shape[0], (rank + 7) // 8 * 8), dtype=up.dtype, device=up.device)
+                padded[:, :rank] = up
+                up = padded
+            problem.update(down=down, up=up)
+        return problem
+
+    def _fused_group(self, lin, members, x, **options):
+        """One lb_fused_linear per run of same-format projections in `members` [(name, y, extra)]."""
+        import lowbit_hip as lb
+        calls, run = [], []
+
+        def flush():
+            if run:
+                first = lin[run[0][0]]
+                calls.append(lb.PreparedFused(x, [self._problem(lin[name], y, **extra) for name, y, extra in run],
+                                              format=first['format'], K=first['K'], group_size=first['group'],
+                                              **options))
+                run.clear()
+
+        for member in members:
+            e = lin[member[0]]
+            if run and (lin[run[0][0]]['format'], lin[run[0][0]]['group']) != (e['format'], e['group']):
+                flush()
+            run.append(member)
+        flush()
+        return calls
+
+    def _build_fused(self, z):
+        import lowbit_hip as lb
+        io = self.io
+        self.h = z(HIDDEN)
+        self.qkv = z(HIDDEN + 2 * KV_HEADS * HEAD_DIM)
+        self.att = z(HIDDEN)
+        self.gu = z(2 * 1536)
+        q, k, v = self.qkv[:HIDDEN], self.qkv[HIDDEN:HIDDEN + 192], self.qkv[HIDDEN + 192:]
+        gate, up = self.gu[:1536], self.gu[1536:]
+        self.calls = []
+        for state, keys, values in zip(self.states, self.keys, self.values):
+            lin = state['lin']
+            seq = self._fused_group(lin, [('self_attn.q_proj.weight', q, {}), ('self_attn.k_proj.weight', k, {}),
+                                          ('self_attn.v_proj.weight', v, {})],
+                                    self.h, prologue='rmsnorm', gamma=state['norm1'], eps=1e-5)
+            seq.append(lb.PreparedAttention(q, k, v, state['cos'], state['sin'], self.pos, keys, values, self.att,
+                                            heads=HEADS, kv_heads=KV_HEADS, scale=0.125))
+            seq += self._fused_group(lin, [('self_attn.o_proj.weight', self.h, dict(residual=self.h))], self.att)
+            seq += self._fused_group(lin, [('mlp.gate_proj.weight', gate, {}), ('mlp.up_proj.weight', up, {})],
+                                     self.h, prologue='rmsnorm', gamma=state['norm2'], eps=1e-5)
+            seq += self._fused_group(lin, [('mlp.down_proj.weight', self.h, dict(residual=self.h))], gate,
+                                     prologue='silu_mul', x2=up)
+            self.calls.append(seq)
+        self.head = lb.PreparedFused(self.h, [dict(codes=io.embedding, scales=None, N=io.vocab_size, y=self.logits)],
+                                     format='fp16', K=HIDDEN, group_size=HIDDEN, prologue='rmsnorm', gamma=io.norm,
+                                     eps=1e-5)
+        self.argmax = lb.PreparedArgmax(self.logits, io.embedding, self.h, self.tokens, self.token, self.pos,
+                                        limit=self.capacity)
+
+    # ---------------------------------------------------------------- staged launches
+    def _build_staged(self, z):
+        import lowbit_hip as lb
+        io = self.io
+        cap = self.capacity
         self.h = z(1, HIDDEN)
         self.n1, self.att, self.o, self.n2, self.down = (z(1, HIDDEN) for _ in range(5))
         self.q, self.k, self.v = z(1, 576), z(1, 192), z(1, 192)
         self.gate, self.up, self.hidden = z(1, 1536), z(1, 1536), z(1, 1536)
         self.normed = z(1, HIDDEN)
-        self.logits = z(1, io.vocab_size)
-        self.slots = torch.arange(cap, device=dev)
-        self.keys = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
-        self.values = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
-        self.states = [layer._dev(dev) for layer in stack.layers]
+        self.slots = torch.arange(cap, device=self.device)
         plan = (('self_attn.q_proj.weight', 'n1', 'q'), ('self_attn.k_proj.weight', 'n1', 'k'),
                 ('self_attn.v_proj.weight', 'n1', 'v'), ('self_attn.o_proj.weight', 'att', 'o'),
                 ('mlp.gate_proj.weight', 'n2', 'gate'), ('mlp.up_proj.weight', 'n2', 'up'),
@@ -591,24 +674,13 @@ class GraphDecoder:
             self.calls.append(calls)
         self.head = lb.PreparedLinear(self.normed, io.embedding, None, format='fp16', N=io.vocab_size, K=HIDDEN,
                                       group_size=HIDDEN, out=self.logits)
-        self.graph = None
-
-    def load(self, caches, next_token):
-        """Start from a prefill snapshot: copy its K/V, set the position and the next input token."""
-        length = caches[0].length
-        for dst_k, dst_v, cache in zip(self.keys, self.values, caches):
-            dst_k[:, :, :length].copy_(cache.keys[:, :, :length])
-            dst_v[:, :, :length].copy_(cache.values[:, :, :length])
-        self.pos.fill_(length)
-        self.token.fill_(int(next_token))
 
     @staticmethod
     def _norm_into(out, x, gamma):
         f = x.float()
         torch.mul((f * torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)).half(), gamma, out=out)
 
-    def step(self):
-        """One greedy token (eager; this is what capture() records)."""
+    def _step_staged(self):
         torch.index_select(self.io.embedding, 0, self.token, out=self.h)
         mask = torch.where(self.slots > self.pos, float('-inf'), 0.0)
         for layer_index, (state, calls) in enumerate(zip(self.states, self.calls)):
@@ -641,11 +713,32 @@ class GraphDecoder:
         self.token.copy_(nxt)
         self.pos.add_(1)
 
+    # ---------------------------------------------------------------- common
+    def load(self, caches, next_token):
+        """Start from a prefill snapshot: copy its K/V, set the position and the next input token."""
+        length = caches[0].length
+        if not 1 <= length < self.capacity:
+            raise ValueError('the snapshot leaves no free KV slot')
+        for dst_k, dst_v, cache in zip(self.keys, self.values, caches):
+            dst_k[:, :, :length].copy_(cache.keys[:, :, :length])
+            dst_v[:, :, :length].copy_(cache.values[:, :, :length])
+        self.pos.fill_(length)
+        self.token.fill_(int(next_token))
+        self.h.view(1, HIDDEN).copy_(self.io.embedding[int(next_token)].view(1, HIDDEN))
+
+    def step(self):
+        """One greedy token (eager; this is what capture() records)."""
+        if not self.fused:
+            return self._step_staged()
+        for seq in self.calls:
+            for call in seq:
+                call.run()
+        self.head.run()
+        self.argmax.run()
+
     def capture(self):
         """Record step() into a HIP graph (warm-up runs first on a side stream, as torch requires)."""
-        pos, token = self.pos.clone(), self.token.clone()
-        keys = [k.clone() for k in self.keys]
-        values = [v.clone() for v in self.values]
+        saved = [t.clone() for t in [self.pos, self.token, self.h] + self.keys + self.values]
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
@@ -654,10 +747,8 @@ class GraphDecoder:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.step()
-        self.pos.copy_(pos)  # the warm-up and capture advanced state; restore it
-        self.token.copy_(token)
-        for dst, src in zip(self.keys + self.values, keys + values):
-            dst.copy_(src)
+        for dst, src in zip([self.pos, self.token, self.h] + self.keys + self.values, saved):
+            dst.copy_(src)  # the warm-up advanced the state; restore it
         return self.graph
 
     def generate(self, steps):
@@ -665,6 +756,8 @@ class GraphDecoder:
         if self.graph is None:
             self.capture()
         start = int(self.pos.item())
+        if start + steps > self.capacity:
+            raise ValueError(f'{steps} steps from position {start} exceed the KV capacity {self.capacity}')
         for _ in range(steps):
             self.graph.replay()
         return self.tokens[start:start + steps].tolist()

@@ -97,12 +97,18 @@ lb_status check_fused(const lb_fused_linear_args *a) {
   return ok();
 }
 
-template <int FMT, bool SCALED>
-void launch_fused_t(const FusedParams &p, int tiles, hipStream_t s) {
+template <int FMT, bool SCALED, bool RANKED>
+void launch_fused_r(const FusedParams &p, int tiles, hipStream_t s) {
   if (p.K <= 640)
-    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, 640>), dim3(tiles), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, 640, RANKED>), dim3(tiles), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, LB_FUSED_MAX_K>), dim3(tiles), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, LB_FUSED_MAX_K, RANKED>), dim3(tiles), dim3(256), 0, s, p);
+}
+
+// RANKED instantiations carry the correction (V and U loads); the others have none at all.
+template <int FMT, bool SCALED>
+void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
+  ranked ? launch_fused_r<FMT, SCALED, true>(p, tiles, s) : launch_fused_r<FMT, SCALED, false>(p, tiles, s);
 }
 
 lb_status launch_status(const char *what) {
@@ -151,13 +157,15 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool scaled = !dense && !p.per_row;
+  bool ranked = false;
+  for (uint32_t i = 0; i < a->count; ++i) ranked = ranked || a->problems[i].rank > 0;
   switch (a->format) {
     case LB_FORMAT_INT8:
-      scaled ? launch_fused_t<FMT_INT8, true>(p, tiles, s) : launch_fused_t<FMT_INT8, false>(p, tiles, s);
+      scaled ? launch_fused_t<FMT_INT8, true>(p, tiles, ranked, s) : launch_fused_t<FMT_INT8, false>(p, tiles, ranked, s);
       break;
-    case LB_FORMAT_INT4: launch_fused_t<FMT_INT4, true>(p, tiles, s); break;
-    case LB_FORMAT_NF4: launch_fused_t<FMT_NF4, true>(p, tiles, s); break;
-    default: launch_fused_t<FMT_FP16, false>(p, tiles, s); break;
+    case LB_FORMAT_INT4: launch_fused_t<FMT_INT4, true>(p, tiles, ranked, s); break;
+    case LB_FORMAT_NF4: launch_fused_t<FMT_NF4, true>(p, tiles, ranked, s); break;
+    default: launch_fused_t<FMT_FP16, false>(p, tiles, ranked, s); break;
   }
   return launch_status("lb_fused_linear");
 }

@@ -73,7 +73,12 @@ __device__ __forceinline__ f16 rope_element(float x, float r, float c, float s) 
 // One workgroup = 4 waves = one 16-row tile of one problem; the waves split K (wave w takes
 // k-steps w, w + 4, ...) and are reduced through LDS.  K <= KMAX, so every lane issues all
 // of its weight loads (D of them) up front and the activation row is staged once.
-template <int FMT, bool SCALED, int KMAX>
+//
+// Every global load is issued, straight-line, before the first wait: the epilogue operands
+// (one load per wave), the prologue row, the activation, the scales, V (RANKED only) and the
+// weights.  Lanes without data read out of range (zeros).  There are no branches around loads:
+// a load under a branch makes the compiler wait for it at the branch's end.
+template <int FMT, bool SCALED, int KMAX, bool RANKED>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
@@ -83,11 +88,14 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   constexpr int D = (KMAX + WSTEP - 1) / WSTEP;  // weight loads per lane
   constexpr int T8 = CPL / 8;
   constexpr int XLD = KMAX + KSTEP + 8;           // staged row, zero beyond K
-  constexpr int VB = KMAX / 64;                   // 16-byte V loads per thread (8 threads per rank row)
+  constexpr int VB = RANKED ? KMAX / 64 : 0;      // 16-byte V loads per thread (8 threads per rank row)
   constexpr int GMAX = KMAX / 32;                 // groups per row (group >= 32)
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;  // staged scales per thread
+  constexpr int kOutOfRange = (int)0x80000000u;
   __shared__ __align__(16) f16 xs[2 * XLD];       // row 0: the activation, row 1: zeros
   __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
+  __shared__ __align__(16) f16 us[RANKED ? 16 * kFusedMaxRank : 8];  // U rows of the tile
+  __shared__ f16 es[3 * 16];                      // residual, bias, per-row scale of the tile
   __shared__ float zs[kFusedMaxRank];
   __shared__ float red[(KG - 1) * 16];
   __shared__ float wsum[4];
@@ -109,50 +117,47 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   const int n0 = (bid - first) * 16;
   const int rows = min(16, P.N - n0);
   const int row_bytes = K * BITS / 8;
-  constexpr int kOutOfRange = (int)0x80000000u;
+  const int rank = RANKED ? P.rank : 0;
 
-  // ---- issue every global load: activation, scales, V, epilogue operands, then weights ----
-  const int blocks = K >> 3;
-  h8 xv = {}, x2v = {}, gv = {};
-  if (t < blocks) {
-    xv = *reinterpret_cast<const h8 *>(p.x + t * 8);
-    if (p.prologue == PRO_SILU_MUL) x2v = *reinterpret_cast<const h8 *>(p.x2 + t * 8);
-    if (p.prologue == PRO_RMSNORM) gv = *reinterpret_cast<const h8 *>(p.gamma + t * 8);
+  // Epilogue operands: wave 0 fetches the residual, wave 1 the bias, wave 2 the per-row
+  // scale of the tile's 16 rows (lanes 0..15); absent operands have an empty buffer.
+  const f16 *ep = wave == 0 ? P.residual : (wave == 1 ? P.bias : (wave == 2 ? P.scales : nullptr));
+  const bool ep_on = wave == 0 ? P.residual != nullptr : (wave == 1 ? P.bias != nullptr : (wave == 2 && p.per_row));
+  const f16 ev = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(ep, ep_on ? (size_t)P.N * 2 : 0),
+                                                lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
+  // U rows of the tile: wave w, lane l < 16 fetches row 4w + l / 4, halves 8 (l % 4) .. + 7.
+  u4 ureg = {0u, 0u, 0u, 0u};
+  if constexpr (RANKED) {
+    const int ur = 4 * wave + (lane >> 2), uq = lane & 3;
+    const int off = lane < 16 && ur < rows && uq * 8 < rank ? ((n0 + ur) * P.up_ld + uq * 8) * 2 : kOutOfRange;
+    ureg = __builtin_bit_cast(
+        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(P.up, rank > 0 ? (size_t)P.N * P.up_ld * 2 : 0), off, 0, 0));
   }
+  // Activation row (and the second row of the prologue: gamma or the up row).
+  const int blocks = K >> 3;
+  const int xoff = t < blocks ? t * 16 : kOutOfRange;
+  const size_t kb = (size_t)K * 2;
+  const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
+  const h8 av = __builtin_bit_cast(
+      h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb), xoff, 0, 0));
+  const h8 xv = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x, kb), xoff, 0, 0));
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
-    const int valid = rows * p.G;
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)n0 * p.G, (size_t)rows * p.G * 2);
 #pragma unroll
-    for (int i = 0; i < SC; ++i) {
-      const int idx = t + i * 256;
-      sreg[i] = idx < valid ? P.scales[(size_t)n0 * p.G + idx] : (f16)0.0f;
-    }
+    for (int i = 0; i < SC; ++i)
+      sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
   }
-  const int rank = P.rank;
-  u4 vreg[VB];
   const int vr = t >> 3, vpart = t & 7;
-  if (rank > 0) {
+  u4 vreg[VB > 0 ? VB : 1];
+  if constexpr (RANKED) {
     const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(P.down, (size_t)rank * K * 2);
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const int k = (vpart + 8 * i) * 8;
       const int off = (vr < rank && k < K) ? (vr * K + k) * 2 : kOutOfRange;
       vreg[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
-    }
-  }
-  // Epilogue operands of lane (j, g == 0) of wave 0: row n0 + j.
-  const bool writer = wave == 0 && g == 0 && j < rows;
-  const int n = n0 + j;
-  u4 ureg[kFusedMaxRank / 8];
-  f16 res = (f16)0.0f, bia = (f16)0.0f, rsc = (f16)1.0f;
-  if (writer) {
-    if (P.residual) res = P.residual[n];
-    if (P.bias) bia = P.bias[n];
-    if (p.per_row) rsc = P.scales[n];
-    if (rank > 0) {
-#pragma unroll
-      for (int q = 0; q < kFusedMaxRank / 8; ++q)
-        ureg[q] = q * 8 < rank ? *reinterpret_cast<const u4 *>(P.up + (size_t)n * P.up_ld + q * 8) : u4{};
     }
   }
   const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(P.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
@@ -163,9 +168,14 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
     const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
     w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
 
   // ---- prologue: stage the activation row (fp16, in the format's slot order) ----
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  if (lane < 16 && wave < 3) es[wave * 16 + lane] = ev;
+  if constexpr (RANKED) {
+    if (lane < 16) *reinterpret_cast<u4 *>(us + (4 * wave + (lane >> 2)) * kFusedMaxRank + (lane & 3) * 8) = ureg;
+  }
   float inv = 1.0f;
   if (p.prologue == PRO_RMSNORM) {
     float s = 0.0f;
@@ -179,14 +189,14 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   }
   if (t < blocks) {
     h8 v;
+    if (p.prologue == PRO_RMSNORM) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (p.prologue == PRO_RMSNORM)
-        v[e] = (f16)((float)(f16)((float)xv[e] * inv) * (float)gv[e]);
-      else if (p.prologue == PRO_SILU_MUL)
-        v[e] = (f16)((float)(f16)silu((float)xv[e]) * (float)x2v[e]);
-      else
-        v[e] = xv[e];
+      for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[e] * inv) * (float)av[e]);
+    } else if (p.prologue == PRO_SILU_MUL) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[e]) * (float)av[e]);
+    } else {
+      v = xv;
     }
     *reinterpret_cast<h8 *>(xs + t * 8) = permute_block<FMT>(v);
   }
@@ -201,19 +211,24 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   __syncthreads();
 
   // ---- correction activations z = fp16(x . V^T), 8 threads per rank row ----
-  if (rank > 0) {
-    float acc = 0.0f;
+  if constexpr (RANKED) {
+    float acc = 0.0f, acc2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
+      asm volatile("" : "+v"(vreg[i]));  // V is consumed here, after the barrier, not at its load
       const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
       const h8 xx = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)xx[e] * (float)vv[e];
+      for (int e = 0; e < 8; e += 2) {
+        acc += (float)xx[e] * (float)vv[e];
+        acc2 += (float)xx[e + 1] * (float)vv[e + 1];
+      }
     }
+    acc += acc2;
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
     acc += __shfl_xor(acc, 4, 64);
-    if (vpart == 0 && vr < kFusedMaxRank) zs[vr] = (float)(f16)acc;
+    if (vpart == 0) zs[vr] = (float)(f16)acc;
   }
 
   // ---- the product on MFMA: A = activation row (row 0) or zeros, B = decoded weights ----
@@ -223,6 +238,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
     if (kb >= K) break;  // wave-uniform
+    asm volatile("" : "+v"(w[u]));  // decode here, not at the load
     h2 s2 = {(f16)1.0f, (f16)1.0f};
     if constexpr (SCALED) {
       const f16 sc = ss[j * p.G + ((kb + g * CPL) >> p.group_shift)];
@@ -238,26 +254,21 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   // Lane (j, g) holds D rows 4g..4g+3 of column j; the activation is row 0 (g == 0, r == 0).
   if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
   __syncthreads();
+  const bool writer = wave == 0 && g == 0 && j < rows;
   if (!writer) return;
   float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
 
   // ---- epilogue (reference torch_npu_lowbit.py:262-266, torch_npu_smollm.py:160-163) ----
-  if (p.per_row) sum *= (float)rsc;
+  if (p.per_row) sum *= (float)es[32 + j];
   f16 h = (f16)sum;
-  if (P.bias) h = (f16)((float)h + (float)bia);
-  if (rank > 0) {
+  if (P.bias) h = (f16)((float)h + (float)es[16 + j]);
+  if (RANKED && rank > 0) {
     float d = 0.0f;
-#pragma unroll
-    for (int q = 0; q < kFusedMaxRank / 8; ++q) {
-      const h8 uu = __builtin_bit_cast(h8, ureg[q]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (q * 8 + e < rank) d += zs[q * 8 + e] * (float)uu[e];
-    }
+    for (int r = 0; r < rank; ++r) d += zs[r] * (float)us[j * kFusedMaxRank + r];
     h = (f16)((float)h + (float)(f16)d);
   }
-  if (P.residual) h = (f16)((float)res + (float)h);
-  P.y[n] = h;
+  if (P.residual) h = (f16)((float)es[j] + (float)h);
+  P.y[n0 + j] = h;
 }
 
 struct AttnParams {
@@ -271,38 +282,82 @@ struct AttnParams {
 };
 
 constexpr int kHeadDim = 64;
-constexpr int kAttnParts = 32;  // position partitions of the P.V product
+constexpr int kAttnParts = 32;   // position partitions of the P.V product (8 threads per V row)
+constexpr int kScoreSlots = 2;   // K rows per thread per round: 512 slots per round
+constexpr int kValueSlots = 12;  // V rows per thread per round: 384 slots per round
 
 // One workgroup per query head.  The first query head of each KV group writes the rotated key
 // and the value into the cache; every workgroup uses its own copy of that new row, so no
-// workgroup reads a cache slot another one writes.
+// workgroup reads a cache slot another one writes.  The cached K and V rows of the first
+// round (slots < 512) are loaded before anything else, so a step costs one memory round trip
+// plus the on-chip softmax; longer caches loop over further rounds.
 __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   extern __shared__ float sc[];  // [capacity] scores, then probabilities
   __shared__ __align__(16) f16 qs[kHeadDim], kn[kHeadDim], vn[kHeadDim];
   __shared__ float wred[4];
   __shared__ float pv[kAttnParts * kHeadDim];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar: buffer bases below are per wave
   const int h = blockIdx.x;
   const int group = p.heads / p.kv_heads;
   const int kvh = h / group;
   const int pos = (int)p.position[0];
   if (pos < 0 || pos >= p.capacity) return;  // host guarantees; never index outside the cache
 
-  if (t < 3 * kHeadDim) {
-    const int which = t >> 6, d = t & 63;
-    const f16 *src = which == 0 ? p.q + h * kHeadDim : (which == 1 ? p.k : p.v) + kvh * kHeadDim;
-    if (which == 2) {
-      vn[d] = src[d];
-    } else {
-      const float c = (float)p.cos[(size_t)pos * kHeadDim + d];
-      const float s = (float)p.sin[(size_t)pos * kHeadDim + d];
-      const float rot = d < 32 ? -(float)src[d + 32] : (float)src[d - 32];
-      const f16 r = rope_element((float)src[d], rot, c, s);
-      if (which == 0) qs[d] = r; else kn[d] = r;
+  // The new rows first: wave 0 reads the query row of head h, wave 1 the key row and wave 2
+  // the value row of its KV head (element d and its rotate-half partner d ^ 32), waves 0 and 1
+  // the RoPE row pos.
+  const int d = lane;
+  const f16 *src = wave == 0 ? p.q + h * kHeadDim : (wave == 1 ? p.k : p.v) + kvh * kHeadDim;
+  const __amdgpu_buffer_rsrc_t rbuf = buffer_rsrc(src, wave < 3 ? kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t cbuf = buffer_rsrc(p.cos + (size_t)pos * kHeadDim, wave < 2 ? kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t snbuf = buffer_rsrc(p.sin + (size_t)pos * kHeadDim, wave < 2 ? kHeadDim * 2 : 0);
+  const f16 x0 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rbuf, d * 2, 0, 0));
+  const f16 x1 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rbuf, (d ^ 32) * 2, 0, 0));
+  const f16 cv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(cbuf, d * 2, 0, 0));
+  const f16 sv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(snbuf, d * 2, 0, 0));
+
+  // Cached rows live in slots [0, pos); the buffers end there, so later slots read zero.
+  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
+  const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(p.keys + head_base, (size_t)pos * kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(p.values + head_base, (size_t)pos * kHeadDim * 2);
+  const int blk = t & 7, part = t >> 3;
+  u4 kreg[kScoreSlots][kHeadDim / 8];
+  u4 vreg[kValueSlots];
+  // Straight-line loads (a load under a branch is waited for at the branch's end); lanes
+  // past the cached slots read out of range (zeros, no memory traffic).
+  auto load_keys = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < kScoreSlots; ++i) {
+      const int s = base + t + 256 * i;
+#pragma unroll
+      for (int b = 0; b < kHeadDim / 8; ++b)
+        kreg[i][b] = __builtin_bit_cast(
+            u4, __builtin_amdgcn_raw_buffer_load_b128(kbuf, s < pos ? (s * kHeadDim + 8 * b) * 2 : kOutOfRange, 0, 0));
     }
+  };
+  auto load_values = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      vreg[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, s < pos ? (s * kHeadDim + 8 * blk) * 2 : kOutOfRange, 0, 0));
+    }
+  };
+  load_keys(0);
+  load_values(0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // RoPE of q and k at row pos (three fp16 roundings); v as given.
+  if (wave == 2) {
+    vn[d] = x0;
+  } else if (wave < 2) {
+    const float rot = d < 32 ? -(float)x1 : (float)x1;
+    const f16 r = rope_element((float)x0, rot, (float)cv, (float)sv);
+    if (wave == 0) qs[d] = r; else kn[d] = r;
   }
   __syncthreads();
-  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
   if (h % group == 0 && t < 2 * kHeadDim) {
     const int d = t & 63;
     f16 *dst = (t < kHeadDim ? p.keys : p.values) + head_base + (size_t)pos * kHeadDim + d;
@@ -311,19 +366,30 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
 
   // scores = fp16(fp16(q . k) * scale) over slots 0..pos
   float lmax = -INFINITY;
-  for (int s = t; s <= pos; s += 256) {
-    float acc = 0.0f;
+  for (int base = 0; base <= pos; base += 256 * kScoreSlots) {
+    if (base > 0) load_keys(base);
 #pragma unroll
-    for (int b = 0; b < kHeadDim / 8; ++b) {
-      const h8 qq = *reinterpret_cast<const h8 *>(qs + 8 * b);
-      const h8 kk = s < pos ? *reinterpret_cast<const h8 *>(p.keys + head_base + (size_t)s * kHeadDim + 8 * b)
-                            : *reinterpret_cast<const h8 *>(kn + 8 * b);
+    for (int i = 0; i < kScoreSlots; ++i) {
+      const int s = base + t + 256 * i;
+      if (base + 256 * i > pos) break;  // wave-uniform
+      float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)qq[e] * (float)kk[e];
+      for (int b = 0; b < kHeadDim / 8; ++b) {
+        asm volatile("" : "+v"(kreg[i][b]));  // consumed here, not at the load
+        const h8 qq = *reinterpret_cast<const h8 *>(qs + 8 * b);
+        const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * b) : __builtin_bit_cast(h8, kreg[i][b]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          acc0 += (float)qq[e] * (float)kk[e];
+          acc1 += (float)qq[e + 1] * (float)kk[e + 1];
+        }
+      }
+      if (s <= pos) {
+        const float v = (float)(f16)((float)(f16)(acc0 + acc1) * p.scale);
+        sc[s] = v;
+        lmax = fmaxf(lmax, v);
+      }
     }
-    const float v = (float)(f16)((float)(f16)acc * p.scale);
-    sc[s] = v;
-    lmax = fmaxf(lmax, v);
   }
   lmax = wave_max(lmax);
   if (lane == 0) wred[wave] = lmax;
@@ -344,14 +410,19 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   __syncthreads();
 
   // out = fp16(P . V): thread (blk, part) sums 8 dims over slots part, part + 32, ...
-  const int blk = t & 7, part = t >> 3;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = part; s <= pos; s += kAttnParts) {
-    const float pr = sc[s];
-    const h8 vv = s < pos ? *reinterpret_cast<const h8 *>(p.values + head_base + (size_t)s * kHeadDim + 8 * blk)
-                          : *reinterpret_cast<const h8 *>(vn + 8 * blk);
+  for (int base = 0; base <= pos; base += kAttnParts * kValueSlots) {
+    if (base > 0) load_values(base);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      if (base + kAttnParts * i > pos) break;  // wave-uniform
+      asm volatile("" : "+v"(vreg[i]));
+      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
+      const float pr = s <= pos ? sc[min(s, pos)] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
+    }
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) pv[part * kHeadDim + blk * 8 + e] = o[e];
@@ -373,19 +444,30 @@ __global__ __launch_bounds__(1024) void argmax_next_kernel(const f16 *logits, in
   __shared__ int bi[16];
   __shared__ int chosen;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  constexpr int kLoads = 6;  // 16-byte loads per thread per round: 49152 logits per round
   float best = -INFINITY;
   int idx = 0x7fffffff;
-  for (int b = t; b * 8 < vocab; b += 1024) {
-    if (b * 8 + 8 <= vocab) {
-      const h8 v = *reinterpret_cast<const h8 *>(logits + b * 8);
+  const int full = vocab >> 3;  // whole 8-logit blocks; the tail is read element by element
+  const __amdgpu_buffer_rsrc_t lbuf = buffer_rsrc(logits, (size_t)full * 16);
+  for (int base = 0; base < full; base += 1024 * kLoads) {
+    u4 v[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int b = base + t + 1024 * i;
+      v[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(lbuf, b < full ? b * 16 : kOutOfRange, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int b = base + t + 1024 * i;
+      const h8 h8v = __builtin_bit_cast(h8, v[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if ((float)v[e] > best) { best = (float)v[e]; idx = b * 8 + e; }
-    } else {
-      for (int i = b * 8; i < vocab; ++i)
-        if ((float)logits[i] > best) { best = (float)logits[i]; idx = i; }
+        if (b < full && (float)h8v[e] > best) { best = (float)h8v[e]; idx = b * 8 + e; }
     }
   }
+  for (int i = full * 8 + t; i < vocab; i += 1024)
+    if ((float)logits[i] > best) { best = (float)logits[i]; idx = i; }
   if (idx == 0x7fffffff) idx = vocab;  // a thread with no element (or only -inf) loses every tie below
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {

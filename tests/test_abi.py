@@ -86,8 +86,16 @@ def test_forced_fast_path_on_unaligned_shape_is_unsupported():
 def test_workspace_sizes():
     status, size, _ = workspace(args())
     assert status == 0 and size == 0
-    # correction on the decode path needs z = M x rank fp16
+    # one row with K <= 1536: the single-tile kernel computes z inside each workgroup
     status, size, _ = workspace(args(rank=32, down=0x50000, up=0x60000, up_ld=32))
+    assert status == 0 and size == 0
+    # the split decode GEMV (forced, or M > 1) stages z = M x rank fp16 in the workspace
+    status, size, _ = workspace(args(rank=32, down=0x50000, up=0x60000, up_ld=32, flags=lowbit_hip.FLAG_FORCE_GEMV))
+    assert status == 0 and size == 256
+    status, size, _ = workspace(args(M=2, rank=32, down=0x50000, up=0x60000, up_ld=32))
+    assert status == 0 and size == 256
+    # an unaligned U keeps one row on the split GEMV, with its z buffer
+    status, size, _ = workspace(args(rank=32, down=0x50000, up=0x60002, up_ld=32))
     assert status == 0 and size == 256
     # split-K decode of a tall K needs fp32 partials
     status, size, _ = workspace(args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128,

@@ -152,6 +152,27 @@ def test_identity_input_is_bit_exact(device, path, fmt, scale):
     np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
+@pytest.mark.parametrize('fmt', ['int8', 'int4', 'nf4'])
+def test_single_row_path_identity_is_bit_exact(device, fmt):
+    """One-row calls (the single-tile path) with unit vectors e_k return column k of dequantize()."""
+    announce('identity single row', fmt)
+    k, n, group = 64, 20, 32
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    if fmt == 'int8':
+        data = rng.integers(-127, 128, (n, k), dtype=np.int8).tobytes()
+    else:
+        data = o.pack(codes)
+    scales = (2.0 ** rng.integers(-6, 4, (n, k // group))).astype(np.float16).tobytes()
+    want = o.dequantize(fmt, (n, k), group, data, scales)
+    for col in range(k):
+        x = np.zeros((1, k), np.float16)
+        x[0, col] = 1.0
+        p = dict(fmt=fmt, m=1, n=n, k=k, group=group, x=x, data=data, scales=scales, bias=None, down=None, up=None)
+        got = run(p, device)
+        np.testing.assert_array_equal(got[0].view(np.uint16), want[:, col].view(np.uint16))
+
+
 SHAPES = [
     # (fmt, M, N, K, group) -- config shapes and awkward edges
     ('int8', 1, 1536, 576, 576),      # config 1 (without correction here)

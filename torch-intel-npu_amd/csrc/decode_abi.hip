@@ -119,6 +119,19 @@ lb_status launch_status(const char *what) {
 
 }  // namespace
 
+namespace lb {
+void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, int tiles, hipStream_t s) {
+  switch (format) {
+    case FMT_INT8:
+      scaled ? launch_fused_t<FMT_INT8, true>(p, tiles, ranked, s) : launch_fused_t<FMT_INT8, false>(p, tiles, ranked, s);
+      break;
+    case FMT_INT4: launch_fused_t<FMT_INT4, true>(p, tiles, ranked, s); break;
+    case FMT_NF4: launch_fused_t<FMT_NF4, true>(p, tiles, ranked, s); break;
+    default: launch_fused_t<FMT_FP16, false>(p, tiles, ranked, s); break;
+  }
+}
+}  // namespace lb
+
 extern "C" {
 
 lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
@@ -155,18 +168,9 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
     }
     q.tiles_end = tiles;  // absent problems own no tiles
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool scaled = !dense && !p.per_row;
   bool ranked = false;
   for (uint32_t i = 0; i < a->count; ++i) ranked = ranked || a->problems[i].rank > 0;
-  switch (a->format) {
-    case LB_FORMAT_INT8:
-      scaled ? launch_fused_t<FMT_INT8, true>(p, tiles, ranked, s) : launch_fused_t<FMT_INT8, false>(p, tiles, ranked, s);
-      break;
-    case LB_FORMAT_INT4: launch_fused_t<FMT_INT4, true>(p, tiles, ranked, s); break;
-    case LB_FORMAT_NF4: launch_fused_t<FMT_NF4, true>(p, tiles, ranked, s); break;
-    default: launch_fused_t<FMT_FP16, false>(p, tiles, ranked, s); break;
-  }
+  launch_fused(p, (int)a->format, !dense && !p.per_row, ranked, tiles, static_cast<hipStream_t>(stream));
   return launch_status("lb_fused_linear");
 }
 

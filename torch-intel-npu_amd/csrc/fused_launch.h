@@ -1,0 +1,37 @@
+// Host/device declarations shared by the translation units that launch the fused decode GEMV
+// (lb_fused_linear and lb_linear's single-row path).
+#pragma once
+#include "lb_common.h"
+
+namespace lb {
+
+constexpr int kFusedMaxProblems = 3;
+constexpr int kFusedMaxRank = 32;
+constexpr int kFusedMaxK = 1536;
+enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
+
+struct FusedProblem {
+  const uint8_t *codes;   // packed codes (fp16 weights for FMT_FP16), rows [N, K]
+  const f16 *scales;      // [N, G]
+  f16 *y;                 // [N]
+  const f16 *bias;        // [N] or null
+  const f16 *residual;    // [N] or null (may equal y: each element is read and written by one lane)
+  const f16 *down;        // V [rank, K] or null
+  const f16 *up;          // U [N, up_ld] or null
+  int N, rank, up_ld;
+  int tiles_end;          // exclusive prefix sum of 16-row tiles over the problems
+};
+
+struct FusedParams {
+  const f16 *x;           // [K] activation (PRO_SILU_MUL: the gate row)
+  const f16 *x2;          // PRO_SILU_MUL: the up row [K]
+  const f16 *gamma;       // PRO_RMSNORM: [K]
+  float eps;
+  int K, G, group_shift, per_row, prologue;
+  FusedProblem prob[kFusedMaxProblems];
+};
+
+// Launches fused_gemv_kernel for `tiles` 16-row tiles (defined with the kernels).
+void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, int tiles, hipStream_t stream);
+
+}  // namespace lb

@@ -16,34 +16,9 @@
 // scores fp16(q.k), fp16(* scale); softmax in fp32 rounded to fp16; P.V fp32 -> fp16;
 // MLP fp16(fp16(silu(gate)) * up); residual fp16(x + delta).
 #pragma once
-#include "lb_common.h"
+#include "fused_launch.h"
 
 namespace lb {
-
-constexpr int kFusedMaxProblems = 3;
-constexpr int kFusedMaxRank = 32;
-enum Prologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
-
-struct FusedProblem {
-  const uint8_t *codes;   // packed codes (fp16 weights for FMT_FP16), rows [N, K]
-  const f16 *scales;      // [N, G]
-  f16 *y;                 // [N]
-  const f16 *bias;        // [N] or null
-  const f16 *residual;    // [N] or null (may equal y: each element is read and written by one lane)
-  const f16 *down;        // V [rank, K] or null
-  const f16 *up;          // U [N, up_ld] or null
-  int N, rank, up_ld;
-  int tiles_end;          // exclusive prefix sum of 16-row tiles over the problems
-};
-
-struct FusedParams {
-  const f16 *x;           // [K] activation (PRO_SILU_MUL: the gate row)
-  const f16 *x2;          // PRO_SILU_MUL: the up row [K]
-  const f16 *gamma;       // PRO_RMSNORM: [K]
-  float eps;
-  int K, G, group_shift, per_row, prologue;
-  FusedProblem prob[kFusedMaxProblems];
-};
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -9,6 +9,7 @@
 
 #include "../../include/lowbit_hip.h"
 #include "abi_util.h"
+#include "fused_launch.h"
 #include "lb_kernels.h"
 
 using namespace lb;
@@ -16,7 +17,7 @@ using namespace lb::abi;
 
 namespace {
 
-enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2 };
+enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3 };
 
 constexpr int kGemvMaxM = 32;
 constexpr size_t kGemvLdsBudget = 48 * 1024;
@@ -93,6 +94,17 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
   return gs;
 }
 
+// One activation row with K <= kFusedMaxK: the single-tile kernel (all of a workgroup's loads in
+// flight at once, correction z computed inside each workgroup) is faster than the split
+// decode GEMV for every such shape; it needs no workspace.
+bool row_eligible(const lb_linear_args *a) {
+  if (a->M != 1 || a->K > kFusedMaxK) return false;
+  if (a->rank > kFusedMaxRank) return false;
+  const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;
+  if (a->rank > 0 && (!aligned(a->down, 16) || !aligned(a->up, 16) || up_ld % 8 != 0)) return false;
+  return true;
+}
+
 Plan make_plan(const lb_linear_args *a, bool eligible) {
   Plan pl;
   const int fmt = (int)a->format;
@@ -100,13 +112,15 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     pl.path = PATH_GENERIC;
   } else if (a->flags & LB_FLAG_FORCE_GEMM) {
     pl.path = PATH_GEMM;
+  } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && row_eligible(a)) {
+    pl.path = PATH_ROW;
   } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) {
     pl.path = PATH_GEMV;
   } else {
     pl.path = PATH_GEMM;
   }
   size_t off = 0;
-  if (a->rank > 0) {
+  if (a->rank > 0 && pl.path != PATH_ROW) {
     pl.z_off = off;
     pl.z_bytes = (size_t)a->M * a->rank * 2;
     off = round_up(off + pl.z_bytes, 256);
@@ -349,6 +363,32 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
   LinearParams p = base_params(fmt, a->M, a->N, a->K, dense ? a->K : a->group_size, a->codes, a->scales, a->x,
                                a->ldx, a->y, a->ldy, a->K);
   p.bias = static_cast<const f16 *>(a->bias);
+  if (plan.path == PATH_ROW) {
+    const bool scaled = !dense && !p.per_row;
+    FusedParams fp{};
+    fp.x = p.x;
+    fp.K = p.K;
+    fp.G = p.G;
+    fp.group_shift = p.group_shift;
+    fp.per_row = p.per_row;
+    fp.prologue = PRO_NONE;
+    const int tiles = (int)((a->N + 15) / 16);
+    FusedProblem &q = fp.prob[0];
+    q.codes = p.codes;
+    q.scales = p.scales;
+    q.y = p.y;
+    q.bias = p.bias;
+    q.N = p.N;
+    q.rank = (int)a->rank;
+    if (a->rank > 0) {
+      q.down = static_cast<const f16 *>(a->down);
+      q.up = static_cast<const f16 *>(a->up);
+      q.up_ld = (int)(a->up_ld == 0 ? a->rank : a->up_ld);
+    }
+    for (FusedProblem &r : fp.prob) r.tiles_end = tiles;
+    launch_fused(fp, fmt, scaled, a->rank > 0, tiles, s);
+    return launch_status("lb_linear");
+  }
   uint8_t *ws = static_cast<uint8_t *>(a->workspace);
   if (a->rank > 0) {
     const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;

@@ -5,10 +5,13 @@ every SmolLM-135M linear shape -- q/o 576x576, k/v 192x576, gate/up 1536x576,
 down 576x1536, lm_head 49152x576.  The reference requires K % group == 0, so K=576
 shapes use group 64 and K=1536 uses group 128.  One step = one pass over the eight
 linears, each reading a distinct weight replica from a pool larger than the 256 MB
-MALL, so the bandwidth is HBM bandwidth.  Launches are replayed from HIP graphs so
-host launch cost is not in the timed region; inputs are resident in HBM beforehand.
+MALL, so the bandwidth is HBM bandwidth.  The pass is issued as the SmolLM decode step
+issues it: q|k|v and gate|up share their input row and run as one grouped launch each,
+o, down and lm_head as one launch each (5 launches).  Launches are replayed from HIP
+graphs so host launch cost is not in the timed region; inputs are resident in HBM.
 
-Also reported: the same pass at M=4 and M=16, per-kernel GB/s, the config-5 roofline
+Also reported: the pass with one launch per shape (8 launches), at M=4 and M=16,
+per-launch GB/s, the config-5 roofline
 sweep, prefill GEMM TFLOP/s (configs 3 and 5), and the CPU baseline (the reference's
 CPU path: fp32 torch matmul on pre-dequantized weights) timed on this host.
 
@@ -117,22 +120,55 @@ def kernel_time_us(linear, stream, replays=8):
     return 1000.0 * ms / (replays * len(linear.calls))
 
 
-def smol_pass(m, device, stream, steps, warmup):
+# Launch groups of the decode step: projections that read the same activation row run as one
+# lb_fused_linear launch (q|k|v, gate|up), exactly as the SmolLM decode step issues them.
+DECODE_GROUPS = [('qkv', ('q_proj', 'k_proj', 'v_proj')), ('o_proj', ('o_proj',)), ('gate_up', ('gate_proj', 'up_proj')),
+                 ('down_proj', ('down_proj',)), ('lm_head', ('lm_head',))]
+
+
+class Group:
+    """Replicated weights of projections sharing one input row, run as one fused launch per replica."""
+
+    def __init__(self, linears, device):
+        import lowbit_hip
+        self.linears = linears
+        self.bytes = sum(lin.bytes for lin in linears) - 2 * linears[0].k * (len(linears) - 1)  # x read once
+        first = linears[0]
+        x = first.x.view(-1)
+        self.ys = [torch.empty(lin.n, dtype=torch.float16, device=device) for lin in linears]
+        self.calls = []
+        for r in range(len(first.replicas)):
+            problems = [dict(codes=lin.replicas[r][0], scales=lin.replicas[r][1], N=lin.n, y=y)
+                        for lin, y in zip(linears, self.ys)]
+            self.calls.append(lowbit_hip.PreparedFused(x, problems, format=first.fmt, K=first.k,
+                                                       group_size=first.group))
+
+
+def smol_pass(m, device, stream, steps, warmup, grouped=False):
+    """One pass over the eight config-2 linears: per shape (8 launches) or, for M=1, in the decode
+    step's launch groups (5 launches)."""
     linears = []
     total = sum(algorithmic_bytes('int4', m, n, k, g) for _, n, k, g in SMOL_SHAPES)
     copies = copies_for(total)
     for i, (name, n, k, g) in enumerate(SMOL_SHAPES):
         linears.append(Linear(make_weight('int4', n, k, g, 100 + i), m, copies, device, 200 + i))
-    for lin in linears:
-        lin.calls[0].run()
-    graphs = [capture([lin.calls[r].run for lin in linears], stream) for r in range(copies)]
+    by_name = {name: lin for (name, *_), lin in zip(SMOL_SHAPES, linears)}
+    if grouped:
+        units = [(label, Group([by_name[n] for n in names], device) if len(names) > 1 else by_name[names[0]])
+                 for label, names in DECODE_GROUPS]
+        total = sum(u.bytes for _, u in units)
+    else:
+        units = [(name, lin) for (name, *_), lin in zip(SMOL_SHAPES, linears)]
+    for _, unit in units:
+        unit.calls[0].run()
+    graphs = [capture([unit.calls[r].run for _, unit in units], stream) for r in range(copies)]
     time_graphs(graphs, warmup, stream)
     ms = time_graphs(graphs, steps, stream)
     per_kernel = {}
-    for (name, *_), lin in zip(SMOL_SHAPES, linears):
-        us = kernel_time_us(lin, stream)
-        per_kernel[name] = dict(us=round(us, 3), gbs=round(lin.bytes / us / 1e3, 1))
-    return dict(ms_per_step=ms / steps, bytes_per_step=total, copies=copies,
+    for name, unit in units:
+        us = kernel_time_us(unit, stream)
+        per_kernel[name] = dict(us=round(us, 3), gbs=round(unit.bytes / us / 1e3, 1))
+    return dict(ms_per_step=ms / steps, bytes_per_step=total, copies=copies, launches=len(units),
                 gbs=total / (ms / steps) / 1e6, per_kernel=per_kernel, linears=linears)
 
 
@@ -300,13 +336,19 @@ def main():
         return
 
     t0 = time.time()
-    log('config-2 pass, M=1')
-    head = smol_pass(1, device, stream, args.steps, args.warmup)
+    log('config-2 pass, M=1 (decode launch groups)')
+    head = smol_pass(1, device, stream, args.steps, args.warmup, grouped=True)
     log(f"M=1: {head['gbs']:.1f} GB/s per pass, {head['ms_per_step'] * 1e3:.2f} us/step")
     dominant = head['per_kernel']['lm_head']
     lm = head['linears'][-1]
     del head['linears']
-    others = {}
+    torch.cuda.empty_cache()
+    log('config-2 pass, M=1 (one launch per shape)')
+    flat = smol_pass(1, device, stream, max(32, args.steps // 4), 8)
+    del flat['linears']
+    others = {'M=1 per shape': dict(gbs=round(flat['gbs'], 1), us_per_step=round(flat['ms_per_step'] * 1e3, 2),
+                                    launches=flat['launches'], per_kernel=flat['per_kernel'])}
+    torch.cuda.empty_cache()
     for m in (4, 16):
         log(f'config-2 pass, M={m}')
         r = smol_pass(m, device, stream, max(32, args.steps // 4), 8)
@@ -338,19 +380,21 @@ def main():
         'config': {
             'workload': 'configs[1]: INT4 group-wise dequant-GEMV, M=1, all SmolLM-135M linear shapes '
                         '(q,k,v,o 576/192x576 g64; gate,up 1536x576 g64; down 576x1536 g128; lm_head 49152x576 g64)',
-            'step': 'one pass over the 8 linears (8 kernel launches replayed from a HIP graph)',
+            'step': ('one pass over the 8 linears in the decode step\'s 5 launches (q|k|v and gate|up share their '
+                     'input row and run as one lb_fused_linear each; o, down, lm_head one lb_linear each), '
+                     'replayed from a HIP graph'),
             'weight_pool_bytes': int(head['bytes_per_step'] * head['copies']),
             'replicas': head['copies'],
             'hbm_frac_of_pass': round(head['gbs'] / HBM_PEAK_GBS, 4),
         },
         'roofline': {
-            'kernel': 'gemv_kernel<INT4> lm_head 49152x576 g64, M=1',
+            'kernel': 'fused_gemv_kernel<INT4> (one-row lb_linear) lm_head 49152x576 g64, M=1',
             'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
             'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_per_launch(),
             'algorithmic_bytes_per_launch': lm.bytes, 'avg_launch_us': dominant['us'],
         },
         'cpu_baseline': cpu,
-        'per_kernel_M1': head['per_kernel'],
+        'per_launch_M1': head['per_kernel'],
         'decode_smollm135m_w8_rank32': decode,
         'passes': others,
         'sweep': rows,

@@ -191,6 +191,10 @@ SHAPES = [
     ('int8', 256, 576, 576, 576),
     ('int8', 33, 1536, 576, 32),      # grouped int8
     ('int4', 130, 129, 96, 32),
+    ('int4', 1, 130, 16384, 128),     # one row, long K (single-tile kernel, 16384-row staging)
+    ('int8', 1, 300, 8192, 8192),     # one row, long K, per-row W8
+    ('nf4', 1, 64, 5000 // 32 * 32, 64),
+    ('int4', 1, 100, 4096, 32),       # one row, long K, group 32: falls back to the split GEMV
 ]
 
 
@@ -276,8 +280,9 @@ def test_split_k_repeated_calls_reuse_workspace(device, spec):
     scales = to_dev(np.frombuffer(p['scales'], np.float16), device)
     x = to_dev(p['x'], device)
     out = torch.empty(m, n, dtype=torch.float16, device=device)
-    call = lowbit_hip.PreparedLinear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, out=out)
-    assert call.workspace_bytes > 0  # this shape is split along K
+    call = lowbit_hip.PreparedLinear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, out=out,
+                                     flags=lowbit_hip.FLAG_FORCE_GEMV)
+    assert call.workspace_bytes > 0  # the split decode GEMV splits this shape along K
     want = expected(p)
     first = None
     for _ in range(3):

@@ -97,12 +97,25 @@ lb_status check_fused(const lb_fused_linear_args *a) {
   return ok();
 }
 
+template <int FMT, bool SCALED, int KMAX, bool RANKED>
+void launch_fused_k(const FusedParams &p, int tiles, hipStream_t s) {
+  hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, KMAX, RANKED>), dim3(tiles), dim3(256), 0, s, p);
+}
+
+// The shortest staged row that holds K: 640 and 1536 (decode shapes), then 4096 / 8192 / 16384
+// for one-row calls without a correction, up to the format's limit.
 template <int FMT, bool SCALED, bool RANKED>
 void launch_fused_r(const FusedParams &p, int tiles, hipStream_t s) {
-  if (p.K <= 640)
-    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, 640, RANKED>), dim3(tiles), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, LB_FUSED_MAX_K, RANKED>), dim3(tiles), dim3(256), 0, s, p);
+  constexpr int LIMIT = fused_kmax_limit(FMT);
+  if (p.K <= 640) return launch_fused_k<FMT, SCALED, 640, RANKED>(p, tiles, s);
+  if (p.K <= kFusedMaxK || RANKED) return launch_fused_k<FMT, SCALED, kFusedMaxK, RANKED>(p, tiles, s);
+  if constexpr (!RANKED) {
+    if (p.K <= 4096) return launch_fused_k<FMT, SCALED, 4096, false>(p, tiles, s);
+    if constexpr (LIMIT >= 8192) {
+      if (p.K <= 8192) return launch_fused_k<FMT, SCALED, 8192, false>(p, tiles, s);
+    }
+    if constexpr (LIMIT >= 16384) return launch_fused_k<FMT, SCALED, 16384, false>(p, tiles, s);
+  }
 }
 
 // RANKED instantiations carry the correction (V and U loads); the others have none at all.

@@ -31,6 +31,12 @@ struct FusedParams {
   FusedProblem prob[kFusedMaxProblems];
 };
 
+// Longest K a format's single-tile kernel takes (32 weight loads per lane); beyond
+// kFusedMaxK only without a correction and with groups of at least 64 (or one per row).
+constexpr int fused_kmax_limit(int format) {
+  return format == FMT_FP16 ? 4096 : format == FMT_INT8 ? 8192 : 16384;
+}
+
 // Launches fused_gemv_kernel for `tiles` 16-row tiles (defined with the kernels).
 void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, int tiles, hipStream_t stream);
 

@@ -45,9 +45,15 @@ __device__ __forceinline__ f16 rope_element(float x, float r, float c, float s) 
   return (f16)((float)a + (float)b);
 }
 
+// Smallest group size the KMAX variant stages scales for: KMAX <= 1536 handles group 32, the
+// long-K variants (one-row lb_linear calls) need group >= 64.
+template <int KMAX> struct FusedGroupMin { static constexpr int value = KMAX <= 1536 ? 32 : 64; };
+
 // One workgroup = 4 waves = one 16-row tile of one problem; the waves split K (wave w takes
 // k-steps w, w + 4, ...) and are reduced through LDS.  K <= KMAX, so every lane issues all
-// of its weight loads (D of them) up front and the activation row is staged once.
+// of its weight loads (D of them) up front and the activation row is staged once.  Every row
+// of the MFMA A operand is the activation row (only row 0 of the result is used), so no zero
+// rows are staged.
 //
 // Every global load is issued, straight-line, before the first wait: the epilogue operands
 // (one load per wave), the prologue row, the activation, the scales, V (RANKED only) and the
@@ -61,13 +67,16 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   constexpr int KG = 4;
   constexpr int WSTEP = KG * KSTEP;
   constexpr int D = (KMAX + WSTEP - 1) / WSTEP;  // weight loads per lane
+  static_assert(D <= 32, "KMAX too long for this format");
   constexpr int T8 = CPL / 8;
-  constexpr int XLD = KMAX + KSTEP + 8;           // staged row, zero beyond K
+  constexpr int XLD = KMAX + KSTEP + 8;           // staged row, zero from K to K + KSTEP
+  constexpr int XB = (KMAX / 8 + 255) / 256;      // 16-byte activation loads per thread
   constexpr int VB = RANKED ? KMAX / 64 : 0;      // 16-byte V loads per thread (8 threads per rank row)
-  constexpr int GMAX = KMAX / 32;                 // groups per row (group >= 32)
-  constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;  // staged scales per thread
+  constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;  // groups per row at most
+  constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0; // staged scales per thread
   constexpr int kOutOfRange = (int)0x80000000u;
-  __shared__ __align__(16) f16 xs[2 * XLD];       // row 0: the activation, row 1: zeros
+  static_assert(!RANKED || KMAX <= kFusedMaxK, "the correction is staged for K <= kFusedMaxK");
+  __shared__ __align__(16) f16 xs[XLD];
   __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
   __shared__ __align__(16) f16 us[RANKED ? 16 * kFusedMaxRank : 8];  // U rows of the tile
   __shared__ f16 es[3 * 16];                      // residual, bias, per-row scale of the tile
@@ -111,12 +120,21 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   }
   // Activation row (and the second row of the prologue: gamma or the up row).
   const int blocks = K >> 3;
-  const int xoff = t < blocks ? t * 16 : kOutOfRange;
   const size_t kb = (size_t)K * 2;
   const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
-  const h8 av = __builtin_bit_cast(
-      h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb), xoff, 0, 0));
-  const h8 xv = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x, kb), xoff, 0, 0));
+  const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.x, kb);
+  h8 av[XB], xv[XB];
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    av[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(abuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    xv[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xbuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+  }
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
     const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)n0 * p.G, (size_t)rows * p.G * 2);
@@ -155,28 +173,35 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   if (p.prologue == PRO_RMSNORM) {
     float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s += (float)xv[e] * (float)xv[e];
+    for (int i = 0; i < XB; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
     s = wave_sum(s);
     if (lane == 0) wsum[wave] = s;
     __syncthreads();
     const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
     inv = 1.0f / sqrtf(total / (float)K + p.eps);
   }
-  if (t < blocks) {
-    h8 v;
-    if (p.prologue == PRO_RMSNORM) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[e] * inv) * (float)av[e]);
-    } else if (p.prologue == PRO_SILU_MUL) {
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    if (b < blocks) {
+      h8 v;
+      if (p.prologue == PRO_RMSNORM) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[e]) * (float)av[e]);
-    } else {
-      v = xv;
+        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[i][e] * inv) * (float)av[i][e]);
+      } else if (p.prologue == PRO_SILU_MUL) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[i][e]) * (float)av[i][e]);
+      } else {
+        v = xv[i];
+      }
+      *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(v);
     }
-    *reinterpret_cast<h8 *>(xs + t * 8) = permute_block<FMT>(v);
   }
-  for (int b = blocks + t; b < 2 * XLD / 8; b += 256)  // zeros: tail of row 0, all of row 1
-    *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  // Zeros past K: MFMA lanes read up to KSTEP beyond it, the z product (RANKED) up to KMAX.
+  const int zend = RANKED ? XLD : min(XLD, K + KSTEP + 8);
+  for (int b = blocks + t; b * 8 < zend; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
   if constexpr (SCALED) {
 #pragma unroll
     for (int i = 0; i < SC; ++i)
@@ -206,9 +231,9 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
     if (vpart == 0) zs[vr] = (float)(f16)acc;
   }
 
-  // ---- the product on MFMA: A = activation row (row 0) or zeros, B = decoded weights ----
+  // ---- the product on MFMA: every A row is the activation row, B = decoded weights ----
   f4 acc = {0.f, 0.f, 0.f, 0.f};
-  const f16 *a0 = xs + (j == 0 ? 0 : XLD) + g * CPL;
+  const f16 *a0 = xs + g * CPL;
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
@@ -226,7 +251,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
     }
   }
-  // Lane (j, g) holds D rows 4g..4g+3 of column j; the activation is row 0 (g == 0, r == 0).
+  // Lane (j, g) holds D rows 4g..4g+3 of column j; all rows are equal, row 0 (g == 0) is used.
   if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
   __syncthreads();
   const bool writer = wave == 0 && g == 0 && j < rows;

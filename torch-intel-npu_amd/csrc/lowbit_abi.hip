@@ -94,11 +94,14 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
   return gs;
 }
 
-// One activation row with K <= kFusedMaxK: the single-tile kernel (all of a workgroup's loads in
-// flight at once, correction z computed inside each workgroup) is faster than the split
-// decode GEMV for every such shape; it needs no workspace.
+// One activation row: the single-tile kernel (all of a workgroup's loads in flight at once,
+// correction z computed inside each workgroup for K <= kFusedMaxK) needs no workspace.
 bool row_eligible(const lb_linear_args *a) {
-  if (a->M != 1 || a->K > kFusedMaxK) return false;
+  if (a->M != 1 || a->K > fused_kmax_limit((int)a->format)) return false;
+  if (a->K > kFusedMaxK) {  // long rows: no correction, groups of at least 64 (or one per row)
+    const bool dense = a->format == LB_FORMAT_FP16;
+    if (a->rank > 0 || !(dense || a->group_size == a->K || a->group_size >= 64)) return false;
+  }
   if (a->rank > kFusedMaxRank) return false;
   const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;
   if (a->rank > 0 && (!aligned(a->down, 16) || !aligned(a->up, 16) || up_ld % 8 != 0)) return false;

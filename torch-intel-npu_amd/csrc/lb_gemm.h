@@ -1,0 +1,215 @@
+// gfx950 prefill GEMM of the low-bit linear path: y[M,N] = x[M,K] . dequant(W)[N,K]^T.
+//
+// 256 threads (2 x 2 waves) per BM x BN tile; each wave owns a (BM/2) x (BN/2) block of
+// v_mfma_f32_32x32x16_f16 tiles.  K advances in steps of BK = 64:
+//   - the activations (fp16) and the packed weights of a step are fetched with 16-byte buffer
+//     loads two steps ahead into registers (rows past M or N, and k past K, read zeros);
+//   - the weights are decoded to fp16 (fp16(q*s), or q for per-row int8) once per tile and
+//     written with the activations into one of two LDS buffers (gfx950 has 160 KB of LDS per
+//     workgroup, so both buffers of a 128 x 128 tile fit);
+//   - one barrier per step separates the MFMAs on buffer s % 2 from the writes of step s + 1
+//     into the other buffer.
+// The loop is unrolled by two so each register stage keeps its own registers (a loaded
+// register is never copied before its load completes).  The epilogue is the linear path's
+// (store_output): per-row scale, fp16, bias, correction.
+#pragma once
+#include "lb_kernels.h"
+
+namespace lb {
+
+#ifndef LB_GEMM_IGLP
+#define LB_GEMM_IGLP 0
+#endif
+#ifndef LB_GEMM_IGLP_VALU
+#define LB_GEMM_IGLP_VALU 4
+#endif
+
+template <int FMT, int BM, int BN, int BK>
+struct G2Traits {
+  static constexpr int BITS = FormatTraits<FMT>::BITS;
+  static constexpr int A_CHUNKS = BM * BK * 2 / 16;              // 16-byte chunks of the A tile
+  static constexpr int B_CHUNKS = BN * BK * BITS / 8 / 16;       // of the packed B tile
+  static constexpr int A_PER = (A_CHUNKS + 255) / 256;
+  static constexpr int B_PER = (B_CHUNKS + 255) / 256;
+  static constexpr int CODES = 16 * 8 / BITS;                    // codes per 16-byte chunk
+  static constexpr int CHUNKS_PER_ROW = BK / CODES;              // B chunks per row per step
+  static constexpr int A_PER_ROW = BK / 8;                       // A chunks per row per step
+};
+
+template <int FMT, int BM, int BN, int BK>
+struct G2Stage {
+  u4 a[G2Traits<FMT, BM, BN, BK>::A_PER];
+  u4 b[G2Traits<FMT, BM, BN, BK>::B_PER];
+  f16 s[G2Traits<FMT, BM, BN, BK>::B_PER];
+};
+
+// K % BK == 0 (the dispatcher guarantees it): no step reads past K.
+template <int FMT, bool SCALED, int BM, int BN, int BK>
+__global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
+  using T = G2Traits<FMT, BM, BN, BK>;
+  using Stage = G2Stage<FMT, BM, BN, BK>;
+  constexpr int LD = BK + 8;                 // LDS row pitch in halves: rows start on different banks
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 MFMA tiles per wave along M and N
+  constexpr int CPC = T::CODES;              // codes per B chunk
+  constexpr int kOutOfRange = (int)0x80000000u;
+  __shared__ __align__(16) f16 As[2][BM * LD];
+  __shared__ __align__(16) f16 Bs[2][BN * LD];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+
+  const int rows_a = min(BM, p.M - bm), rows_b = min(BN, p.N - bn);
+  const size_t row_bytes = T::BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * T::BITS / 8;
+  // Buffer views start at the tile's first row; rows past M / N are out of range (zeros).
+  const __amdgpu_buffer_rsrc_t xbuf =
+      buffer_rsrc(p.x + (size_t)bm * p.ldx, rows_a > 0 ? ((size_t)(rows_a - 1) * p.ldx + p.K) * 2 : 0);
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(p.codes + (size_t)bn * row_bytes, (size_t)rows_b * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      buffer_rsrc(SCALED ? p.scales + (size_t)bn * p.G : p.scales, SCALED ? (size_t)rows_b * p.G * 2 : 0);
+
+  // Per-thread byte offsets of its chunks at k = 0 (out of range for rows past M / N); a step
+  // adds its k offset.  The out-of-range offset plus any k stays out of range (unsigned).
+  int a_off[T::A_PER], b_off[T::B_PER], s_off[T::B_PER];
+#pragma unroll
+  for (int i = 0; i < T::A_PER; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c / T::A_PER_ROW, k = (c % T::A_PER_ROW) * 8;
+    a_off[i] = c < T::A_CHUNKS && r < rows_a ? (r * p.ldx + k) * 2 : kOutOfRange;
+  }
+#pragma unroll
+  for (int i = 0; i < T::B_PER; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c / T::CHUNKS_PER_ROW, k = (c % T::CHUNKS_PER_ROW) * CPC;
+    const bool ok = c < T::B_CHUNKS && r < rows_b;
+    b_off[i] = ok ? (int)(r * row_bytes) + k * T::BITS / 8 : kOutOfRange;
+    s_off[i] = ok ? r * p.G * 2 : kOutOfRange;
+  }
+  auto load = [&](Stage &st, int k0) {
+#pragma unroll
+    for (int i = 0; i < T::A_PER; ++i)
+      st.a[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, a_off[i] + k0 * 2, 0, 0));
+#pragma unroll
+    for (int i = 0; i < T::B_PER; ++i) {
+      st.b[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, b_off[i] + k0 * T::BITS / 8, 0, 0));
+      if constexpr (SCALED)  // a chunk lies inside one group (group >= 32 >= codes per chunk)
+        st.s[i] = __builtin_bit_cast(
+            f16, __builtin_amdgcn_raw_buffer_load_b16(
+                     sbuf, s_off[i] + (((k0 + (tid % T::CHUNKS_PER_ROW) * CPC) >> p.group_shift) << 1), 0, 0));
+    }
+  };
+  auto store = [&](Stage &st, int buf) {
+#pragma unroll
+    for (int i = 0; i < T::A_PER; ++i) {
+      const int c = tid + 256 * i;
+      asm volatile("" : "+v"(st.a[i]));
+      if (c < T::A_CHUNKS)
+        *reinterpret_cast<u4 *>(&As[buf][(c / T::A_PER_ROW) * LD + (c % T::A_PER_ROW) * 8]) = st.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < T::B_PER; ++i) {
+      const int c = tid + 256 * i;
+      asm volatile("" : "+v"(st.b[i]));
+      if (c >= T::B_CHUNKS) continue;
+      const int r = c / T::CHUNKS_PER_ROW, kk = (c % T::CHUNKS_PER_ROW) * CPC;
+      f16 *dst = &Bs[buf][r * LD + kk];
+      const h2 s2 = SCALED ? h2{st.s[i], st.s[i]} : h2{(f16)1.0f, (f16)1.0f};
+      if constexpr (T::BITS == 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<h8 *>(dst + 8 * q) = decode8_natural<FMT, SCALED>(st.b[i][q], 0u, s2, nf4_table);
+      } else if constexpr (T::BITS == 8) {
+        *reinterpret_cast<h8 *>(dst) = decode8_natural<FMT, SCALED>(st.b[i][0], st.b[i][1], s2, nf4_table);
+        *reinterpret_cast<h8 *>(dst + 8) = decode8_natural<FMT, SCALED>(st.b[i][2], st.b[i][3], s2, nf4_table);
+      } else {
+        *reinterpret_cast<u4 *>(dst) = st.b[i];
+      }
+    }
+  };
+
+  f16x acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
+
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      h8 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const h8 *>(&As[buf][(wm * (BM / 2) + i * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj)
+        b[jj] = *reinterpret_cast<const h8 *>(&Bs[buf][(wn * (BN / 2) + jj * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[jj], acc[i][jj], 0, 0, 0);
+    }
+  };
+
+  // Scheduling hint for one step: spread the decode VALU work and the LDS traffic of the next
+  // step between the MFMAs (they use different units and have no data dependences).
+  auto interleave = [&]() {
+#if LB_GEMM_IGLP
+    constexpr int MFMAS = TM * TN * (BK / 16);
+#pragma unroll
+    for (int i = 0; i < MFMAS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x002, LB_GEMM_IGLP_VALU, 0);  // VALU
+    }
+#endif
+  };
+
+  // Step s computes on buffer s % 2; the register stage holding step s + 1 (loaded two steps
+  // earlier) is decoded into the other buffer, and step s + 3 is loaded into the stage just
+  // emptied.  Loads are unconditional (steps past K read out of range): the waits stay exact.
+  // Loads of steps past the last one re-read the last step (in range, unused).
+  const int steps = p.K / BK;
+  const int klast = (steps - 1) * BK;
+  Stage r0, r1;
+  load(r0, 0);
+  load(r1, min(BK, klast));
+  store(r0, 0);
+  load(r0, min(2 * BK, klast));
+  __syncthreads();
+  int s = 0;
+  for (; s + 2 <= steps; s += 2) {
+    compute(0);                 // step s; r1 = step s + 1, r0 = step s + 2
+    store(r1, 1);
+    load(r1, min((s + 3) * BK, klast));
+    interleave();
+    __syncthreads();
+    compute(1);                 // step s + 1; r0 = step s + 2, r1 = step s + 3
+    store(r0, 0);
+    load(r0, min((s + 4) * BK, klast));
+    interleave();
+    __syncthreads();
+  }
+  if (s < steps) compute(0);    // odd step count: the last step is in buffer 0
+
+  // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < TN; ++jj) {
+      const int n = bn + wn * (BN / 2) + jj * 32 + (lane & 31);
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < p.M) store_output(p, m, n, acc[i][jj][r]);
+      }
+    }
+}
+
+}  // namespace lb

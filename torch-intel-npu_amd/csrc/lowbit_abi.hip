@@ -10,6 +10,7 @@
 #include "../../include/lowbit_hip.h"
 #include "abi_util.h"
 #include "fused_launch.h"
+#include "lb_gemm.h"
 #include "lb_kernels.h"
 
 using namespace lb;
@@ -264,10 +265,31 @@ void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kg, int kc, hi
   }
 }
 
+#ifndef LB_GEMM_BM
+#define LB_GEMM_BM 128
+#endif
+#ifndef LB_GEMM_BN
+#define LB_GEMM_BN 128
+#endif
+#ifndef LB_GEMM_BK
+#define LB_GEMM_BK 64
+#endif
+// Large tiles when they alone give every CU a workgroup, else 64 x 64 tiles (k steps of 64
+// where K allows, else 32).
 template <int FMT, bool SCALED>
 void launch_gemm_t(const LinearParams &p, hipStream_t s) {
-  const dim3 grid((p.N + kGemmBN - 1) / kGemmBN, (p.M + kGemmBM - 1) / kGemmBM);
-  hipLaunchKernelGGL((gemm_kernel<FMT, SCALED>), grid, dim3(256), 0, s, p);
+  constexpr int BM = LB_GEMM_BM, BN = LB_GEMM_BN, BK = LB_GEMM_BK;
+  const int64_t big = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  if (big >= 256 && p.K % BK == 0) {
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM),
+                       dim3(256), 0, s, p);
+  } else if (p.K % 64 == 0) {
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64), dim3(256), 0,
+                       s, p);
+  } else {
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64), dim3(256), 0,
+                       s, p);
+  }
 }
 
 void launch_gemm(int fmt, bool scaled, const LinearParams &p, hipStream_t s) {

@@ -97,9 +97,10 @@ def test_workspace_sizes():
     # an unaligned U keeps one row on the split GEMV, with its z buffer
     status, size, _ = workspace(args(rank=32, down=0x50000, up=0x60002, up_ld=32))
     assert status == 0 and size == 256
-    # split-K decode of a tall K needs fp32 partials
+    # split-K decode of a tall K (the forced split GEMV) needs fp32 partials
     status, size, _ = workspace(args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128,
-                                     x=0x1000000, y=0x2000000, scales=0x3000000, codes=0x4000000))
+                                     x=0x1000000, y=0x2000000, scales=0x3000000, codes=0x4000000,
+                                     flags=lowbit_hip.FLAG_FORCE_GEMV))
     assert status == 0 and size > 0 and size % (1024 * 4) == 0  # fp32 split-K partials [splits, M, N]
     # prefill with correction needs z and the fp16 delta
     status, size, _ = workspace(args(M=256, rank=32, down=0x5000000, up=0x6000000, up_ld=32,
@@ -109,7 +110,7 @@ def test_workspace_sizes():
 
 def test_missing_workspace_is_rejected_by_lb_linear():
     a = args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128, x=0x1000000, y=0x2000000,
-             scales=0x3000000, codes=0x4000000)
+             scales=0x3000000, codes=0x4000000, flags=lowbit_hip.FLAG_FORCE_GEMV)
     status = lowbit_hip.library().lb_linear(ctypes.byref(a), None)
     assert status == lowbit_hip.INVALID_ARGUMENT
     assert 'workspace' in lowbit_hip.library().lb_last_error().decode()

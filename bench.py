@@ -17,6 +17,7 @@ CPU path: fp32 torch matmul on pre-dequantized weights) timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cpu]
        python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
+       python bench.py --decode-only      (config-4 decode leg alone, for rocprofv3 --kernel-trace)
 """
 import argparse
 import json
@@ -110,6 +111,32 @@ def time_graphs(graphs, count, stream):
     return start.elapsed_time(stop)
 
 
+PASSES_PER_GRAPH = 16
+
+
+def time_passes(pass_fns, copies, steps, warmup, stream):
+    """Time exactly `steps` passes (ms).  Passes are recorded PASSES_PER_GRAPH to a graph (pass t of
+    graph i reads replica (i * PASSES_PER_GRAPH + t) mod copies), so one graph launch is shared by
+    several passes, as in a decode loop captured whole; a remainder uses one-pass graphs."""
+    per = PASSES_PER_GRAPH
+    full = [capture([fn for t in range(per) for fn in pass_fns(i * per + t)], stream)
+            for i in range((copies + per - 1) // per)]
+    single = [capture(pass_fns(r), stream) for r in range(min(copies, steps % per))]
+    time_graphs(full, max(1, warmup // per), stream)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for i in range(steps // per):
+            full[i % len(full)].replay()
+        for i in range(steps % per):
+            single[i % len(single)].replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop)
+
+
 def kernel_time_us(linear, stream, replays=8):
     """Average duration of one launch of `linear`, over a graph of all its replicas."""
     for call in linear.calls[:2]:
@@ -161,9 +188,7 @@ def smol_pass(m, device, stream, steps, warmup, grouped=False):
         units = [(name, lin) for (name, *_), lin in zip(SMOL_SHAPES, linears)]
     for _, unit in units:
         unit.calls[0].run()
-    graphs = [capture([unit.calls[r].run for _, unit in units], stream) for r in range(copies)]
-    time_graphs(graphs, warmup, stream)
-    ms = time_graphs(graphs, steps, stream)
+    ms = time_passes(lambda r: [unit.calls[r % copies].run for _, unit in units], copies, steps, warmup, stream)
     per_kernel = {}
     for name, unit in units:
         us = kernel_time_us(unit, stream)
@@ -219,6 +244,9 @@ def cpu_leg(budget_s):
                 dequant_inclusive_gbs=round(total / deq / 1e9, 3))
 
 
+DECODE_TOKENS_PER_GRAPH = 8
+
+
 def decode_leg(device, steps, cpu_steps):
     """Config 4: 30-layer random-init SmolLM-135M, W8 per-row + rank-32 corrections, theta 1e4,
     256-token prompt, then greedy decode with the fp16 KV cache (GraphDecoder replays)."""
@@ -249,17 +277,18 @@ def decode_leg(device, steps, cpu_steps):
         out['eager_decode_tokens_per_s'] = round(8 / (time.perf_counter() - t0), 1)
         decoder = GraphDecoder(stack, io)
         decoder.load(caches, first)
-        decoder.capture()
+        per_graph = DECODE_TOKENS_PER_GRAPH if steps % DECODE_TOKENS_PER_GRAPH == 0 else 1
+        decoder.capture(tokens=per_graph)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record()
-        for _ in range(steps):
+        for _ in range(steps // per_graph):
             decoder.graph.replay()
         stop.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(stop)
-        out.update(decode_steps=steps, decode_ms_per_token=round(ms / steps, 4),
+        out.update(decode_steps=steps, tokens_per_graph=per_graph, decode_ms_per_token=round(ms / steps, 4),
                    decode_tokens_per_s=round(steps * 1000.0 / ms, 1),
                    first_tokens=decoder.tokens[256:256 + 8].tolist())
     if cpu_steps:
@@ -317,6 +346,7 @@ def main():
     ap.add_argument('--profile-kernel', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=128)
+    ap.add_argument('--decode-only', action='store_true', help='only the config-4 decode leg (for tracing)')
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -333,6 +363,10 @@ def main():
     torch.manual_seed(0)
     if args.profile_kernel:
         profile_kernel(device, stream)
+        return
+    if args.decode_only:
+        decode = decode_leg(device, args.decode_steps, 0)
+        print(json.dumps(dict(decode_smollm135m_w8_rank32=decode)), flush=True)
         return
 
     t0 = time.time()

@@ -583,6 +583,7 @@ class GraphDecoder:
         else:
             self._build_staged(z)
         self.graph = None
+        self.graph_tokens = 1
 
     # ---------------------------------------------------------------- fused launches
     @staticmethod
@@ -736,17 +737,27 @@ class GraphDecoder:
         self.head.run()
         self.argmax.run()
 
-    def capture(self):
-        """Record step() into a HIP graph (warm-up runs first on a side stream, as torch requires)."""
+    def capture(self, tokens=1):
+        """Record `tokens` consecutive step()s into one HIP graph (warm-up runs first on a side
+        stream, as torch requires).  Every step reads its position from the device, so one replay
+        generates `tokens` tokens; more than one shares a graph launch between them."""
+        if type(tokens) is not int or tokens < 1:
+            raise ValueError('tokens must be a positive int')
+        start = int(self.pos.item())
+        if start + tokens > self.capacity:
+            raise ValueError(f'capturing {tokens} steps from position {start} exceeds the KV capacity')
         saved = [t.clone() for t in [self.pos, self.token, self.h] + self.keys + self.values]
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
-            self.step()
+            for _ in range(tokens):
+                self.step()
         torch.cuda.current_stream(self.device).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.step()
+            for _ in range(tokens):
+                self.step()
+        self.graph_tokens = tokens
         for dst, src in zip([self.pos, self.token, self.h] + self.keys + self.values, saved):
             dst.copy_(src)  # the warm-up advanced the state; restore it
         return self.graph
@@ -755,9 +766,11 @@ class GraphDecoder:
         """Replay `steps` tokens; returns the generated token ids (one host sync at the end)."""
         if self.graph is None:
             self.capture()
+        if steps % self.graph_tokens:
+            raise ValueError(f'steps must be a multiple of the {self.graph_tokens} tokens per captured graph')
         start = int(self.pos.item())
         if start + steps > self.capacity:
             raise ValueError(f'{steps} steps from position {start} exceed the KV capacity {self.capacity}')
-        for _ in range(steps):
+        for _ in range(steps // self.graph_tokens):
             self.graph.replay()
         return self.tokens[start:start + steps].tolist()

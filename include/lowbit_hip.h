@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define LB_ABI_VERSION 1
+#define LB_ABI_VERSION 2
 
 typedef enum lb_status {
   LB_OK = 0,
@@ -63,6 +63,18 @@ typedef enum lb_format {
 #define LB_FLAG_FORCE_GEMV    0x1u /* decode-regime kernel regardless of M (M <= 32) */
 #define LB_FLAG_FORCE_GEMM    0x2u /* prefill-regime MFMA GEMM regardless of M */
 #define LB_FLAG_FORCE_GENERIC 0x4u /* shape-agnostic fallback kernel (any N, K, group) */
+/* One fp16 product per group of K, summed by a balanced fp16 add tree (neighbours pair up,
+ * an odd last piece moves up unpaired), then + bias: the compact_groups graph of the
+ * reference (torch_npu_lowbit.py:235-256).  At most 32 groups; no correction.  With one
+ * group the call is the default linear, as in the reference. */
+#define LB_FLAG_COMPACT_GROUPS 0x8u
+/* W8A8: int8 per-row weights (group_size == K) and activations quantized on the power-of-two
+ * grid activation_scale: qx = clip(rint(x / s_x), -128, 127); the weight grid has the
+ * zero point at code 128, step_n = (fp16(127 s_n) - fp16(-128 s_n)) / 255;
+ * y = fp16((sum_k qx.qw) * s_x * step_n) with an exact integer sum and one fp64 product,
+ * then fp16(y + b).  The FakeQuantize graph of torch_npu_lowbit.py:224-231 as validated by
+ * torch_npu_int8_demo.py:34-51.  No correction; K <= 131072. */
+#define LB_FLAG_W8A8 0x10u
 
 typedef struct lb_linear_args {
   uint32_t struct_size;     /* sizeof(lb_linear_args) */
@@ -84,6 +96,8 @@ typedef struct lb_linear_args {
   size_t workspace_bytes;   /* >= lb_workspace_bytes(args) */
   uint32_t flags;           /* LB_FLAG_* */
   uint32_t reserved;
+  float activation_scale;   /* LB_FLAG_W8A8: a power of two in [2^-24, 256] (ignored otherwise) */
+  uint32_t reserved2;
 } lb_linear_args;
 
 /* ABI version of the loaded library (LB_ABI_VERSION at build time). */
@@ -109,7 +123,9 @@ lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes);
  *   z = fp16(x.V^T), d = fp16(z.U^T), y = fp16(y + d).
  * Weight values: int8 with per-row scales use the exact product q*s
  * (acc * s in fp32); every other case uses fp16(q*s), the reference's
- * PackedWeight.dequantize() value.
+ * PackedWeight.dequantize() value.  LB_FLAG_COMPACT_GROUPS and LB_FLAG_W8A8 select the
+ * reference's compact_groups and activation_scale graphs (see the flags above); their
+ * workspace holds the fp16 partials [groups, M, N] or the quantized activations int8 [M, K].
  * Replaces the lowbit_linear graph of weight_graph()
  * (torch_npu_lowbit.py:189-277) executed through _C.run / run_many_impl
  * (npunlock-probe/torch-device/backend.cpp:253-348) and

@@ -11,6 +11,10 @@ the reference's CPU semantics from LCS-Official/torch-intel-npu:
                        correction z=fp16(x.V^T), d=fp16(z.U^T), y=fp16(y+d));
                        bias staging torch_npu_lowbit.py:262-266
   rounding budget      torch_npu_lowbit_demo.py:88-95
+  compact_linear       torch_npu_lowbit.py:235-256 (per-group fp16 products, balanced fp16
+                       add tree), bias :262-266
+  w8a8_linear          torch_npu_int8_demo.py:34-51 (linear_reference with an activation
+                       scale: the DPU's zero-point-128 weight grid), graph :224-231
 
 Pinning (what checks each function, see tests/test_oracle.py):
   pack/unpack   reference known answers (test_torch_npu_lowbit.py:36,41;
@@ -22,6 +26,14 @@ Pinning (what checks each function, see tests/test_oracle.py):
                 (|q| <= limit, s >= 2^-24, zero rows), reconstruction error bound.
   linear        textbook fp64 matmul of decoded weights, identity-input bit-exact case,
                 zero-factor correction leaves output unchanged, linearity.
+  compact_linear  one group equals linear; the reference's edge cases (all codes in two
+                groups with identity input bit-exact, zero weights, overflowing fp16
+                partials); the pairing order against an explicitly written tree on pieces
+                chosen so that sequential and other pairings round differently.
+  w8a8_linear   the reference's exact cases (all 256 weight codes, activation ties and
+                clipping, large-integer accumulation with cancellation, scale boundaries,
+                zero weights), a pure-Python integer brute force on small shapes, and the
+                quantization error bound against the unquantized product.
 """
 import numpy as np
 
@@ -172,3 +184,65 @@ def rel_l2(actual, expected):
     e = np.asarray(expected, dtype=np.float64)
     denom = np.linalg.norm(e)
     return float(np.linalg.norm(a - e) / (denom if denom else 1.0))
+
+
+def _tree_sum(pieces):
+    """Balanced fp16 addition: neighbours pair up (0+1, 2+3, ...); an odd last piece moves up."""
+    with np.errstate(over='ignore', invalid='ignore'):
+        while len(pieces) > 1:
+            pieces = [_f16(pieces[i].astype(np.float64) + pieces[i + 1].astype(np.float64)) if i + 1 < len(pieces)
+                      else pieces[i] for i in range(0, len(pieces), 2)]
+    return pieces[0]
+
+
+def compact_linear(x, fmt, shape, group, data, scales_bytes, *, bias=None):
+    """compact_groups: y = tree(fp16(x_g . fp16(q s)_g^T) for each group g), then fp16(y + b).
+
+    With one group the reference builds the default graph (torch_npu_lowbit.py:235 tests
+    `groups > 1`), so that case is `linear`.  A partial that overflows fp16 stays +-inf
+    (the reference records this as a known limitation of compact graphs).
+    """
+    n, k = shape
+    groups = k // group
+    if groups == 1:
+        return linear(x, fmt, shape, group, data, scales_bytes, bias=bias)
+    x64 = np.asarray(x, dtype=np.float16).astype(np.float64)
+    w = dequantize(fmt, shape, group, data, scales_bytes).astype(np.float64)
+    with np.errstate(over='ignore', invalid='ignore'):
+        pieces = [_f16(x64[:, g * group:(g + 1) * group] @ w[:, g * group:(g + 1) * group].T) for g in range(groups)]
+        y = _tree_sum(pieces)
+        if bias is not None:
+            y = _f16(y.astype(np.float64) + np.asarray(bias, np.float16).astype(np.float64))
+    return y
+
+
+def w8a8_weight_steps(scales_bytes):
+    """Per-row weight step of the W8A8 grid: (fp16(127 s) - fp16(-128 s)) / 255 in fp64."""
+    s = np.frombuffer(scales_bytes, dtype=np.float16).astype(np.float64)
+    with np.errstate(over='ignore'):
+        low = (-128 * s).astype(np.float16).astype(np.float64)
+        high = (127 * s).astype(np.float16).astype(np.float64)
+    return (high - low) / 255
+
+
+def quantize_activations(x, activation_scale):
+    """clip(rint(x / s_x), -128, 127) as int64 (s_x a power of two, so x / s_x is exact)."""
+    return np.clip(np.rint(np.asarray(x, np.float16).astype(np.float64) / activation_scale), -128, 127).astype(np.int64)
+
+
+def w8a8_linear(x, shape, data, scales_bytes, activation_scale, *, bias=None):
+    """W8A8 linear: y = fp16((sum_k qx qw) * s_x * step_n), fp16(y + b) with a bias.
+
+    qx = clip(rint(x / s_x), -128, 127); qw the stored int8 codes (per-row scales); the integer
+    sum is exact and the scaling one fp64 product, in the reference's order
+    (torch_npu_int8_demo.py:41-51).
+    """
+    n, k = shape
+    qx = quantize_activations(x, activation_scale)
+    qw = np.frombuffer(data, dtype=np.int8).reshape(n, k).astype(np.int64)
+    acc = qx @ qw.T
+    with np.errstate(over='ignore', invalid='ignore'):
+        y = _f16(acc.astype(np.float64) * activation_scale * w8a8_weight_steps(scales_bytes)[None, :])
+        if bias is not None:
+            y = _f16(y.astype(np.float64) + np.asarray(bias, np.float16).astype(np.float64))
+    return y

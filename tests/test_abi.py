@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches_header():
     # struct_size is checked by the library: a wrong Python mirror is rejected as too small.
-    assert ctypes.sizeof(lowbit_hip.LinearArgs) == 8 + 8 * 4 + 8 * 2 + 8 * 2 + 8 * 2 + 8 + 8 * 3 + 8 + 8 + 8 + 8
+    assert ctypes.sizeof(lowbit_hip.LinearArgs) == 8 + 8 * 4 + 8 * 2 + 8 * 2 + 8 * 2 + 8 + 8 * 3 + 8 + 8 + 8 + 8 + 8
     assert ctypes.sizeof(lowbit_hip.FusedProblem) == 10 * 8
     assert ctypes.sizeof(lowbit_hip.FusedLinearArgs) == 8 + 8 + 8 + 8 + 3 * 8 + 8 + 3 * 80
     assert ctypes.sizeof(lowbit_hip.DecodeAttentionArgs) == 8 + 4 * 8 + 9 * 8 + 8
@@ -209,3 +209,51 @@ def test_argmax_next_argument_errors():
         bad = list(ok)
         bad[index] = value
         assert lib.lb_argmax_next(*bad, None) == lowbit_hip.INVALID_ARGUMENT, (index, value)
+
+
+W8 = dict(format=0, group_size=128, K=128, flags=lowbit_hip.FLAG_W8A8, activation_scale=1 / 128)
+
+
+@pytest.mark.parametrize('over,status,needle', [
+    (dict(flags=0x40), lowbit_hip.INVALID_ARGUMENT, 'unknown flags'),
+    # compact groups (reference QuantizedLinear: at most 32 groups, packed weights only)
+    (dict(K=4096, ldx=4096, group_size=32, flags=lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.INVALID_ARGUMENT,
+     'at most 32 groups'),
+    (dict(format=3, flags=lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.INVALID_ARGUMENT, 'packed'),
+    (dict(flags=lowbit_hip.FLAG_COMPACT_GROUPS, rank=4, down=0x50000, up=0x60000, up_ld=4), lowbit_hip.UNSUPPORTED,
+     'correction'),
+    # W8A8 (reference _activation_scale, torch_npu_lowbit.py:155-166)
+    (dict(W8, format=1), lowbit_hip.INVALID_ARGUMENT, 'per-channel int8'),
+    (dict(W8, group_size=64), lowbit_hip.INVALID_ARGUMENT, 'per-channel int8'),
+    (dict(W8, flags=lowbit_hip.FLAG_W8A8 | lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.INVALID_ARGUMENT,
+     'no compact groups'),
+    (dict(W8, activation_scale=3 / 256), lowbit_hip.INVALID_ARGUMENT, 'power of two'),
+    (dict(W8, activation_scale=512.0), lowbit_hip.INVALID_ARGUMENT, 'power of two'),
+    (dict(W8, activation_scale=2.0 ** -25), lowbit_hip.INVALID_ARGUMENT, 'power of two'),
+    (dict(W8, activation_scale=float('inf')), lowbit_hip.INVALID_ARGUMENT, 'power of two'),
+    (dict(W8, rank=4, down=0x50000, up=0x60000, up_ld=4), lowbit_hip.UNSUPPORTED, 'correction'),
+    (dict(W8, K=131136, ldx=131136, group_size=131136, N=1, ldy=1, codes=0x1000000, scales=0x2000000, x=0x3000000,
+          y=0x4000000), lowbit_hip.UNSUPPORTED, 'K <='),
+    (dict(W8, K=96, ldx=96, group_size=96, flags=lowbit_hip.FLAG_W8A8 | lowbit_hip.FLAG_FORCE_GEMV),
+     lowbit_hip.UNSUPPORTED, 'K % 64'),
+])
+def test_variant_argument_errors(over, status, needle):
+    got, _, message = workspace(args(**over))
+    assert got == status, message
+    assert needle in message
+
+
+def test_variant_workspace_sizes():
+    # compact: fp16 pieces [groups, M, N]; one group is the default graph (no workspace at M=1)
+    status, size, message = workspace(args(M=3, flags=lowbit_hip.FLAG_COMPACT_GROUPS))
+    assert status == 0, message
+    assert size == (128 // 32) * 3 * 64 * 2
+    status, size, _ = workspace(args(group_size=128, flags=lowbit_hip.FLAG_COMPACT_GROUPS))
+    assert (status, size) == (0, 0)
+    # W8A8 with K % 64 == 0: the quantized activations int8 [M, K], 256-byte rounded
+    status, size, message = workspace(args(M=5, **W8))
+    assert status == 0, message
+    assert size == 5 * 128 + 128  # 640 rounded up to 768
+    # W8A8 on the generic path (K not a multiple of 64) quantizes as it reads: no workspace
+    status, size, _ = workspace(args(M=5, **dict(W8, K=96, ldx=96, group_size=96)))
+    assert (status, size) == (0, 0)

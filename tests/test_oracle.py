@@ -173,3 +173,148 @@ def test_fixtures_reproduce():
             kw['down'], kw['up'] = data[f'{name}/down'], data[f'{name}/up']
         y = o.linear(data[f'{name}/x'], fmt, (n, k), g, raw, scales, **kw)
         np.testing.assert_array_equal(y.view(np.uint16), data[f'{name}/y'].view(np.uint16), err_msg=name)
+
+
+# ---------------------------------------------------------------- compact_groups
+def test_compact_one_group_is_the_default_graph():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((3, 64)) / 8).astype(np.float16)
+    for fmt in ('int4', 'nf4', 'int8'):
+        data, scales = o.quantize(rng.standard_normal((5, 64)) / 8, fmt, None)
+        np.testing.assert_array_equal(o.compact_linear(x, fmt, (5, 64), 64, data, scales),
+                                      o.linear(x, fmt, (5, 64), 64, data, scales))
+
+
+def test_compact_reference_edges():
+    # all 16 codes split over two groups of 8, identity input: the output is dequantize()^T bit
+    # for bit (torch_npu_lowbit_group_demo.py edges, 'all_codes_two_groups')
+    codes = o.pack(np.arange(16, dtype=np.uint8))
+    for fmt in ('int4', 'nf4'):
+        for scale in (0.125, 1.0, 16.0):
+            scales = np.full(2, scale, np.float16).tobytes()
+            got = o.compact_linear(np.eye(16, dtype=np.float16), fmt, (1, 16), 8, codes, scales)
+            want = o.dequantize(fmt, (1, 16), 8, codes, scales).T
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+        # zero weights in groups of 3 ('odd_group_zero')
+        data, scales = o.quantize(np.zeros((5, 9), np.float32), fmt, 3)
+        assert not o.compact_linear(np.ones((7, 9), np.float16), fmt, (5, 9), 3, data, scales).any()
+    # a finite full product whose fp16 partials overflow ('partial_overflow_limitation')
+    for fmt, pos, neg, act, sc in (('int4', 7, 13, 1024.0, [1.0, 2.0]), ('nf4', 15, 0, 4096.0, [1.0, 0.5])):
+        data = o.pack(np.array([pos] * 16 + [neg] * 16, np.uint8))
+        scales = np.array(sc, np.float16).tobytes()
+        x = np.full((1, 32), act, np.float16)
+        full = o.linear(x, fmt, (1, 32), 16, data, scales)
+        expected = float((x.astype(np.float64) @ o.dequantize(fmt, (1, 32), 16, data, scales).astype(np.float64).T)[0, 0])
+        assert float(full[0, 0]) == expected
+        assert float(o.compact_linear(x, fmt, (1, 32), 16, data, scales)[0, 0]) != expected
+
+
+def _pieces_weight(values, group=32):
+    """int8 weight row whose group g sums to values[g] against an all-ones input (scales 1)."""
+    codes = np.zeros((1, group * len(values)), np.int8)
+    for g, v in enumerate(values):
+        q, r = divmod(v, group)
+        codes[0, g * group:(g + 1) * group] = q
+        codes[0, g * group:g * group + r] += 1
+    return codes.tobytes(), np.ones(len(values), np.float16).tobytes()
+
+
+def test_compact_tree_pairs_neighbours():
+    f = lambda v: float(np.float16(v))
+    # eight pieces: ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)); sequential addition would give 2048
+    data, scales = _pieces_weight([2048] + [1] * 7)
+    x = np.ones((1, 256), np.float16)
+    tree = f(f(f(2048 + 1) + f(1 + 1)) + f(f(1 + 1) + f(1 + 1)))
+    assert tree == 2054.0
+    assert float(o.compact_linear(x, 'int8', (1, 256), 32, data, scales)[0, 0]) == tree
+    assert float(o.linear(x, 'int8', (1, 256), 32, data, scales)[0, 0]) == 2056.0  # one fp16 rounding
+    # five pieces: the odd last piece moves up unpaired: ((p0+p1)+(p2+p3))+p4
+    data, scales = _pieces_weight([2048, 1, 1, 1, 1])
+    x = np.ones((1, 160), np.float16)
+    tree = f(f(f(2048 + 1) + f(1 + 1)) + 1)
+    assert float(o.compact_linear(x, 'int8', (1, 160), 32, data, scales)[0, 0]) == tree == 2052.0
+    # three pieces with bias: fp16(fp16((p0+p1)+p2) + b)
+    data, scales = _pieces_weight([2048, 1, 3])
+    x = np.ones((1, 96), np.float16)
+    got = o.compact_linear(x, 'int8', (1, 96), 32, data, scales, bias=np.array([1.0], np.float16))
+    assert float(got[0, 0]) == f(f(f(2048 + 1) + 3) + 1)
+
+
+# ---------------------------------------------------------------- W8A8 (activation_scale)
+def test_w8a8_all_weight_codes_exact():
+    # torch_npu_int8_demo.py 'w8a8_all_weight_codes': identity input, activation scale 1/64
+    codes = np.arange(-128, 128, dtype=np.int8)
+    for sc in (0.125, 1.0, 16.0):
+        got = o.w8a8_linear(np.eye(256, dtype=np.float16), (1, 256), codes.tobytes(), np.float16(sc).tobytes(), 1 / 64)
+        np.testing.assert_array_equal(got.ravel().astype(np.float64), codes.astype(np.float64) * sc)
+
+
+def test_w8a8_activation_ties_and_clipping():
+    # 'all_activation_codes_ties_clipping': identity int8 weights, unit scales, activation 1/128
+    grid = np.arange(-128, 128, dtype=np.float64) / 128
+    x = np.stack((grid, grid + 1 / 256, grid - 1 / 256, grid * 2)).astype(np.float16)
+    eye = np.eye(256, dtype=np.int8).tobytes()
+    got = o.w8a8_linear(x, (256, 256), eye, np.ones(256, np.float16).tobytes(), 1 / 128)
+    # independent expectation: Python's round() is half-to-even on exact binary fractions
+    want = [[max(-128, min(127, round(float(v) * 128))) / 128 for v in row] for row in x]
+    np.testing.assert_array_equal(got.astype(np.float64), np.array(want))
+    assert got[1, 128] == 0 and got[1, 129] == np.float16(2 / 128)  # 0.5 -> 0, 1.5 -> 2
+    assert got[3].max() == np.float16(127 / 128) and got[3].min() == -1.0  # clipping
+
+
+def test_w8a8_large_integer_accumulation():
+    # 'large_integer_accumulation_cancellation': K=4096, |sum| above 2^24 stays exact
+    codes = np.stack((np.full(4096, 127, np.int8), np.tile([127, -127], 2048).astype(np.int8)))
+    scales = np.full(2, 1 / 128, np.float16).tobytes()
+    got = o.w8a8_linear(np.full((1, 4096), 127 / 128, np.float16), (2, 4096), codes.tobytes(), scales, 1 / 128)
+    # 4096*127*127 / 128 * step, step = (fp16(127/128) + 1) / 255 = 1/128 -> 4032.25 -> fp16 4032
+    assert got.tolist() == [[4032.0, 0.0]]
+
+
+def test_w8a8_scale_boundaries_and_zero():
+    eye = np.eye(16, dtype=np.int8).tobytes()
+    ones = np.ones(16, np.float16).tobytes()
+    for s in (2.0 ** -24, 2.0 ** -14, 256.0):
+        x = (np.arange(-8, 8, dtype=np.float64) * s).astype(np.float16).reshape(1, 16)
+        np.testing.assert_array_equal(o.w8a8_linear(x, (16, 16), eye, ones, s), x)
+    data, scales = o.quantize(np.zeros((3, 17), np.float32), 'int8')
+    assert not o.w8a8_linear(np.ones((2, 17), np.float16), (3, 17), data, scales, 1 / 128).any()
+
+
+def test_w8a8_integer_brute_force():
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    for m, k, n, sx in ((1, 17, 3, 1 / 128), (5, 64, 32, 1 / 256), (7, 64, 13, 1 / 128)):
+        data, scales = o.quantize(rng.standard_normal((n, k)) / 8, 'int8')
+        x = (rng.standard_normal((m, k)) / 8).astype(np.float16)
+        bias = (rng.standard_normal(n) / 8).astype(np.float16)
+        got = o.w8a8_linear(x, (n, k), data, scales, sx, bias=bias)
+        codes = np.frombuffer(data, np.int8).reshape(n, k)
+        s16 = np.frombuffer(scales, np.float16)
+        for i in range(m):
+            qx = [max(-128, min(127, round(Fraction(float(v)) / Fraction(sx)))) for v in x[i]]
+            for j in range(n):
+                acc = sum(a * int(b) for a, b in zip(qx, codes[j]))
+                hi = Fraction(float(np.float16(127 * float(s16[j]))))
+                lo = Fraction(float(np.float16(-128 * float(s16[j]))))
+                step = float((hi - lo) / 255)          # fp64 division, as the reference
+                r = float(Fraction(acc) * Fraction(sx)) * step  # exact acc*sx, one fp64 product
+                y = np.float16(r)
+                y = np.float16(float(y) + float(bias[j]))
+                assert got[i, j].view(np.uint16) == y.view(np.uint16), (m, k, n, i, j)
+
+
+def test_w8a8_quantization_error_bound():
+    rng = np.random.default_rng(12)
+    n, k, sx = 24, 256, 1 / 128
+    data, scales = o.quantize(rng.standard_normal((n, k)) / 8, 'int8')
+    x = (rng.standard_normal((4, k)) / 8).astype(np.float16)
+    got = o.w8a8_linear(x, (n, k), data, scales, sx).astype(np.float64)
+    w = o.exact_weight('int8', (n, k), k, data, scales)
+    ideal = x.astype(np.float64) @ w.T
+    qw = np.frombuffer(data, np.int8).reshape(n, k).astype(np.float64)
+    step = o.w8a8_weight_steps(scales)
+    xq = o.quantize_activations(x, sx) * sx
+    bound = (sx / 2) * np.abs(w).sum(1)[None, :] + np.abs(xq) @ (np.abs(qw) * np.abs(step - np.frombuffer(scales, np.float16))[:, None]).T
+    bound += np.finfo(np.float16).eps * np.abs(got) + 1e-6
+    assert (np.abs(got - ideal) <= bound).all()

@@ -160,7 +160,24 @@ struct LinearParams {
   int per_row;            // int8 with one scale per row: scale applied to the fp32 sum
   int group_shift;        // scale index = k >> group_shift (31 when group == K)
   int scales_aligned;     // scales pointer is 16-byte aligned
+  int code_ld;            // bytes per weight row (K * bits / 8; 2 * ldw for fp16 weights)
+  // Per grid-z-slice offsets (compact groups: slice z computes group z into its own fp16
+  // partial output); all zero for a single product.
+  int z_x, z_codes, z_scales;
+  long long z_y;
+  float act_scale;        // W8A8: the activation grid (a power of two)
+  const int8_t *xq;       // W8A8: quantized activations [M, K] (row stride K)
+  int slices;             // grid z extent (host side: the launchers read it)
 };
+
+// Moves p to grid slice blockIdx.z (a no-op when the launch has one slice).
+__device__ __forceinline__ void select_slice(LinearParams &p) {
+  const int z = blockIdx.z;
+  p.x += (size_t)z * p.z_x;
+  p.codes += (size_t)z * p.z_codes;
+  p.scales += (size_t)z * p.z_scales;
+  p.y += (size_t)z * p.z_y;
+}
 
 // Epilogue with the reference's staging (torch_npu_lowbit.py:262-266,
 // torch_npu_smollm.py:160-163): main -> fp16, + bias -> fp16, + fp16 correction -> fp16.

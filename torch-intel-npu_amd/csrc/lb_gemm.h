@@ -61,9 +61,10 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  select_slice(p);
 
   const int rows_a = min(BM, p.M - bm), rows_b = min(BN, p.N - bn);
-  const size_t row_bytes = T::BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * T::BITS / 8;
+  const size_t row_bytes = (size_t)p.code_ld;
   // Buffer views start at the tile's first row; rows past M / N are out of range (zeros).
   const __amdgpu_buffer_rsrc_t xbuf =
       buffer_rsrc(p.x + (size_t)bm * p.ldx, rows_a > 0 ? ((size_t)(rows_a - 1) * p.ldx + p.K) * 2 : 0);

@@ -3,8 +3,7 @@
 //   gemv_kernel    decode regime (M <= 32): packed rows streamed with 16-byte loads,
 //                  dequantized in registers, multiplied on v_mfma_f32_16x16x32_f16 with
 //                  the activations as the (zero padded) A operand; optional split-K.
-//   gemm_kernel    prefill regime: 128x128x32 tiles, activations and dequantized weights
-//                  staged in LDS, v_mfma_f32_32x32x16_f16, fp32 accumulation.
+//   (the prefill GEMM, gemm2_kernel, is in lb_gemm.h)
 //   generic_kernel any shape / group size (odd K, rows starting mid-byte, groups < 32).
 //   unpack_kernel, dequant_kernel   bit-exact decode used by tests and by callers that
 //                  want the reference's dequantized fp16 weights on device.
@@ -65,6 +64,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(LinearParams p, int 
   // Scales of this workgroup's rows for the current chunk: ROWS x sc_ld halves, zero padded
   // (rows past N and the 4 entries after the chunk's last group read as zero).
   f16 *ss = xs + (p.M + 1) * xs_ld;
+  select_slice(p);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: loop control stays uniform
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(LinearParams p, int 
   const int n = n0 + rg * 16 + j;
   const int ks = blockIdx.y * p.kslice;
   const int ke = min(p.K, ks + p.kslice);
-  const size_t row_bytes = BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * BITS / 8;
+  const size_t row_bytes = (size_t)p.code_ld;
   // Buffer views start at this workgroup's first row, so offsets stay 32-bit.
   const __amdgpu_buffer_rsrc_t wbuf =
       buffer_rsrc(p.codes + (size_t)n0 * row_bytes, (size_t)(p.N - n0) * row_bytes);
@@ -294,118 +294,6 @@ __device__ __forceinline__ h8 decode8_natural(uint32_t w0, uint32_t w1, h2 s2, c
   return __builtin_shufflevector(__builtin_shufflevector(p[0], p[1], 0, 1, 2, 3),
                                  __builtin_shufflevector(p[2], p[3], 0, 1, 2, 3),
                                  0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 32, kGemmLd = kGemmBK + 8;
-
-template <int FMT, bool SCALED>
-__global__ __launch_bounds__(256) void gemm_kernel(LinearParams p) {
-  constexpr int BM = kGemmBM, BN = kGemmBN, BK = kGemmBK, LD = kGemmLd;
-  __shared__ __align__(16) f16 As[BM * LD];
-  __shared__ __align__(16) f16 Bs[BN * LD];
-  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
-  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
-
-  // A: 128 rows x 64 bytes -> two 16-byte chunks per thread.
-  const int a_row0 = tid >> 2, a_col = (tid & 3) * 8;  // chunk tid and tid + 256 (row + 64)
-  // B: weights for 128 rows x 32 k.  Each thread produces 16 k of one row.
-  const int b_row = tid >> 1, b_k = (tid & 1) * 16;
-  const int bn_row = bn + b_row;
-  const bool b_ok = bn_row < p.N;
-  constexpr int BITS = FormatTraits<FMT>::BITS;
-  const size_t row_bytes = BITS == 16 ? (size_t)p.ldw * 2 : (size_t)p.K * BITS / 8;
-  const uint8_t *wrow = p.codes + (b_ok ? (size_t)bn_row * row_bytes : 0);
-  const f16 *srow = p.scales + (b_ok && SCALED ? (size_t)bn_row * p.G : 0);
-
-  h8 a_reg[2];
-  u4 b_reg;  // up to 16 bytes: 16 codes (4-bit uses 8 bytes, int8 16 bytes, fp16 32 -> two loads)
-  u4 b_reg2;
-  f16 b_scale = (f16)0.0f;
-
-  auto load_tile = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int m = bm + a_row0 + i * 64;
-      a_reg[i] = m < p.M ? *reinterpret_cast<const h8 *>(p.x + (size_t)m * p.ldx + k0 + a_col) : h8{};
-    }
-    const int k = k0 + b_k;
-    if constexpr (BITS == 4) {
-      const uint2 v = b_ok ? *reinterpret_cast<const uint2 *>(wrow + (size_t)k / 2) : uint2{0u, 0u};
-      b_reg = u4{v.x, v.y, 0u, 0u};
-    } else if constexpr (BITS == 8) {
-      b_reg = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k) : u4{0u, 0u, 0u, 0u};
-    } else {
-      b_reg = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k * 2) : u4{0u, 0u, 0u, 0u};
-      b_reg2 = b_ok ? *reinterpret_cast<const u4 *>(wrow + (size_t)k * 2 + 16) : u4{0u, 0u, 0u, 0u};
-    }
-    if constexpr (SCALED) b_scale = b_ok ? srow[k >> p.group_shift] : (f16)0.0f;
-  };
-
-  f16x acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
-
-  load_tile(0);
-  for (int k0 = 0; k0 < p.K; k0 += BK) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<h8 *>(&As[(a_row0 + i * 64) * LD + a_col]) = a_reg[i];
-    {
-      const h2 s2 = {b_scale, b_scale};
-      h8 lo, hi;
-      if constexpr (BITS == 4) {
-        lo = decode8_natural<FMT, SCALED>(b_reg[0], 0u, s2, nf4_table);
-        hi = decode8_natural<FMT, SCALED>(b_reg[1], 0u, s2, nf4_table);
-      } else if constexpr (BITS == 8) {
-        lo = decode8_natural<FMT, SCALED>(b_reg[0], b_reg[1], s2, nf4_table);
-        hi = decode8_natural<FMT, SCALED>(b_reg[2], b_reg[3], s2, nf4_table);
-      } else {
-        lo = __builtin_bit_cast(h8, b_reg);
-        hi = __builtin_bit_cast(h8, b_reg2);
-      }
-      *reinterpret_cast<h8 *>(&Bs[b_row * LD + b_k]) = lo;
-      *reinterpret_cast<h8 *>(&Bs[b_row * LD + b_k + 8]) = hi;
-    }
-    __syncthreads();
-    if (k0 + BK < p.K) load_tile(k0 + BK);
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      h8 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const h8 *>(&As[(wm * 64 + i * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-        b[jj] = *reinterpret_cast<const h8 *>(&Bs[(wn * 64 + jj * 32 + (lane & 31)) * LD + kk + 8 * (lane >> 5)]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[jj], acc[i][jj], 0, 0, 0);
-    }
-  }
-
-  // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int n = bn + wn * 64 + jj * 32 + (lane & 31);
-      if (n >= p.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = bm + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < p.M) store_output(p, m, n, acc[i][jj][r]);
-      }
-    }
 }
 
 // Decoded integer value of element (n, k) for the flat packed layout.

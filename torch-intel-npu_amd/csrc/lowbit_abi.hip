@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <cmath>
 #include <cstdio>
 #include <string>
 
@@ -12,6 +13,7 @@
 #include "fused_launch.h"
 #include "lb_gemm.h"
 #include "lb_kernels.h"
+#include "lb_variants.h"
 
 using namespace lb;
 using namespace lb::abi;
@@ -19,6 +21,9 @@ using namespace lb::abi;
 namespace {
 
 enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3 };
+enum Variant { VAR_PLAIN = 0, VAR_COMPACT = 1, VAR_W8A8 = 2 };
+constexpr int kCompactMaxGroups = 32;
+constexpr int64_t kW8A8MaxK = 131072;  // |sum| <= K * 128 * 127 stays inside int32
 
 constexpr int kGemvMaxM = 32;
 constexpr size_t kGemvLdsBudget = 48 * 1024;
@@ -27,6 +32,8 @@ int codes_per_load(int fmt) { return fmt == FMT_FP16 ? 8 : fmt == FMT_INT8 ? 16 
 
 struct Plan {
   int path = PATH_GENERIC;
+  int variant = VAR_PLAIN;
+  size_t xq_off = 0, pieces_off = 0;
   int kg = 1, splits = 1, kslice = 0, kc = 0;
   size_t z_off = 0, z_bytes = 0;
   size_t d_off = 0, d_bytes = 0;
@@ -107,6 +114,42 @@ bool row_eligible(const lb_linear_args *a) {
   const int64_t up_ld = a->up_ld == 0 ? a->rank : a->up_ld;
   if (a->rank > 0 && (!aligned(a->down, 16) || !aligned(a->up, 16) || up_ld % 8 != 0)) return false;
   return true;
+}
+
+// Workspace and kernel path of the compact_groups and W8A8 variants.
+Plan make_variant_plan(const lb_linear_args *a, int variant) {
+  Plan pl;
+  pl.variant = variant;
+  const int fmt = (int)a->format;
+  bool eligible;
+  if (variant == VAR_W8A8) {
+    eligible = a->K % 64 == 0 && aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
+  } else {
+    // each group is a product of its own: K_group % 32 == 0 keeps its codes, scales and
+    // activations at 16-byte offsets
+    eligible = a->group_size % 32 == 0 && aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
+  }
+  if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) pl.path = PATH_GENERIC;
+  else if (a->flags & LB_FLAG_FORCE_GEMM) pl.path = PATH_GEMM;
+  else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) pl.path = PATH_GEMV;
+  else pl.path = PATH_GEMM;
+  size_t off = 0;
+  if (variant == VAR_W8A8 && pl.path != PATH_GENERIC) {
+    pl.xq_off = off;
+    off = round_up(off + (size_t)a->M * a->K, 256);
+  }
+  if (variant == VAR_COMPACT) {
+    pl.pieces_off = off;
+    off = round_up(off + (size_t)(a->K / a->group_size) * a->M * a->N * 2, 256);
+    if (pl.path == PATH_GEMV) {
+      const GemvShape gs = gemv_shape(fmt, a->M, a->N, a->group_size, false);
+      pl.kg = gs.kg;
+      pl.kc = gs.kc;
+    }
+  }
+  (void)fmt;
+  pl.total = off;
+  return pl;
 }
 
 Plan make_plan(const lb_linear_args *a, bool eligible) {
@@ -198,16 +241,47 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
     if (overlaps(inputs[6], inputs[i]))
       return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace overlaps %s", inputs[i].name);
 
-  const bool eligible = fast_eligible((int)a->format, a->K, dense ? a->K : a->group_size, a->codes, a->x, a->ldx, a->K);
+  if (a->flags & ~(LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear: unknown flags 0x%x", a->flags);
   if ((a->flags & LB_FLAG_FORCE_GEMV) && a->M > kGemvMaxM)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: LB_FLAG_FORCE_GEMV needs M <= %d", kGemvMaxM);
-  if ((a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM)) && !(a->flags & LB_FLAG_FORCE_GENERIC) && !eligible)
-    return fail(LB_UNSUPPORTED,
-                "lb_linear: forced MFMA path needs K %% 32 == 0, group == K or group %% 32 == 0, "
-                "16-byte aligned codes/x and ldx %% 8 == 0");
   if (__builtin_popcount(a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC)) > 1)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: at most one LB_FLAG_FORCE_* flag");
-  *plan = make_plan(a, eligible);
+  int variant = VAR_PLAIN;
+  if (a->flags & LB_FLAG_W8A8) {
+    // reference _activation_scale (torch_npu_lowbit.py:155-166)
+    const float s = a->activation_scale;
+    int exponent = 0;
+    if ((a->flags & LB_FLAG_COMPACT_GROUPS) || a->format != LB_FORMAT_INT8 || a->group_size != a->K)
+      return fail(LB_INVALID_ARGUMENT, "lb_linear: W8A8 requires per-channel int8 weights and no compact groups");
+    if (!std::isfinite(s) || s < 0x1p-24f || s > 511.0f || std::frexp(s, &exponent) != 0.5f)
+      return fail(LB_INVALID_ARGUMENT, "lb_linear: activation_scale must be a power of two in [2^-24, 511]");
+    if (a->rank > 0) return fail(LB_UNSUPPORTED, "lb_linear: W8A8 takes no low-rank correction");
+    if (a->K > kW8A8MaxK) return fail(LB_UNSUPPORTED, "lb_linear: W8A8 supports K <= %lld", (long long)kW8A8MaxK);
+    variant = VAR_W8A8;
+  } else if (a->flags & LB_FLAG_COMPACT_GROUPS) {
+    if (dense) return fail(LB_INVALID_ARGUMENT, "lb_linear: compact groups need a packed int8/int4/nf4 weight");
+    const int64_t groups = a->K / a->group_size;
+    if (groups > kCompactMaxGroups)
+      return fail(LB_INVALID_ARGUMENT, "lb_linear: compact groups support at most %d groups (got %lld)", kCompactMaxGroups,
+                  (long long)groups);
+    if (a->rank > 0) return fail(LB_UNSUPPORTED, "lb_linear: compact groups take no low-rank correction");
+    if (groups > 1) variant = VAR_COMPACT;  // one group: the default graph (torch_npu_lowbit.py:235)
+  }
+  if (variant != VAR_PLAIN) {
+    *plan = make_variant_plan(a, variant);
+    if ((a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM)) && plan->path == PATH_GENERIC)
+      return fail(LB_UNSUPPORTED, variant == VAR_W8A8
+                                      ? "lb_linear: W8A8 MFMA path needs K %% 64 == 0, 16-byte aligned codes/x and ldx %% 8 == 0"
+                                      : "lb_linear: compact MFMA path needs group %% 32 == 0, 16-byte aligned codes/x, ldx %% 8 == 0");
+  } else {
+    const bool eligible = fast_eligible((int)a->format, a->K, dense ? a->K : a->group_size, a->codes, a->x, a->ldx, a->K);
+    if ((a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM)) && !(a->flags & LB_FLAG_FORCE_GENERIC) && !eligible)
+      return fail(LB_UNSUPPORTED,
+                  "lb_linear: forced MFMA path needs K %% 32 == 0, group == K or group %% 32 == 0, "
+                  "16-byte aligned codes/x and ldx %% 8 == 0");
+    *plan = make_plan(a, eligible);
+  }
   if (check_workspace && plan->total > 0) {
     if (!a->workspace || a->workspace_bytes < plan->total)
       return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace of %zu bytes required (got %zu)", plan->total,
@@ -220,7 +294,7 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
 template <int FMT, int MT, int KG, bool SCALED>
 void launch_gemv_t(const LinearParams &p, int kc, hipStream_t s) {
   constexpr int rows = 16 * (kGemvWaves / KG);
-  const dim3 grid((p.N + rows - 1) / rows, p.splits);
+  const dim3 grid((p.N + rows - 1) / rows, p.splits, p.slices);
   // Staged scales per row: the chunk's groups plus 4 zero entries for tail lanes.
   const int sc_ld = SCALED ? (p.group_shift >= 31 ? 1 : (kc >> p.group_shift) + 2) + 4 : 0;
   const size_t stage = (size_t)(p.M + 1) * (kc + 4 * codes_per_load(FMT) + 8) * 2 + (size_t)rows * sc_ld * 2;
@@ -279,16 +353,16 @@ void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kg, int kc, hi
 template <int FMT, bool SCALED>
 void launch_gemm_t(const LinearParams &p, hipStream_t s) {
   constexpr int BM = LB_GEMM_BM, BN = LB_GEMM_BN, BK = LB_GEMM_BK;
-  const int64_t big = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const int64_t big = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * p.slices;
   if (big >= 256 && p.K % BK == 0) {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM),
-                       dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>),
+                       dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, p.slices), dim3(256), 0, s, p);
   } else if (p.K % 64 == 0) {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64), dim3(256), 0,
-                       s, p);
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64, p.slices),
+                       dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64), dim3(256), 0,
-                       s, p);
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64, p.slices),
+                       dim3(256), 0, s, p);
   }
 }
 
@@ -325,6 +399,8 @@ LinearParams base_params(int fmt, int64_t M, int64_t N, int64_t K, int64_t group
   p.scales_aligned = aligned(scales, 16);
   p.splits = 1;
   p.kslice = (int)K;
+  p.code_ld = (int)(fmt == FMT_FP16 ? ldw * 2 : fmt == FMT_INT8 ? K : K / 2);
+  p.slices = 1;
   return p;
 }
 
@@ -341,6 +417,66 @@ void dense_fp16(int64_t M, int64_t N, int64_t K, const void *w, int64_t ldw, con
   } else {
     launch_gemm(FMT_FP16, false, p, s);
   }
+}
+
+// W8A8: quantize the activations into the workspace, then the int8 MFMA GEMV / GEMM (or the
+// generic kernel, which quantizes as it reads).
+void launch_w8a8(const lb_linear_args *a, const Plan &pl, LinearParams p, hipStream_t s) {
+  p.act_scale = a->activation_scale;
+  if (pl.path == PATH_GENERIC) {
+    hipLaunchKernelGGL(generic_w8a8_kernel, dim3(p.N, (p.M + 7) / 8), dim3(64), 0, s, p);
+    return;
+  }
+  p.xq = reinterpret_cast<const int8_t *>(static_cast<uint8_t *>(a->workspace) + pl.xq_off);
+  const size_t blocks = (size_t)p.M * (p.K / 8);
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, p);
+  if (pl.path == PATH_GEMV) {
+    const dim3 grid((p.N + 15) / 16);
+    if (p.M <= 16)
+      hipLaunchKernelGGL(i8_gemv_kernel<1>, grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(i8_gemv_kernel<2>, grid, dim3(256), 0, s, p);
+  } else if (((int64_t)(p.M + 127) / 128) * ((p.N + 127) / 128) >= 256) {
+    hipLaunchKernelGGL((i8_gemm_kernel<128, 128>), dim3((p.N + 127) / 128, (p.M + 127) / 128), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((i8_gemm_kernel<64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64), dim3(256), 0, s, p);
+  }
+}
+
+// compact_groups: the fp16 product of each group into pieces[group, M, N] (the GEMV / GEMM
+// kernels on grid slice z = group, or the generic kernel), then the balanced add tree + bias.
+void launch_compact(const lb_linear_args *a, const Plan &pl, const LinearParams &p, hipStream_t s) {
+  const int fmt = (int)a->format;
+  const int groups = (int)(a->K / a->group_size);
+  f16 *pieces = reinterpret_cast<f16 *>(static_cast<uint8_t *>(a->workspace) + pl.pieces_off);
+  LinearParams q = p;
+  q.per_row = 0;  // each piece multiplies by fp16(q*s): the group's Convert + Multiply (:249-251)
+  q.bias = nullptr;
+  if (pl.path == PATH_GENERIC) {
+    hipLaunchKernelGGL(generic_pieces_kernel, dim3(p.N, (p.M + 7) / 8, groups), dim3(64), 0, s, q, fmt, pieces);
+  } else {
+    const int bits = fmt == FMT_INT8 ? 8 : 4;
+    q.K = (int)a->group_size;
+    q.group_shift = 31;  // one scale per row of a piece: index k >> 31 == 0
+    q.kslice = q.K;
+    q.splits = 1;
+    q.code_ld = (int)(a->K * bits / 8);
+    q.scales_aligned = 0;
+    q.y = pieces;
+    q.ldy = p.N;
+    q.z_x = q.K;
+    q.z_codes = q.K * bits / 8;
+    q.z_scales = 1;
+    q.z_y = (long long)p.M * p.N;
+    q.slices = groups;
+    if (pl.path == PATH_GEMV)
+      launch_gemv(fmt, true, q, pl.kg, pl.kc, s);
+    else
+      launch_gemm(fmt, true, q, s);
+  }
+  const size_t count = (size_t)p.M * p.N;
+  hipLaunchKernelGGL(compact_tree_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p,
+                     (const f16 *)pieces, groups);
 }
 
 lb_status launch_status(const char *what) {
@@ -388,6 +524,14 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
   LinearParams p = base_params(fmt, a->M, a->N, a->K, dense ? a->K : a->group_size, a->codes, a->scales, a->x,
                                a->ldx, a->y, a->ldy, a->K);
   p.bias = static_cast<const f16 *>(a->bias);
+  if (plan.variant == VAR_W8A8) {
+    launch_w8a8(a, plan, p, s);
+    return launch_status("lb_linear");
+  }
+  if (plan.variant == VAR_COMPACT) {
+    launch_compact(a, plan, p, s);
+    return launch_status("lb_linear");
+  }
   if (plan.path == PATH_ROW) {
     const bool scaled = !dense && !p.per_row;
     FusedParams fp{};

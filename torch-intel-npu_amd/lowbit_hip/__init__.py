@@ -16,10 +16,11 @@ import torch
 
 LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve().parent.parent / 'liblowbit_hip.so'))
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC = 0x1, 0x2, 0x4
+FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_workspace_bytes', 'lb_linear',
            'lb_unpack_codes', 'lb_dequantize')
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
@@ -39,7 +40,8 @@ class LinearArgs(ctypes.Structure):
                 ('rank', ctypes.c_int64), ('down', ctypes.c_void_p), ('up', ctypes.c_void_p),
                 ('up_ld', ctypes.c_int64),
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t),
-                ('flags', ctypes.c_uint32), ('reserved', ctypes.c_uint32)]
+                ('flags', ctypes.c_uint32), ('reserved', ctypes.c_uint32),
+                ('activation_scale', ctypes.c_float), ('reserved2', ctypes.c_uint32)]
 
 
 class FusedProblem(ctypes.Structure):
@@ -138,7 +140,7 @@ def _device_tensor(t, name, dtype=None):
 
 
 def make_args(x, codes, scales, *, format, N, K, group_size, y, bias=None, down=None, up=None, rank=0,
-              flags=0):
+              flags=0, activation_scale=None):
     """Fill an lb_linear_args for device tensors; x and y are 2-D views with unit column stride."""
     args = LinearArgs()
     args.struct_size = ctypes.sizeof(LinearArgs)
@@ -154,6 +156,9 @@ def make_args(x, codes, scales, *, format, N, K, group_size, y, bias=None, down=
         args.down, args.up = _ptr(down), _ptr(up)
         args.up_ld = up.stride(0)
     args.flags = flags
+    if activation_scale is not None:
+        args.flags |= FLAG_W8A8
+        args.activation_scale = activation_scale
     return args
 
 
@@ -164,11 +169,12 @@ def workspace_bytes(args):
 
 
 def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, up=None, rank=0, flags=0,
-           out=None, workspace=None):
+           out=None, workspace=None, activation_scale=None):
     """y[M,N] fp16 = x . dequant(W)^T (+bias) (+fp16(fp16(x.V^T).U^T)) on the current stream.
 
     x: fp16 [M,K] cuda (unit column stride).  codes: uint8 (or fp16 for format='fp16').
     scales: fp16 [N, K/group_size].  down: fp16 [rank,K] (row stride K); up: fp16 [N, >=rank].
+    flags may add FLAG_COMPACT_GROUPS; activation_scale (a power of two) selects W8A8.
     """
     _device_tensor(x, 'x', torch.float16)
     if x.ndim != 2 or x.shape[1] != K:
@@ -183,7 +189,7 @@ def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, 
     M = x.shape[0]
     y = torch.empty((M, N), dtype=torch.float16, device=x.device) if out is None else out
     args = make_args(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=y, bias=bias,
-                     down=down, up=up, rank=rank, flags=flags)
+                     down=down, up=up, rank=rank, flags=flags, activation_scale=activation_scale)
     need = workspace_bytes(args)
     if need:
         if workspace is None or workspace.numel() < need:
@@ -221,7 +227,7 @@ class PreparedLinear:
     """
 
     def __init__(self, x, codes, scales, *, format, N, K, group_size, out, bias=None, down=None, up=None,
-                 rank=0, flags=0, workspace=None):
+                 rank=0, flags=0, workspace=None, activation_scale=None):
         _device_tensor(x, 'x', torch.float16)
         _device_tensor(out, 'out', torch.float16)
         if x.ndim != 2 or x.shape[1] != K or (K > 1 and x.stride(1) != 1):
@@ -230,7 +236,8 @@ class PreparedLinear:
             raise ValueError('PreparedLinear needs out [M, N] with unit column stride')
         self._keep = [x, codes, scales, out, bias, down, up]
         self.args = make_args(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out,
-                              bias=bias, down=down, up=up, rank=rank, flags=flags)
+                              bias=bias, down=down, up=up, rank=rank, flags=flags,
+                              activation_scale=activation_scale)
         need = workspace_bytes(self.args)
         if need:
             if workspace is None or workspace.numel() < need:

@@ -276,11 +276,13 @@ class QuantizedLinear(torch.nn.Module):
         return self._bias_device[key]
 
     def forward(self, x):
+        """y = x . W^T (+ bias) in fp16 (reference :339-360).  compact_groups selects the per-group
+        fp16 products and balanced add tree of the reference's compact graph (:235-256);
+        activation_scale selects W8A8 (:224-231), int8 activations on that power-of-two grid."""
         n, k = self._weight.shape
         _validate_activation(x, k)
-        if self._compact_groups or self._activation_scale is not None:
-            raise NotImplementedError('compact_groups / activation_scale (W8A8) are not implemented on the '
-                                      'HIP path yet')
         codes, scales = self._weight.device_tensors(x.device)
+        flags = lowbit_hip.FLAG_COMPACT_GROUPS if self._compact_groups else 0
         return lowbit_hip.linear(x, codes, scales, format=self._weight.format, N=n, K=k,
-                                 group_size=self._weight.group_size, bias=self._device_bias(x.device))
+                                 group_size=self._weight.group_size, bias=self._device_bias(x.device),
+                                 flags=flags, activation_scale=self._activation_scale)

@@ -48,6 +48,10 @@ CASES = [
     ('nf4', 64, 1024, 'rmsnorm', (40, 300), 24, False, True),
     ('fp16', None, 576, 'rmsnorm', (4096,), 0, False, False),            # tied-head shape (smaller N)
     ('fp16', None, 1536, 'silu_mul', (64, 64), 8, True, False),
+    # one problem over many rows (rows_gemv_kernel): the full tied head, epilogue operands, 2 tiles
+    ('fp16', None, 576, 'rmsnorm', (49152,), 0, False, False),
+    ('int8', None, 1536, 'silu_mul', (32768,), 0, True, True),
+    ('int4', 64, 576, 'none', (16400,), 0, True, False),
 ]
 
 

@@ -195,6 +195,19 @@ SHAPES = [
     ('int8', 1, 300, 8192, 8192),     # one row, long K, per-row W8
     ('nf4', 1, 64, 5000 // 32 * 32, 64),
     ('int4', 1, 100, 4096, 32),       # one row, long K, group 32: falls back to the split GEMV
+    # several rows and a large weight: 64-row workgroups, K split across workgroups
+    ('int4', 8, 4096, 4096, 128),
+    ('int4', 32, 2048, 4096, 64),
+    ('int8', 16, 2048, 1536, 1536),
+    ('nf4', 5, 1000, 8192, 128),      # N not a multiple of 64
+    ('int8', 3, 1100, 2048, 64),      # grouped int8
+    ('int4', 8, 40000, 1024, 128),    # enough 64-row tiles to fill the chip: no K split
+    ('nf4', 16, 33000, 2048, 64),     # no K split, K walked in LDS chunks
+    # one row over many rows: several 16-row tiles per workgroup (rows_gemv_kernel)
+    ('int4', 1, 49152, 576, 64),      # config-2 lm_head: 4 tiles per workgroup
+    ('int8', 1, 33000, 1024, 1024),   # per-row W8, partial last workgroup (a wave past N)
+    ('nf4', 1, 20000, 4096, 128),     # 2 tiles per workgroup, waves split K in two
+    ('int4', 1, 32768, 2048, 128),    # 32 loads per lane
 ]
 
 

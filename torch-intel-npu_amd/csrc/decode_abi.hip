@@ -118,9 +118,39 @@ void launch_fused_r(const FusedParams &p, int tiles, hipStream_t s) {
   }
 }
 
-// RANKED instantiations carry the correction (V and U loads); the others have none at all.
+#ifndef LB_ROWS_MIN_WGS
+#define LB_ROWS_MIN_WGS 512  // rows_gemv_kernel only when it still gives this many workgroups
+#endif
+
+template <int FMT, bool SCALED, int KMAX, int RG>
+bool launch_rows_k(const FusedParams &p, int tiles, hipStream_t s) {
+  constexpr int WSTEP = (4 / RG) * 4 * FormatTraits<FMT>::CPL;
+  if constexpr ((KMAX + WSTEP - 1) / WSTEP <= 32) {  // all of a lane's loads fit in registers
+    hipLaunchKernelGGL((rows_gemv_kernel<FMT, SCALED, KMAX, RG>), dim3((tiles + RG - 1) / RG), dim3(256), 0, s, p);
+    return true;
+  }
+  return false;
+}
+
+// RG tiles per workgroup for the shortest staged row that holds K (false: not available).  Used
+// for int4 and fp16 rows of up to 1536 k, where it measured faster than the single-tile kernel
+// (int8 and nf4 weights, and longer rows whose loads no longer fit in few registers, did not).
+template <int FMT, bool SCALED, int RG>
+bool launch_rows(const FusedParams &p, int tiles, hipStream_t s) {
+  if constexpr (FMT == FMT_INT8 || FMT == FMT_NF4) return false;
+  if (p.K <= 640) return launch_rows_k<FMT, SCALED, 640, RG>(p, tiles, s);
+  if (p.K <= 1536) return launch_rows_k<FMT, SCALED, 1536, RG>(p, tiles, s);
+  return false;
+}
+
+// RANKED instantiations carry the correction (V and U loads); the others have none at all.  One
+// problem without a correction over many rows runs with several tiles per workgroup.
 template <int FMT, bool SCALED>
 void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
+  if (!ranked && p.prob[0].tiles_end == tiles) {
+    if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;
+    if (tiles / 2 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 2>(p, tiles, s)) return;
+  }
   ranked ? launch_fused_r<FMT, SCALED, true>(p, tiles, s) : launch_fused_r<FMT, SCALED, false>(p, tiles, s);
 }
 

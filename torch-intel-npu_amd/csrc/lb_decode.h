@@ -1,5 +1,7 @@
 // gfx950 kernels of one SmolLM decode step (one sequence, one token).
 //
+//   rows_gemv_kernel      one-row linear over many rows (no correction): several 16-row tiles per
+//                         workgroup share the staged activation row.
 //   fused_gemv_kernel     up to three low-bit linears that share one activation row, in one
 //                         launch, with the layer's neighbouring element-wise work folded in:
 //                         a prologue (RMSNorm, or SiLU(gate) * up) that every workgroup
@@ -268,6 +270,168 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
     h = (f16)((float)h + (float)(f16)d);
   }
   if (P.residual) h = (f16)((float)es[j] + (float)h);
+  P.y[n0 + j] = h;
+}
+
+// One activation row, one problem, no correction, many rows (the long-N one-row linears: a tied
+// head, the Llama-shaped projections).  A workgroup holds RG 16-row tiles; wave (rg, kg) computes
+// tile rg over the k-steps kg, kg + KG, ... with KG = 4 / RG, so the staged activation row serves
+// RG tiles, and with RG = 4 every wave covers all of K and no cross-wave reduction is needed.
+// As in fused_gemv_kernel, every global load is issued straight-line before the first wait.
+template <int FMT, bool SCALED, int KMAX, int RG>
+__global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
+  constexpr int CPL = FormatTraits<FMT>::CPL;
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  constexpr int KSTEP = 4 * CPL;
+  constexpr int KG = 4 / RG;
+  constexpr int WSTEP = KG * KSTEP;
+  constexpr int D = (KMAX + WSTEP - 1) / WSTEP;  // weight loads per lane
+  static_assert(D <= 32, "KMAX too long for this tile split");
+  constexpr int T8 = CPL / 8;
+  constexpr int ROWS = 16 * RG;                   // rows per workgroup
+  constexpr int XLD = KMAX + KSTEP + 8;
+  constexpr int XB = (KMAX / 8 + 255) / 256;
+  constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;
+  constexpr int SC = SCALED ? (ROWS * GMAX + 255) / 256 : 0;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  __shared__ __align__(16) f16 xs[XLD];
+  __shared__ __align__(16) f16 ss[SCALED ? ROWS * GMAX + 8 : 8];
+  __shared__ f16 es[3 * ROWS];                    // residual, bias, per-row scale of the rows
+  __shared__ float red[KG > 1 ? (KG - 1) * ROWS : 1];
+  __shared__ float wsum[4];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int rg = wave % RG, kg = wave / RG;
+  const int j = lane & 15, g = lane >> 4;
+  const int K = p.K;
+  const FusedProblem &P = p.prob[0];
+  const int w0 = blockIdx.x * ROWS;               // first row of the workgroup
+  const int wrows = min(ROWS, P.N - w0);
+  const int n0 = w0 + 16 * rg;                    // first row of this wave's tile
+  const int rows = min(16, P.N - n0);             // <= 0: the tile lies past N (no loads, no stores)
+  const int row_bytes = K * BITS / 8;
+
+  // Epilogue operands: wave 0 fetches the residual, wave 1 the bias, wave 2 the per-row scale
+  // of the workgroup's rows (lane r < ROWS reads row w0 + r).
+  const f16 *ep = wave == 0 ? P.residual : (wave == 1 ? P.bias : (wave == 2 ? P.scales : nullptr));
+  const bool ep_on = wave == 0 ? P.residual != nullptr : (wave == 1 ? P.bias != nullptr : (wave == 2 && p.per_row));
+  const f16 ev = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(ep, ep_on ? (size_t)P.N * 2 : 0),
+                                                lane < wrows ? (w0 + lane) * 2 : kOutOfRange, 0, 0));
+  const int blocks = K >> 3;
+  const size_t kb_bytes = (size_t)K * 2;
+  const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
+  const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb_bytes);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.x, kb_bytes);
+  h8 av[XB], xv[XB];
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    av[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(abuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    xv[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xbuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+  }
+  f16 sreg[SC > 0 ? SC : 1];
+  if constexpr (SCALED) {
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)w0 * p.G, (size_t)max(wrows, 0) * p.G * 2);
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
+  }
+  const __amdgpu_buffer_rsrc_t wbuf =
+      buffer_rsrc(P.codes + (size_t)max(n0, 0) * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
+  u4 w[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int k = (kg + KG * u) * KSTEP + g * CPL;
+    const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
+    w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
+
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  if (wave < 3 && lane < ROWS) es[wave * ROWS + lane] = ev;
+  float inv = 1.0f;
+  if (p.prologue == PRO_RMSNORM) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XB; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
+    s = wave_sum(s);
+    if (lane == 0) wsum[wave] = s;
+    __syncthreads();
+    const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    inv = 1.0f / sqrtf(total / (float)K + p.eps);
+  }
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    if (b < blocks) {
+      h8 v;
+      if (p.prologue == PRO_RMSNORM) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[i][e] * inv) * (float)av[i][e]);
+      } else if (p.prologue == PRO_SILU_MUL) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[i][e]) * (float)av[i][e]);
+      } else {
+        v = xv[i];
+      }
+      *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(v);
+    }
+  }
+  for (int b = blocks + t; b * 8 < min(XLD, K + KSTEP + 8); b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      if (t + i * 256 < ROWS * GMAX) ss[t + i * 256] = sreg[i];
+    if (t < 8) ss[ROWS * GMAX + t] = (f16)0.0f;  // lanes past K of the last row index up to 4 beyond
+  }
+  __syncthreads();
+
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const f16 *a0 = xs + g * CPL;
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int kb = (kg + KG * u) * KSTEP;
+    if (kb >= K) break;  // wave-uniform
+    asm volatile("" : "+v"(w[u]));  // decode here, not at the load
+    h2 s2 = {(f16)1.0f, (f16)1.0f};
+    if constexpr (SCALED) {
+      const f16 sc = ss[(rg * 16 + j) * p.G + ((kb + g * CPL) >> p.group_shift)];
+      s2 = h2{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < T8; ++q) {
+      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
+      const h8 b = decode8<FMT, !SCALED>(w[u], q, s2, nf4_table);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+  // Lane (j, g) holds D rows 4g..4g+3 of column j; all rows are equal, row 0 (g == 0) is used.
+  float sum = acc[0];
+  if constexpr (KG > 1) {
+    if (kg > 0 && g == 0) red[(kg - 1) * ROWS + rg * 16 + j] = acc[0];
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int q = 0; q < KG - 1; ++q) sum += red[q * ROWS + rg * 16 + j];
+  }
+  if (g != 0 || j >= rows) return;
+
+  // ---- epilogue (reference torch_npu_lowbit.py:262-266, torch_npu_smollm.py:160-163) ----
+  const int r = rg * 16 + j;
+  if (p.per_row) sum *= (float)es[2 * ROWS + r];
+  f16 h = (f16)sum;
+  if (P.bias) h = (f16)((float)h + (float)es[ROWS + r]);
+  if (P.residual) h = (f16)((float)es[r] + (float)h);
   P.y[n0 + j] = h;
 }
 

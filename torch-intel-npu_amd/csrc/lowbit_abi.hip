@@ -77,9 +77,46 @@ struct GemvShape {
   int kg = 1, splits = 1, kslice = 0, kc = 0;
 };
 
+#ifndef LB_GEMV_M_TARGET_WGS
+#define LB_GEMV_M_TARGET_WGS 512  // workgroups the several-row GEMV aims for
+#endif
+#ifndef LB_GEMV_M_MIN_BYTES
+#define LB_GEMV_M_MIN_BYTES (2 << 20)  // weights from this size on use the several-row shape
+#endif
+#ifndef LB_GEMV_M_MIN_M
+#define LB_GEMV_M_MIN_M 8              // ... at this many activation rows or more
+#endif
+constexpr size_t kGemvRowsLds = 64 * 1024;
+
+// Several activation rows, a large weight and too few 64-row tiles to fill the chip: four 16-row
+// tiles per workgroup (one per wave, so the staged activations serve 64 weight rows) and K split
+// across workgroups, each staging its slice of x once, for ~LB_GEMV_M_TARGET_WGS workgroups with
+// at least four 16-byte loads per lane in every slice.
+GemvShape gemv_shape_rows(int fmt, int64_t M, int64_t N, int64_t K) {
+  GemvShape gs;
+  const int cpl = codes_per_load(fmt);
+  const int kstep = 4 * cpl;
+  const int64_t ksteps = (K + kstep - 1) / kstep;
+  const int64_t wg_tiles = (N + 63) / 64;
+  const int64_t room = (int64_t)((kGemvRowsLds - 8 * 1024) / 2 / (M + 1)) - 4 * cpl - 8;  // 8 KB for scales
+  const int64_t ks_max = std::max<int64_t>(kstep, room / kstep * kstep);
+  gs.kg = 1;
+  int64_t s = std::max<int64_t>((K + ks_max - 1) / ks_max,
+                                std::min<int64_t>((LB_GEMV_M_TARGET_WGS + wg_tiles - 1) / wg_tiles,
+                                                  std::max<int64_t>(1, ksteps / 4)));
+  const int64_t ks = round_up((K + s - 1) / s, kstep);
+  gs.splits = (int)((K + ks - 1) / ks);
+  gs.kslice = (int)ks;
+  gs.kc = (int)ks;
+  return gs;
+}
+
 // In-workgroup K groups (KG) and cross-workgroup splits so the grid holds ~kGemvTargetWaves
 // waves while each wave keeps at least one full batch of loads per split.
 GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split) {
+  const int64_t weight_bytes = fmt == FMT_FP16 ? 2 * N * K : fmt == FMT_INT8 ? N * K : N * K / 2;
+  if (allow_split && M >= LB_GEMV_M_MIN_M && weight_bytes >= LB_GEMV_M_MIN_BYTES && (N + 63) / 64 < LB_GEMV_M_TARGET_WGS)
+    return gemv_shape_rows(fmt, M, N, K);
   GemvShape gs;
   const int kstep = 4 * codes_per_load(fmt);
   const int64_t tiles = (N + 15) / 16;

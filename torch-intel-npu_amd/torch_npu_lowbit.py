@@ -139,14 +139,16 @@ def quantize_weight(weight, *, format='int4', group_size=None):
 
 
 @torch.no_grad()
-def calibrate_int8(weight, inputs):
-    """GPTQ-style W8 preparation (reference :108-152), fp64, on CPU.
+def calibrate_int8(weight, inputs, *, device=None):
+    """GPTQ-style W8 preparation (reference :108-152), fp64.
 
     Same contract as the reference: fixed fp16 per-row scales from quantize_weight,
     codes in [-127,127], descending-energy activation order with stable ties, 1% mean
     diagonal damping, dead columns keep their original codes, 128-column blocks, and a
     per-row fallback to the plain codes when calibration does not reduce the
-    reconstruction error on `inputs`.
+    reconstruction error on `inputs`.  The arguments are CPU tensors as in the reference;
+    `device` (e.g. 'cuda') runs the fp64 linear algebra there instead of on the CPU (its
+    BLAS sums in another order, so a code at an exact rounding tie may differ).
     """
     original = quantize_weight(weight, format='int8')
     n, k = weight.shape
@@ -156,7 +158,8 @@ def calibrate_int8(weight, inputs):
             or max(inputs.numel(), inputs.shape[0] * n) > 4 * 1048576
             or not torch.isfinite(inputs).all()):
         raise ValueError('Calibration requires bounded finite CPU FP16/FP32 (rows,K), rows/K<=4096, matching weight K')
-    x = inputs.detach().double()
+    dev = torch.device('cpu' if device is None else device)
+    x = inputs.detach().to(dev, torch.float64)
     hessian = x.T @ x / x.shape[0]
     energy = hessian.diagonal().clone()
     order = torch.argsort(energy, descending=True, stable=True)
@@ -164,12 +167,12 @@ def calibrate_int8(weight, inputs):
     dead = energy[order] == 0
     hessian[dead, dead] = 1.0
     damp = 0.01 * hessian.diagonal().mean().clamp_min(1e-20)
-    hessian += damp * torch.eye(k, dtype=torch.float64)
+    hessian += damp * torch.eye(k, dtype=torch.float64, device=dev)
     # Upper Cholesky factor of H^-1 drives the column-by-column error feedback.
     inverse_factor = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(hessian)), upper=True)
-    work = weight.detach().double()[:, order].clone()
-    scales = torch.from_numpy(np.frombuffer(original.scales, dtype=np.float16).astype(np.float64))
-    codes = torch.empty((n, k), dtype=torch.int8)
+    work = weight.detach().to(dev, torch.float64)[:, order].clone()
+    scales = torch.from_numpy(np.frombuffer(original.scales, dtype=np.float16).astype(np.float64)).to(dev)
+    codes = torch.empty((n, k), dtype=torch.int8, device=dev)
     for start in range(0, k, 128):
         stop = min(start + 128, k)
         block = work[:, start:stop].clone()
@@ -183,13 +186,13 @@ def calibrate_int8(weight, inputs):
             block[:, i:] -= err[:, None] * inverse_factor[col, col:stop][None, :]
             errors[:, i] = err
         work[:, stop:] -= errors @ inverse_factor[start:stop, stop:]
-    proposed = codes[:, torch.argsort(order)].contiguous().numpy()
+    proposed = codes[:, torch.argsort(order)].contiguous().cpu().numpy()
     plain = np.frombuffer(original.data, dtype=np.int8).reshape(n, k).copy()
-    target = x @ weight.detach().double().T
+    target = x @ weight.detach().to(dev, torch.float64).T
 
     def row_error(c):
-        predicted = (x @ torch.from_numpy(c.astype(np.float64)).T) * scales[None, :]
-        return (predicted - target).square().sum(0).numpy()
+        predicted = (x @ torch.from_numpy(c.astype(np.float64)).to(dev).T) * scales[None, :]
+        return (predicted - target).square().sum(0).cpu().numpy()
 
     better = row_error(proposed) < row_error(plain)
     plain[better] = proposed[better]

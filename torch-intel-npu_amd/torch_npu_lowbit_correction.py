@@ -60,11 +60,13 @@ class LowRankCorrection:
 
 
 @torch.no_grad()
-def fit_lowrank_correction(weight, packed, inputs, *, rank=32):
+def fit_lowrank_correction(weight, packed, inputs, *, rank=32, device=None):
     """Fit E ~= U V for E = W - q*s, minimising ||E L||_F with L L^T = X^T X / m + ridge.
 
-    Same contract as the reference (:42-69): per-row W8 only, fp64 on CPU, 1% mean-diagonal
-    ridge, SVD of E.L, balanced sqrt(sigma) split, factors stored in fp16.
+    Same contract as the reference (:42-69): per-row W8 only, fp64, 1% mean-diagonal ridge,
+    SVD of E.L, balanced sqrt(sigma) split, factors stored in fp16.  The arguments are CPU
+    tensors; `device` (e.g. 'cuda') runs the Cholesky / SVD there instead of on the CPU
+    (singular vectors are defined up to sign, so U and V may both flip sign column-wise).
     """
     if (not isinstance(packed, PackedWeight) or packed.format != 'int8' or packed.group_size != packed.shape[1]
             or not isinstance(weight, torch.Tensor) or weight.device.type != 'cpu' or tuple(weight.shape) != packed.shape
@@ -77,16 +79,17 @@ def fit_lowrank_correction(weight, packed, inputs, *, rank=32):
         raise ValueError('Correction fitting requires finite matching CPU W8A16 weights/activations, '
                          'rows/K<=4096 and a valid rank')
     n, k = packed.shape
-    q = torch.from_numpy(np.frombuffer(packed.data, dtype=np.int8).reshape(n, k).astype(np.float64))
-    s = torch.from_numpy(np.frombuffer(packed.scales, dtype=np.float16).astype(np.float64))
-    error = weight.detach().double() - q * s[:, None]
-    x = inputs.detach().double()
+    dev = torch.device('cpu' if device is None else device)
+    q = torch.from_numpy(np.frombuffer(packed.data, dtype=np.int8).reshape(n, k).astype(np.float64)).to(dev)
+    s = torch.from_numpy(np.frombuffer(packed.scales, dtype=np.float16).astype(np.float64)).to(dev)
+    error = weight.detach().to(dev, torch.float64) - q * s[:, None]
+    x = inputs.detach().to(dev, torch.float64)
     covariance = x.T @ x / x.shape[0]
-    covariance += 0.01 * covariance.diagonal().mean().clamp_min(1e-20) * torch.eye(k, dtype=torch.float64)
+    covariance += 0.01 * covariance.diagonal().mean().clamp_min(1e-20) * torch.eye(k, dtype=torch.float64, device=dev)
     lower = torch.linalg.cholesky(covariance)
     left, sigma, right_h = torch.linalg.svd(error @ lower, full_matrices=False)
     root = sigma[:rank].sqrt()
     up = (left[:, :rank] * root).half().contiguous()
     # V = (L^-T right_h[:rank]^T)^T scaled by sqrt(sigma): undo the whitening on the input side.
     down = (torch.linalg.solve_triangular(lower.T, right_h[:rank].T, upper=True).T * root[:, None]).half().contiguous()
-    return LowRankCorrection(packed.shape, rank, down.numpy().tobytes(), up.numpy().tobytes())
+    return LowRankCorrection(packed.shape, rank, down.cpu().numpy().tobytes(), up.cpu().numpy().tobytes())

@@ -102,19 +102,22 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
                      sbuf, s_off[i] + (((k0 + (tid % T::CHUNKS_PER_ROW) * CPC) >> p.group_shift) << 1), 0, 0));
     }
   };
+  // Chunk guards are compile-time when the chunk counts are whole multiples of the 256 threads:
+  // a runtime guard would split the step into basic blocks and keep the decode from being
+  // scheduled among the MFMAs.
   auto store = [&](Stage &st, int buf) {
 #pragma unroll
     for (int i = 0; i < T::A_PER; ++i) {
       const int c = tid + 256 * i;
       asm volatile("" : "+v"(st.a[i]));
-      if (c < T::A_CHUNKS)
+      if (T::A_CHUNKS % 256 == 0 || c < T::A_CHUNKS)
         *reinterpret_cast<u4 *>(&As[buf][(c / T::A_PER_ROW) * LD + (c % T::A_PER_ROW) * 8]) = st.a[i];
     }
 #pragma unroll
     for (int i = 0; i < T::B_PER; ++i) {
       const int c = tid + 256 * i;
       asm volatile("" : "+v"(st.b[i]));
-      if (c >= T::B_CHUNKS) continue;
+      if (T::B_CHUNKS % 256 != 0 && c >= T::B_CHUNKS) continue;
       const int r = c / T::CHUNKS_PER_ROW, kk = (c % T::CHUNKS_PER_ROW) * CPC;
       f16 *dst = &Bs[buf][r * LD + kk];
       const h2 s2 = SCALED ? h2{st.s[i], st.s[i]} : h2{(f16)1.0f, (f16)1.0f};
@@ -214,3 +217,4 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
 }
 
 }  // namespace lb
+

@@ -18,6 +18,7 @@ CPU path: fp32 torch matmul on pre-dequantized weights) timed on this host.
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cpu]
        python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
        python bench.py --decode-only      (config-4 decode leg alone, for rocprofv3 --kernel-trace)
+       python bench.py --profile-gemm     (prefill GEMMs + hipBLASLt fp16 of the same shapes, for --pmc)
 """
 import argparse
 import json
@@ -334,6 +335,27 @@ def profile_kernel(device, stream):
                           algorithmic_bytes=lin.bytes, copy_bytes=src.numel())), flush=True)
 
 
+GEMM_PROFILE_SHAPES = [('int4', 1024, 14336, 4096, 128), ('nf4', 512, 2560, 960, 64)]
+
+
+def profile_gemm(device, stream):
+    """Prefill GEMMs alone (configs 5 and 3), 20 launches each, then hipBLASLt fp16 matmuls of the
+    same shapes (torch.matmul) as the reference rate; for rocprofv3 --pmc (MFMA busy cycles)."""
+    for i, (fmt, m, n, k, g) in enumerate(GEMM_PROFILE_SHAPES):
+        lin = Linear(make_weight(fmt, n, k, g, 500 + i), m, 2, device, 600 + i)
+        for _ in range(10):
+            for call in lin.calls:
+                call.run()
+        torch.cuda.synchronize()
+        a = torch.randn(m, k, device=device, dtype=torch.float16)
+        b = torch.randn(n, k, device=device, dtype=torch.float16)
+        for _ in range(20):
+            torch.matmul(a, b.t())
+        torch.cuda.synchronize()
+        print(json.dumps(dict(profile='gemm', fmt=fmt, M=m, N=n, K=k, group=g, launches=20,
+                              flops_per_launch=2 * m * n * k)), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -347,6 +369,7 @@ def main():
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=128)
     ap.add_argument('--decode-only', action='store_true', help='only the config-4 decode leg (for tracing)')
+    ap.add_argument('--profile-gemm', action='store_true', help='prefill GEMMs alone (for rocprofv3 --pmc)')
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -363,6 +386,9 @@ def main():
     torch.manual_seed(0)
     if args.profile_kernel:
         profile_kernel(device, stream)
+        return
+    if args.profile_gemm:
+        profile_gemm(device, stream)
         return
     if args.decode_only:
         decode = decode_leg(device, args.decode_steps, 0)

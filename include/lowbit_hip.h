@@ -63,6 +63,10 @@ typedef enum lb_format {
 #define LB_FLAG_FORCE_GEMV    0x1u /* decode-regime kernel regardless of M (M <= 32) */
 #define LB_FLAG_FORCE_GEMM    0x2u /* prefill-regime MFMA GEMM regardless of M */
 #define LB_FLAG_FORCE_GENERIC 0x4u /* shape-agnostic fallback kernel (any N, K, group) */
+/* Streaming one-row GEMV regardless of size: M == 1, INT4/INT8 codes, no correction, K <= 16384,
+ * K a multiple of 32 (INT4) or 16 (INT8), and each 128-code (INT4) / 64-code (INT8) piece of a row
+ * spanning 1, 2 or 4 whole groups.  Its sums use the exact q * s weights. */
+#define LB_FLAG_FORCE_STREAM  0x20u
 /* One fp16 product per group of K, summed by a balanced fp16 add tree (neighbours pair up,
  * an odd last piece moves up unpaired), then + bias: the compact_groups graph of the
  * reference (torch_npu_lowbit.py:235-256).  At most 32 groups; no correction.  With one

@@ -243,6 +243,34 @@ def test_variant_argument_errors(over, status, needle):
     assert needle in message
 
 
+S = lowbit_hip.FLAG_FORCE_STREAM
+
+
+@pytest.mark.parametrize('over,status,needle', [
+    (dict(flags=S | lowbit_hip.FLAG_FORCE_GEMV), lowbit_hip.INVALID_ARGUMENT, 'at most one'),
+    (dict(flags=S, M=2), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
+    (dict(flags=S, format=2), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),   # nf4
+    (dict(flags=S, format=3), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),   # fp16
+    (dict(flags=S, rank=4, down=0x50000, up=0x60000, up_ld=8), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
+    (dict(flags=S | lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
+    (dict(flags=S, K=192, ldx=192, group_size=96), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),  # 96 spans 1.33 pieces
+    (dict(flags=S, K=768, ldx=768, group_size=384), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),  # not a power of two
+    (dict(flags=S, format=0, K=128, group_size=8, ldx=128), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),  # group < 16
+    (dict(flags=S, K=32768, ldx=32768, group_size=128, N=1, ldy=1), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
+])
+def test_force_stream_argument_errors(over, status, needle):
+    got, _, message = workspace(args(**over))
+    assert got == status, message
+    assert needle in message
+
+
+@pytest.mark.parametrize('over', [dict(), dict(group_size=64), dict(group_size=128), dict(K=4096, ldx=4096, group_size=4096),
+                                  dict(format=0, group_size=16), dict(format=0, K=576, ldx=576, group_size=576)])
+def test_force_stream_accepts_and_needs_no_workspace(over):
+    status, size, message = workspace(args(flags=S, **over))
+    assert (status, size) == (0, 0), message
+
+
 def test_variant_workspace_sizes():
     # compact: fp16 pieces [groups, M, N]; one group is the default graph (no workspace at M=1)
     status, size, message = workspace(args(M=3, flags=lowbit_hip.FLAG_COMPACT_GROUPS))

@@ -7,6 +7,7 @@
 #include "../../include/lowbit_decode_hip.h"
 #include "abi_util.h"
 #include "lb_decode.h"
+#include "lb_stream.h"
 
 using namespace lb;
 using namespace lb::abi;
@@ -143,10 +144,108 @@ bool launch_rows(const FusedParams &p, int tiles, hipStream_t s) {
   return false;
 }
 
+// stream_gemv_kernel takes one-row calls with rows longer than LB_STREAM_MIN_K or at least
+// LB_STREAM_MIN_BYTES of weights (measured on MI355X: below both, the single-tile kernels, whose
+// workgroups issue every load at once, finish first).
+#ifndef LB_STREAM_MIN_BYTES
+#define LB_STREAM_MIN_BYTES (64ll << 20)
+#endif
+#ifndef LB_STREAM_MIN_K
+#define LB_STREAM_MIN_K 4096
+#endif
+#ifndef LB_STREAM_WGS_PER_CU
+#define LB_STREAM_WGS_PER_CU 4         // persistent workgroups per CU
+#endif
+#ifndef LB_STREAM_SPLIT_TILES_PER_CU
+#define LB_STREAM_SPLIT_TILES_PER_CU 4 // below this many 16-row tiles per CU, split K over the 4 waves
+#endif
+#ifndef LB_STREAM_PD
+#define LB_STREAM_PD 2                 // chunks in flight per wave
+#endif
+
+// Compute units of the current device (cached per device ordinal).
+int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cache[dev];
+}
+
+template <int FMT, bool SCALED, int NS, int KMAX, int KSPLIT>
+void launch_stream_k(const StreamParams &p, int grid, hipStream_t s) {
+  constexpr int CH = KMAX <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
+  hipLaunchKernelGGL((stream_gemv_kernel<FMT, SCALED, NS, KMAX, CH, LB_STREAM_PD, KSPLIT>), dim3(grid), dim3(256), 0,
+                     s, p);
+}
+
+template <int FMT, bool SCALED, int NS>
+void launch_stream_n(StreamParams p, hipStream_t s) {
+  constexpr int CPW = 4 * StreamTraits<FMT>::CPL;
+  const int cus = device_cus();
+  const int kmax = p.K <= 640 ? 640 : p.K <= 4096 ? 4096 : 16384;
+  const int ch = kmax <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
+  p.chunks = (p.K + ch * CPW - 1) / (ch * CPW);
+  const bool split = kmax > 640 && p.chunks >= 4 && p.tiles < LB_STREAM_SPLIT_TILES_PER_CU * cus;
+  if (split) {
+    if (kmax == 4096) launch_stream_k<FMT, SCALED, NS, 4096, 4>(p, p.tiles, s);
+    else launch_stream_k<FMT, SCALED, NS, 16384, 4>(p, p.tiles, s);
+    return;
+  }
+  const int grid = std::max(1, std::min((p.tiles + 3) / 4, cus * LB_STREAM_WGS_PER_CU));
+  if (kmax == 640) launch_stream_k<FMT, SCALED, NS, 640, 1>(p, grid, s);
+  else if (kmax == 4096) launch_stream_k<FMT, SCALED, NS, 4096, 1>(p, grid, s);
+  else launch_stream_k<FMT, SCALED, NS, 16384, 1>(p, grid, s);
+}
+
+// One problem, one activation row, no prologue or correction, INT4 / INT8 codes with groups that
+// stream_gemv_kernel handles (a 4*CPL-code load spans 1, 2 or 4 whole groups), K <= 16384, long
+// rows or many weights (above): launched there (false otherwise).
+template <int FMT, bool SCALED>
+bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
+  if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
+    return false;
+  } else {
+    const FusedProblem &q = p.prob[0];
+    if (p.prologue != PRO_NONE || q.rank > 0) return false;
+    const int ns = stream_group_span(FMT, p.K, SCALED ? p.K / p.G : p.K);
+    if (ns == 0) return false;
+    const int64_t weight_bytes = (int64_t)q.N * p.K * StreamTraits<FMT>::BITS / 8;
+    if (!p.force_stream && p.K <= fused_kmax_limit(FMT) && weight_bytes < LB_STREAM_MIN_BYTES &&
+        p.K <= LB_STREAM_MIN_K)
+      return false;
+    StreamParams sp{};
+    sp.x = p.x;
+    sp.codes = q.codes;
+    sp.scales = q.scales;
+    sp.y = q.y;
+    sp.bias = q.bias;
+    sp.residual = q.residual;
+    sp.N = q.N;
+    sp.K = p.K;
+    sp.G = p.G;
+    sp.group_shift = p.group_shift;
+    sp.tiles = tiles;
+    if constexpr (!SCALED) {
+      launch_stream_n<FMT, false, 1>(sp, s);
+    } else {
+      if (ns == 1) launch_stream_n<FMT, true, 1>(sp, s);
+      else if (ns == 2) launch_stream_n<FMT, true, 2>(sp, s);
+      else launch_stream_n<FMT, true, 4>(sp, s);
+    }
+    return true;
+  }
+}
+
 // RANKED instantiations carry the correction (V and U loads); the others have none at all.  One
-// problem without a correction over many rows runs with several tiles per workgroup.
+// problem without a correction over many rows runs with several tiles per workgroup, or, when it
+// is long enough, in stream_gemv_kernel.
 template <int FMT, bool SCALED>
 void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
+  if (!ranked && p.prob[0].tiles_end == tiles && try_stream<FMT, SCALED>(p, tiles, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles) {
     if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;
     if (tiles / 2 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 2>(p, tiles, s)) return;

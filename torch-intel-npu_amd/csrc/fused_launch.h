@@ -23,6 +23,7 @@ struct FusedProblem {
 };
 
 struct FusedParams {
+  int force_stream;       // host-side dispatch only: take stream_gemv_kernel whatever the size
   const f16 *x;           // [K] activation (PRO_SILU_MUL: the gate row)
   const f16 *x2;          // PRO_SILU_MUL: the up row [K]
   const f16 *gamma;       // PRO_RMSNORM: [K]
@@ -35,6 +36,21 @@ struct FusedParams {
 // kFusedMaxK only without a correction and with groups of at least 64 (or one per row).
 constexpr int fused_kmax_limit(int format) {
   return format == FMT_FP16 ? 4096 : format == FMT_INT8 ? 8192 : 16384;
+}
+
+// Scales per 16-byte-load flush of stream_gemv_kernel for an INT4 / INT8 row of K codes in groups
+// of `group` (1, 2 or 4), or 0 when the kernel does not take the shape: K <= 16384 and a multiple
+// of the codes per lane load, one group per row or power-of-two groups (the kernel indexes scales
+// by a shift), each 4-lane-load piece of a row spanning whole groups.
+inline int stream_group_span(int format, long long K, long long group) {
+  if (format != FMT_INT4 && format != FMT_INT8) return 0;
+  const long long cpl = format == FMT_INT4 ? 32 : 16, cpw = 4 * cpl;
+  if (K <= 0 || K > 16384 || K % cpl != 0 || group <= 0 || K % group != 0) return 0;
+  if (group == K) return 1;
+  if ((group & (group - 1)) != 0) return 0;
+  if (group % cpw == 0) return 1;
+  if (cpw % group != 0 || group < cpl) return 0;
+  return (int)(cpw / group);
 }
 
 // Launches fused_gemv_kernel for `tiles` 16-row tiles (defined with the kernels).

@@ -142,7 +142,9 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 // One activation row: the single-tile kernel (all of a workgroup's loads in flight at once,
 // correction z computed inside each workgroup for K <= kFusedMaxK) needs no workspace.
 bool row_eligible(const lb_linear_args *a) {
-  if (a->M != 1 || a->K > fused_kmax_limit((int)a->format)) return false;
+  if (a->M != 1) return false;
+  if (a->K > fused_kmax_limit((int)a->format))  // past the single-tile kernels: the stream kernel only
+    return a->rank == 0 && stream_group_span((int)a->format, a->K, a->group_size) != 0;
   if (a->K > kFusedMaxK) {  // long rows: no correction, groups of at least 64 (or one per row)
     const bool dense = a->format == LB_FORMAT_FP16;
     if (a->rank > 0 || !(dense || a->group_size == a->K || a->group_size >= 64)) return false;
@@ -192,7 +194,9 @@ Plan make_variant_plan(const lb_linear_args *a, int variant) {
 Plan make_plan(const lb_linear_args *a, bool eligible) {
   Plan pl;
   const int fmt = (int)a->format;
-  if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) {
+  if (a->flags & LB_FLAG_FORCE_STREAM) {  // validated: the stream kernel takes the shape
+    pl.path = PATH_ROW;
+  } else if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) {
     pl.path = PATH_GENERIC;
   } else if (a->flags & LB_FLAG_FORCE_GEMM) {
     pl.path = PATH_GEMM;
@@ -278,12 +282,21 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
     if (overlaps(inputs[6], inputs[i]))
       return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace overlaps %s", inputs[i].name);
 
-  if (a->flags & ~(LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8))
+  constexpr uint32_t kForce = LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_FORCE_STREAM;
+  if (a->flags & ~(kForce | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8))
     return fail(LB_INVALID_ARGUMENT, "lb_linear: unknown flags 0x%x", a->flags);
   if ((a->flags & LB_FLAG_FORCE_GEMV) && a->M > kGemvMaxM)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: LB_FLAG_FORCE_GEMV needs M <= %d", kGemvMaxM);
-  if (__builtin_popcount(a->flags & (LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC)) > 1)
+  if (__builtin_popcount(a->flags & kForce) > 1)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: at most one LB_FLAG_FORCE_* flag");
+  if (a->flags & LB_FLAG_FORCE_STREAM) {
+    if ((a->flags & (LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8)) || a->M != 1 || a->rank > 0 ||
+        stream_group_span((int)a->format, a->K, a->group_size) == 0 || !aligned(a->codes, 16) || !aligned(a->x, 16))
+      return fail(LB_UNSUPPORTED,
+                  "lb_linear: LB_FLAG_FORCE_STREAM needs M == 1, int4/int8 codes, no correction or variant, "
+                  "K <= 16384 (a multiple of 32 / 16), groups spanning whole 128 / 64-code pieces, "
+                  "16-byte aligned codes/x");
+  }
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {
     // reference _activation_scale (torch_npu_lowbit.py:155-166)
@@ -578,6 +591,7 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     fp.group_shift = p.group_shift;
     fp.per_row = p.per_row;
     fp.prologue = PRO_NONE;
+    fp.force_stream = (a->flags & LB_FLAG_FORCE_STREAM) != 0;
     const int tiles = (int)((a->N + 15) / 16);
     FusedProblem &q = fp.prob[0];
     q.codes = p.codes;

@@ -155,3 +155,85 @@ def test_long_rows_take_stream_unforced(device, spec):
     rng = np.random.default_rng(n + k)
     p = problem(rng, fmt, 1, n, k, group)
     check(p, run(p, device), f'long rows {spec}')
+
+
+# Several activation rows (2 <= M <= 16, K <= 4096): each MFMA A row spans more code blocks as M
+# grows, so INT4 needs groups >= 64 up to 8 rows and >= 128 beyond; INT8 one scale per 64 codes.
+ROWS_CASES = [
+    ('int4', 2, 1040, 4096, 128), ('int4', 3, 1040, 2048, 64), ('int4', 4, 2064, 4096, 64),
+    ('int4', 5, 1040, 4096, 128), ('int4', 8, 1040, 1024, 64), ('int4', 11, 1040, 4096, 128),
+    ('int4', 16, 1040, 4096, 4096), ('int4', 16, 16400, 1024, 128),   # the last one: persistent waves
+    ('int4', 4, 16400, 576, 64),
+    ('int8', 2, 1040, 4096, 4096), ('int8', 7, 1040, 2048, 2048), ('int8', 16, 1040, 4096, 4096),
+    ('int8', 3, 1040, 4096, 64), ('int8', 12, 16400, 1024, 128),
+]
+
+
+@pytest.mark.parametrize('spec', ROWS_CASES, ids=lambda s: '-'.join(map(str, s)))
+def test_stream_rows_match_oracle(device, spec):
+    fmt, m, n, k, group = spec
+    announce('stream rows', spec)
+    rng = np.random.default_rng(m * 131 + n + k + group)
+    p = problem(rng, fmt, m, n, k, group, bias=(m % 2 == 1))
+    check(p, run(p, device, STREAM), f'stream rows {spec}')
+
+
+def test_stream_rows_strided_activations_and_outputs(device):
+    """x rows with ldx > K and y rows with ldy > N (views into wider buffers)."""
+    m, n, k, group = 6, 2064, 2048, 128
+    announce('stream rows strided')
+    rng = np.random.default_rng(77)
+    p = problem(rng, 'int4', m, n, k, group)
+    wide = torch.zeros((m, k + 64), dtype=torch.float16, device=device)
+    wide[:, 8:8 + k] = to_dev(p['x'], device)
+    out = torch.full((m, n + 40), 7.0, dtype=torch.float16, device=device)
+    y = lowbit_hip.linear(wide[:, 8:8 + k], to_dev(np.frombuffer(p['data'], np.uint8), device),
+                          to_dev(np.frombuffer(p['scales'], np.float16), device), format='int4', N=n, K=k,
+                          group_size=group, flags=STREAM, out=out[:, 16:16 + n])
+    torch.cuda.synchronize()
+    check(p, y.cpu().numpy(), 'stream rows strided')
+    untouched = torch.cat([out[:, :16], out[:, 16 + n:]], dim=1)
+    assert (untouched == 7.0).all()
+
+
+def test_stream_rows_identity_is_bit_exact(device):
+    """Row m of x is one-hot at column c_m (power-of-two scales): y[m] is the dequantized column."""
+    m, n, k, group = 8, 1040, 2048, 64
+    announce('stream rows identity')
+    rng = np.random.default_rng(8)
+    data = o.pack(rng.integers(0, 16, n * k).astype(np.uint8))
+    scales = (2.0 ** rng.integers(-10, 3, n * (k // group))).astype(np.float16)
+    w = o.dequantize('int4', (n, k), group, data, scales.tobytes())
+    cols = [0, 1, 33, 64, 127, 1000, 2046, 2047]
+    x = np.zeros((m, k), np.float16)
+    for r, c in enumerate(cols):
+        x[r, c] = 1.0
+    y = lowbit_hip.linear(to_dev(x, device), to_dev(np.frombuffer(data, np.uint8), device), to_dev(scales, device),
+                          format='int4', N=n, K=k, group_size=group, flags=STREAM).cpu().numpy()
+    for r, c in enumerate(cols):
+        np.testing.assert_array_equal(y[r].view(np.uint16), w[:, c].view(np.uint16), err_msg=f'row {r}')
+
+
+@pytest.mark.parametrize('spec', [('int4', 8, 32768, 4096, 128), ('int8', 3, 16384, 4096, 4096)],
+                         ids=lambda s: '-'.join(map(str, s)))
+def test_stream_rows_unforced(device, spec):
+    """Several rows over >= 64 MB of weights take the stream kernel without a flag; random codes,
+    the oracle checks row slices (same bars)."""
+    fmt, m, n, k, group = spec
+    announce('stream rows auto', spec)
+    rng = np.random.default_rng(n * m)
+    if fmt == 'int4':
+        data = rng.integers(0, 256, n * k // 2).astype(np.uint8).tobytes()
+    else:
+        data = rng.integers(-127, 128, n * k).astype(np.int8).tobytes()
+    g = k // group
+    scales = (rng.uniform(0.5, 1.5, n * g) * (0.02 / 7 if fmt == 'int4' else 0.02 / 127)).astype(np.float16)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = lowbit_hip.linear(to_dev(x, device), to_dev(np.frombuffer(data, np.uint8), device), to_dev(scales, device),
+                          format=fmt, N=n, K=k, group_size=group).cpu().numpy()
+    row_bytes = k // 2 if fmt == 'int4' else k
+    for lo in (0, n // 2 + 16, n - 2048):
+        d = data[lo * row_bytes:(lo + 2048) * row_bytes]
+        sc = scales[lo * g:(lo + 2048) * g].tobytes()
+        p = dict(fmt=fmt, m=m, n=2048, k=k, group=group, x=x, data=d, scales=sc, bias=None, down=None, up=None)
+        check(p, np.ascontiguousarray(y[:, lo:lo + 2048]), f'stream rows auto {spec} rows from {lo}')

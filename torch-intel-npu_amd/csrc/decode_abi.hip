@@ -175,30 +175,70 @@ int device_cus() {
   return cache[dev];
 }
 
-template <int FMT, bool SCALED, int NS, int KMAX, int KSPLIT>
+// Waves per persistent workgroup: more rows stage more LDS (fewer workgroups per CU), so their
+// workgroups are wider to keep about sixteen waves of loads in flight per CU.
+template <int MP, int KSPLIT>
+constexpr int stream_waves() { return KSPLIT == 4 || MP <= 4 ? 4 : MP == 8 ? 8 : 16; }
+
+template <int FMT, bool SCALED, int NS, int KMAX, int KSPLIT, int MP>
 void launch_stream_k(const StreamParams &p, int grid, hipStream_t s) {
   constexpr int CH = KMAX <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
-  hipLaunchKernelGGL((stream_gemv_kernel<FMT, SCALED, NS, KMAX, CH, LB_STREAM_PD, KSPLIT>), dim3(grid), dim3(256), 0,
-                     s, p);
+  constexpr int WAVES = stream_waves<MP, KSPLIT>();
+  hipLaunchKernelGGL((stream_gemv_kernel<FMT, SCALED, NS, KMAX, CH, LB_STREAM_PD, KSPLIT, MP, WAVES>), dim3(grid),
+                     dim3(64 * WAVES), 0, s, p);
 }
 
-template <int FMT, bool SCALED, int NS>
-void launch_stream_n(StreamParams p, hipStream_t s) {
-  constexpr int CPW = 4 * StreamTraits<FMT>::CPL;
+// LDS bytes of one stream_gemv_kernel workgroup (activation rows, zero region, block sums).
+constexpr int stream_lds_bytes(int mp, int kp, int cpl) { return (mp + 1) * kp * 2 + mp * (kp / cpl + 16) * 4; }
+
+// Launch mode and staged length for MP activation rows: K split over one workgroup's waves when
+// there are few tiles per CU (and K spans at least 4 chunks), else persistent workgroups.
+template <int FMT, bool SCALED, int NS, int MP>
+void launch_stream_m(StreamParams p, hipStream_t s) {
+  constexpr int CPL = StreamTraits<FMT>::CPL, CPW = 4 * CPL;
   const int cus = device_cus();
-  const int kmax = p.K <= 640 ? 640 : p.K <= 4096 ? 4096 : 16384;
+  const int kmax = MP > 1 ? 4096 : p.K <= 640 ? 640 : p.K <= 4096 ? 4096 : 16384;
   const int ch = kmax <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
   p.chunks = (p.K + ch * CPW - 1) / (ch * CPW);
-  const bool split = kmax > 640 && p.chunks >= 4 && p.tiles < LB_STREAM_SPLIT_TILES_PER_CU * cus;
-  if (split) {
-    if (kmax == 4096) launch_stream_k<FMT, SCALED, NS, 4096, 4>(p, p.tiles, s);
-    else launch_stream_k<FMT, SCALED, NS, 16384, 4>(p, p.tiles, s);
-    return;
+  if constexpr (MP <= 4) {  // more rows stage too much per workgroup for one tile each
+    if (kmax > 640 && p.chunks >= 4 && p.tiles < LB_STREAM_SPLIT_TILES_PER_CU * cus) {
+      if (kmax == 4096) launch_stream_k<FMT, SCALED, NS, 4096, 4, MP>(p, p.tiles, s);
+      else if constexpr (MP == 1) launch_stream_k<FMT, SCALED, NS, 16384, 4, MP>(p, p.tiles, s);
+      return;
+    }
   }
-  const int grid = std::max(1, std::min((p.tiles + 3) / 4, cus * LB_STREAM_WGS_PER_CU));
-  if (kmax == 640) launch_stream_k<FMT, SCALED, NS, 640, 1>(p, grid, s);
-  else if (kmax == 4096) launch_stream_k<FMT, SCALED, NS, 4096, 1>(p, grid, s);
-  else launch_stream_k<FMT, SCALED, NS, 16384, 1>(p, grid, s);
+  constexpr int WAVES = stream_waves<MP, 1>();
+  const int per_cu = std::max(1, std::min(LB_STREAM_WGS_PER_CU * 4 / WAVES, (160 * 1024) / stream_lds_bytes(MP, kmax, CPL)));
+  const int grid = std::max(1, std::min((p.tiles + WAVES - 1) / WAVES, cus * per_cu));
+  if constexpr (MP == 1) {
+    if (kmax == 640) return launch_stream_k<FMT, SCALED, NS, 640, 1, MP>(p, grid, s);
+    if (kmax == 16384) return launch_stream_k<FMT, SCALED, NS, 16384, 1, MP>(p, grid, s);
+  }
+  launch_stream_k<FMT, SCALED, NS, 4096, 1, MP>(p, grid, s);
+}
+
+// Activation rows -> MP (the instantiated group spans: any for one row; INT4 up to two groups per
+// load for MP <= 8 and one for MP = 16; INT8 groups one per load for MP > 1).
+template <int FMT, bool SCALED, int NS>
+void launch_stream_ns(const StreamParams &p, hipStream_t s) {
+  if (p.M == 1) return launch_stream_m<FMT, SCALED, NS, 1>(p, s);
+  if constexpr (NS <= 2 && (FMT == FMT_INT4 || NS == 1)) {
+    if (p.M == 2) return launch_stream_m<FMT, SCALED, NS, 2>(p, s);
+    if (p.M <= 4) return launch_stream_m<FMT, SCALED, NS, 4>(p, s);
+    if (p.M <= 8) return launch_stream_m<FMT, SCALED, NS, 8>(p, s);
+    if constexpr (NS == 1) return launch_stream_m<FMT, SCALED, NS, 16>(p, s);
+  }
+}
+
+template <int FMT, bool SCALED>
+void launch_stream_f(const StreamParams &p, int ns, hipStream_t s) {
+  if constexpr (!SCALED) {
+    launch_stream_ns<FMT, false, 1>(p, s);
+  } else {
+    if (ns == 1) launch_stream_ns<FMT, true, 1>(p, s);
+    else if (ns == 2) launch_stream_ns<FMT, true, 2>(p, s);
+    else launch_stream_ns<FMT, true, 4>(p, s);
+  }
 }
 
 // One problem, one activation row, no prologue or correction, INT4 / INT8 codes with groups that
@@ -224,18 +264,15 @@ bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
     sp.y = q.y;
     sp.bias = q.bias;
     sp.residual = q.residual;
+    sp.M = 1;
     sp.N = q.N;
     sp.K = p.K;
     sp.G = p.G;
     sp.group_shift = p.group_shift;
+    sp.ldx = p.K;
+    sp.ldy = q.N;
     sp.tiles = tiles;
-    if constexpr (!SCALED) {
-      launch_stream_n<FMT, false, 1>(sp, s);
-    } else {
-      if (ns == 1) launch_stream_n<FMT, true, 1>(sp, s);
-      else if (ns == 2) launch_stream_n<FMT, true, 2>(sp, s);
-      else launch_stream_n<FMT, true, 4>(sp, s);
-    }
+    launch_stream_f<FMT, SCALED>(sp, ns, s);
     return true;
   }
 }
@@ -262,6 +299,12 @@ lb_status launch_status(const char *what) {
 }  // namespace
 
 namespace lb {
+void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t s) {
+  if (format == FMT_INT4) launch_stream_f<FMT_INT4, true>(p, ns, s);
+  else if (scaled) launch_stream_f<FMT_INT8, true>(p, ns, s);
+  else launch_stream_f<FMT_INT8, false>(p, ns, s);
+}
+
 void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, int tiles, hipStream_t s) {
   switch (format) {
     case FMT_INT8:

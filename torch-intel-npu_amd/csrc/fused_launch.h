@@ -53,6 +53,17 @@ inline int stream_group_span(int format, long long K, long long group) {
   return (int)(cpw / group);
 }
 
+// Whether stream_gemv_kernel takes M activation rows (2 <= M <= 16) of such a shape: the rows
+// are staged whole (K <= 4096), and with more rows each MFMA A row spans more code blocks, so the
+// groups must be longer (INT4: <= 2 groups per 128-code load up to 8 rows, 1 for 16; INT8: one
+// scale per 64-code load or one per row).
+inline bool stream_rows_ok(int format, long long M, long long K, long long group) {
+  const int span = stream_group_span(format, K, group);
+  if (span == 0 || M < 2 || M > 16 || K > 4096) return false;
+  if (format == FMT_INT4) return M <= 8 ? span <= 2 : span == 1;
+  return span == 1;
+}
+
 // Launches fused_gemv_kernel for `tiles` 16-row tiles (defined with the kernels).
 void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, int tiles, hipStream_t stream);
 

@@ -1,6 +1,6 @@
-// gfx950 streaming GEMV for one activation row over long INT4 / INT8 weight matrices (the tied
-// head, the Llama-shaped projections): y[N] = x[K] . (q * s)[N, K]^T, scales applied to exact
-// integer-code sums.
+// gfx950 streaming GEMV for up to 16 activation rows over long INT4 / INT8 weight matrices (the
+// tied head, the Llama-shaped projections): y[M, N] = x[M, K] . (q * s)[N, K]^T, scales applied
+// to exact integer-code sums.
 //
 // Weight decode without per-weight arithmetic.  A code enters the MFMA as the fp16 value of a
 // "magic" half-word: the (sign-flipped) nibble or byte is OR-ed under the exponent of 1024, so the
@@ -15,12 +15,16 @@
 // exact x . (q * s) product up to fp32 rounding (the reference's rounding-budget gate,
 // torch_npu_lowbit_demo.py:97-106, bounds the distance to its fp16(q * s) weights).
 //
-// Per-block sums come from the MFMA rows that a one-row product leaves unused: MFMA A row i is the
-// activation masked to one block (lanes read a zero region of LDS where their row is inactive), so
-// the 16 x 16 result holds 16 block partials per output row, flushed every window of 4 loads.
+// Per-block sums come from the MFMA's 16 A rows: with MP (1, 2, 4, 8 or 16) activation rows, each
+// activation row owns R = 16 / MP A rows, and A row (m, r) is activation row m masked to the
+// blocks it accumulates (lanes read a zero region of LDS where their row is inactive):
+//   R >= 4  one 32/16-code block each: a flush window covers R / 4 loads (any group >= a block);
+//   R == 2  two blocks (half of a 16-byte load's four lane groups): groups >= 2 blocks;
+//   R == 1  all four blocks of a load: groups >= 4 blocks.
+// The 16 x 16 result is flushed (scaled, bias removed, accumulated in fp32) once per window.
 //
 // A wave streams 16-row tiles chunk by chunk (CH 16-byte loads per lane per chunk, PD chunks in
-// flight); the activation row, its zero twin and the block sums are staged in LDS once per
+// flight); the activation rows, a zero region and the block sums are staged in LDS once per
 // workgroup.  KSPLIT = 1: persistent waves, each owning whole tiles; KSPLIT = 4: one tile per
 // workgroup, the four waves taking interleaved chunks and reducing through LDS.
 #pragma once
@@ -33,13 +37,14 @@ template <> struct StreamTraits<FMT_INT4> { static constexpr int CPL = 32, BITS 
 template <> struct StreamTraits<FMT_INT8> { static constexpr int CPL = 16, BITS = 8, T8 = 2; };
 
 struct StreamParams {
-  const f16 *x;           // [K]
+  const f16 *x;           // [M, ldx]
   const uint8_t *codes;   // [N, K * bits / 8]
   const f16 *scales;      // [N, G]
-  f16 *y;                 // [N]
+  f16 *y;                 // [M, ldy]
   const f16 *bias;        // [N] or null
-  const f16 *residual;    // [N] or null (may equal y)
-  int N, K, G, group_shift;
+  const f16 *residual;    // [N] or null (may equal y; M == 1 only)
+  int M, N, K, G, group_shift;
+  int ldx, ldy;
   int tiles, chunks;      // 16-row tiles; chunks per tile row
 };
 
@@ -76,32 +81,45 @@ __device__ __forceinline__ h8 stream_decode(const u4 &w, int q) {
   return __builtin_bit_cast(h8, v);
 }
 
-// NS: scales a lane reads per flush (the groups one 4*CPL-code load spans: 1, 2 or 4).
-template <int CH, int NS, bool SCALED>
+// Geometry of the A-row assignment for MP activation rows (see the file comment).
+template <int MP, int NS, int CH>
+struct StreamGeom {
+  static_assert(MP == 1 || MP == 2 || MP == 4 || MP == 8 || MP == 16, "MP is a power of two <= 16");
+  static constexpr int R = 16 / MP;                 // A rows per activation row
+  static constexpr int WL = R >= 4 ? R / 4 : 1;     // loads per flush window
+  static constexpr int BPR = R >= 4 ? 1 : 4 / R;    // blocks per A row
+  static constexpr int NMR = R >= 4 ? 1 : 4 / R;    // activation rows a lane flushes
+  static constexpr int NSL = NS;                    // scales a lane reads per window (one load's groups)
+  static constexpr int WIN = (CH + WL - 1) / WL;    // flush windows per chunk
+  static_assert(R >= 4 || NS <= 4 / BPR, "groups must cover an A row's blocks");
+};
+
+template <int CH, int NSL, int WIN, bool SCALED>
 struct StreamBuf {
-  static constexpr int WIN = (CH + 3) / 4;
   u4 w[CH];
-  f16 s[SCALED ? WIN * NS : 1];
+  f16 s[SCALED ? WIN * NSL : 1];
   f16 e[3];                // bias, residual, per-row scale of the lane's row (KSPLIT = 1)
 };
 
-template <int FMT, bool SCALED, int NS, int KMAX, int CH, int PD, int KSPLIT>
-__global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
+template <int FMT, bool SCALED, int NS, int KMAX, int CH, int PD, int KSPLIT, int MP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void stream_gemv_kernel(StreamParams p) {
   using TR = StreamTraits<FMT>;
   using SL = StreamSlots<FMT>;
-  using Buf = StreamBuf<CH, NS, SCALED>;
+  using GE = StreamGeom<MP, NS, CH>;
+  constexpr int R = GE::R, WL = GE::WL, BPR = GE::BPR, NMR = GE::NMR, NSL = GE::NSL, WIN = GE::WIN;
+  using Buf = StreamBuf<CH, NSL, WIN, SCALED>;
   constexpr int CPL = TR::CPL, CPW = 4 * CPL, BITS = TR::BITS, T8 = TR::T8;
   constexpr int KC = CH * CPW;                       // codes per chunk
   constexpr int KP = (KMAX + KC - 1) / KC * KC;      // staged row length
-  constexpr int WIN = Buf::WIN;                      // flush windows per chunk
-  constexpr int NB = KP / 8;                         // 8-code groups of the staged row
-  constexpr int XPER = (NB + 255) / 256;
+  constexpr int NB = KP / 8;                         // 8-code groups of a staged row
+  constexpr int XBLD = KP / CPL + 16;                // block sums per staged row (zero tail)
   constexpr int kOutOfRange = (int)0x80000000u;
-  static_assert(KSPLIT == 1 || KSPLIT == 4, "KSPLIT is 1 or 4");
-  __shared__ __align__(16) f16 xs[KP];
+  static_assert(KSPLIT == 1 || (KSPLIT == 4 && WAVES == 4), "KSPLIT is 1, or 4 with four waves");
+  constexpr int NT = 64 * WAVES;
+  __shared__ __align__(16) f16 xs[MP * KP];
   __shared__ __align__(16) f16 xz[KP];
-  __shared__ __align__(16) float xb[KP / CPL + 16];
-  __shared__ float red[KSPLIT > 1 ? 3 * 16 : 1];
+  __shared__ __align__(16) float xb[MP * XBLD];
+  __shared__ float red[KSPLIT > 1 ? 3 * 64 * NMR : 1];
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -119,13 +137,13 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
           buffer_rsrc(p.scales + (size_t)(rows > 0 ? n0 : 0) * p.G, (size_t)rows * p.G * 2);
 #pragma unroll
       for (int w = 0; w < WIN; ++w) {
-        const int u = 4 * w + g;  // the load whose blocks this lane flushes
+        const int u = w * WL + (R >= 4 ? (4 * g % R) / 4 : 0);  // the load this lane flushes
         const int kb = (chunk * CH + u) * CPW;
 #pragma unroll
-        for (int r = 0; r < NS; ++r) {
+        for (int r = 0; r < NSL; ++r) {
           const int kk = kb + r * (CPW / NS);
           const int off = (u < CH && kk < K) ? (j * p.G + (kk >> p.group_shift)) * 2 : kOutOfRange;
-          b.s[w * NS + r] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sb, off, 0, 0));
+          b.s[w * NSL + r] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sb, off, 0, 0));
         }
       }
     }
@@ -151,7 +169,7 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
   // Work list of this wave: (tile, chunk) items.
   int it_tile, it_chunk, c_tile, c_chunk, items;
   if constexpr (KSPLIT == 1) {
-    const int gw = blockIdx.x * 4 + wave, W = gridDim.x * 4;
+    const int gw = blockIdx.x * WAVES + wave, W = gridDim.x * WAVES;
     it_tile = c_tile = gw;
     it_chunk = c_chunk = 0;
     items = gw < p.tiles ? ((p.tiles - 1 - gw) / W + 1) * C : 0;
@@ -162,7 +180,7 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
   }
   auto advance = [&](int &tile, int &chunk) {
     if constexpr (KSPLIT == 1) {
-      if (++chunk == C) { chunk = 0; tile += gridDim.x * 4; }
+      if (++chunk == C) { chunk = 0; tile += gridDim.x * WAVES; }
     } else {
       chunk += 4;
     }
@@ -178,7 +196,7 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
   f16 ek[3] = {(f16)0.0f, (f16)0.0f, (f16)1.0f};
   if constexpr (KSPLIT == 4) {
     const int n0 = blockIdx.x * 16;
-    const int eoff = (wave == 0 && g == 0 && n0 + j < p.N) ? (n0 + j) * 2 : kOutOfRange;
+    const int eoff = (wave == 0 && n0 + j < p.N) ? (n0 + j) * 2 : kOutOfRange;
     const size_t nb = (size_t)p.N * 2;
     ek[0] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? nb : 0), eoff, 0, 0));
     ek[1] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.residual, p.residual ? nb : 0), eoff, 0, 0));
@@ -186,53 +204,73 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
       ek[2] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.scales, nb), eoff, 0, 0));
   }
 
-  // ---- stage the activation row (slot order, factors), its zero twin and the block bias sums ----
+  // ---- stage the activation rows (slot order, factors), the zero region and the block bias sums.
+  // Rows m >= M are not staged (no lane reads them); their block sums are zero.  Loads go out XU
+  // per thread at a time, so a batch costs one memory round trip. ----
   {
-    const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.x, (size_t)K * 2);
-    h8 xv[XPER];
+    constexpr int TOTAL = MP * NB;
+    constexpr int ITER = (TOTAL + NT - 1) / NT;
+    constexpr int XU = ITER < 8 ? ITER : 8;
+    for (int base = 0; base < ITER; base += XU) {  // uniform trip counts: the shuffles see every lane
+      h8 xv[XU];
 #pragma unroll
-    for (int i = 0; i < XPER; ++i) {
-      const int b = t + 256 * i;
-      xv[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xbuf, b < NB ? b * 16 : kOutOfRange, 0, 0));
-    }
-#pragma unroll
-    for (int i = 0; i < XPER; ++i) {
-      const int b = t + 256 * i;
-      h8 v;
-      float bsum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[e] = (f16)((float)xv[i][SL::perm[e]] * SL::factor[e]);
-        bsum += (float)v[e] * SL::bias[e];
+      for (int i = 0; i < XU; ++i) {
+        const int idx = (base + i) * NT + t;
+        const int m = idx / NB, b = idx - m * NB;
+        const bool live = base + i < ITER && idx < TOTAL && m < p.M && 8 * b < K;
+        xv[i] = __builtin_bit_cast(
+            h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x + (size_t)(live ? m : 0) * p.ldx, (size_t)K * 2),
+                                                      live ? b * 16 : kOutOfRange, 0, 0));
       }
-      bsum += __shfl_xor(bsum, 1, 64);
-      if constexpr (CPL == 32) bsum += __shfl_xor(bsum, 2, 64);
-      if (b < NB) {
-        *reinterpret_cast<h8 *>(xs + 8 * b) = v;
-        *reinterpret_cast<h8 *>(xz + 8 * b) = h8{};
-        if (b % (CPL / 8) == 0) xb[b / (CPL / 8)] = bsum;
+#pragma unroll
+      for (int i = 0; i < XU; ++i) {
+        const int idx = (base + i) * NT + t;
+        const int m = idx / NB, b = idx - m * NB;
+        const bool live = idx < TOTAL && m < p.M;
+        h8 v;
+        float bsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[e] = (f16)((float)xv[i][SL::perm[e]] * SL::factor[e]);
+          bsum += (float)v[e] * SL::bias[e];
+        }
+        bsum += __shfl_xor(bsum, 1, 64);
+        if constexpr (CPL == 32) bsum += __shfl_xor(bsum, 2, 64);
+        if (base + i < ITER && idx < TOTAL) {
+          if (live) *reinterpret_cast<h8 *>(xs + m * KP + 8 * b) = v;
+          if (m == 0) *reinterpret_cast<h8 *>(xz + 8 * b) = h8{};
+          if (b % (CPL / 8) == 0) xb[m * XBLD + b / (CPL / 8)] = live ? bsum : 0.0f;
+        }
       }
     }
-    if (t < 16) xb[KP / CPL + t] = 0.0f;
+    for (int idx = t; idx < MP * 16; idx += NT) xb[(idx / 16) * XBLD + KP / CPL + idx % 16] = 0.0f;
   }
   __syncthreads();
 
-  // A operand of load position u' (0..3) of a window: lane (j, g) is row j of the MFMA A matrix and
-  // is active for position u' when j == 4 u' + g; inactive lanes read zeros.
-  const f16 *abase[4];
+  // A operand of load position v (0 .. WL-1) of a window: lane (j, g) is A row j = (m, r) with
+  // m = j / R, r = j % R, active when m < M and (R >= 4) r == 4 v + g or (R < 4) r == g / BPR.
+  const f16 *abase[WL];
+  {
+    const int m = j / R, r = j % R;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) abase[v] = (j == 4 * v + g ? xs : xz) + g * CPL;
+    for (int v = 0; v < WL; ++v) {
+      const bool active = m < p.M && (R >= 4 ? r == 4 * v + g : r == g / BPR);
+      abase[v] = (active ? xs + m * KP : xz) + g * CPL;
+    }
+  }
 
-  float tot = 0.0f;
+  float tot[NMR];
+#pragma unroll
+  for (int i = 0; i < NMR; ++i) tot[i] = 0.0f;
   auto consume = [&](Buf &b, int chunk) {
 #pragma unroll
     for (int w = 0; w < WIN; ++w) {
-      const int k0 = (chunk * CH + 4 * w) * CPW;  // first code of the window (uniform)
+      const int k0 = (chunk * CH + w * WL) * CPW;  // first code of the window (uniform)
       if (k0 >= K) break;
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int u = 4 * w + v;
+      for (int v = 0; v < WL; ++v) {
+        const int u = w * WL + v;
         if (u >= CH) break;
         const int kb = k0 + v * CPW;
         if (kb >= K) break;
@@ -244,26 +282,52 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, stream_decode<FMT>(b.w[u], q), acc, 0, 0, 0);
         }
       }
-      // Lane (j, g) holds rows 4g + r: the blocks r of the window's load g.
-      const f4 bias = *reinterpret_cast<const f4 *>(xb + (k0 + g * CPW) / CPL);
+      // Lane (j, g) holds A rows 4g + r' (r' = 0..3) of output row j.
+      if constexpr (R >= 4) {
+        const int v = (4 * g % R) / 4;           // the window load of these rows
+        const int m = 4 * g / R;                 // their activation row
+        const f4 bias = *reinterpret_cast<const f4 *>(xb + m * XBLD + (k0 + v * CPW) / CPL);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s;
-        if constexpr (SCALED) s = (float)b.s[w * NS + (r * NS) / 4];
-        else s = (4 * w + g < CH) ? 1.0f : 0.0f;
-        tot += s * (acc[r] - bias[r]);
+        for (int r = 0; r < 4; ++r) {
+          float s;
+          if constexpr (SCALED) s = (float)b.s[w * NSL + (r * NS) / 4];
+          else s = (w * WL + v < CH) ? 1.0f : 0.0f;
+          tot[0] += s * (acc[r] - bias[r]);
+        }
+      } else {
+#pragma unroll
+        for (int mi = 0; mi < NMR; ++mi) {
+          const int m = 4 * g / R + mi;
+          const f4 bias4 = *reinterpret_cast<const f4 *>(xb + m * XBLD + k0 / CPL);
+#pragma unroll
+          for (int rr = 0; rr < R; ++rr) {
+            float bias = 0.0f;
+#pragma unroll
+            for (int q = 0; q < BPR; ++q) bias += bias4[rr * BPR + q];
+            const float s = SCALED ? (float)b.s[w * NSL + (rr * BPR * NS) / 4] : 1.0f;
+            tot[mi] += s * (acc[mi * R + rr] - bias);
+          }
+        }
       }
     }
   };
-  auto finish = [&](float v, const f16 *e, int n0) -> void {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (g == 0 && n0 + j < p.N) {
-      if constexpr (!SCALED) v *= (float)e[2];
-      f16 h = (f16)v;
+  // Final row sums of a tile: lanes of one activation row are reduced (R >= 8), then the owners
+  // write y[m, n0 + j] with the reference's epilogue staging.
+  auto finish = [&](float *v, const f16 *e, int n0) -> void {
+    if constexpr (R >= 8) v[0] += __shfl_xor(v[0], 16, 64);
+    if constexpr (R >= 16) v[0] += __shfl_xor(v[0], 32, 64);
+    const bool owner = R >= 4 ? (4 * g % R) == 0 : true;
+    if (!owner || n0 + j >= p.N) return;
+#pragma unroll
+    for (int mi = 0; mi < NMR; ++mi) {
+      const int m = 4 * g / R + mi;
+      if (m >= p.M) continue;
+      float a = v[mi];
+      if constexpr (!SCALED) a *= (float)e[2];
+      f16 h = (f16)a;
       if (p.bias) h = (f16)((float)h + (float)e[0]);
       if (p.residual) h = (f16)((float)e[1] + (float)h);
-      p.y[n0 + j] = h;
+      p.y[(size_t)m * p.ldy + n0 + j] = h;
     }
   };
 
@@ -277,7 +341,8 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
         if constexpr (KSPLIT == 1) {
           if (c_chunk == C - 1) {
             finish(tot, buf[s].e, c_tile * 16);
-            tot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NMR; ++i) tot[i] = 0.0f;
           }
         }
         advance(c_tile, c_chunk);
@@ -285,18 +350,22 @@ __global__ __launch_bounds__(256) void stream_gemv_kernel(StreamParams p) {
     }
   }
   if constexpr (KSPLIT == 4) {
-    float v = tot;
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = v;
+    if (wave > 0) {
+#pragma unroll
+      for (int i = 0; i < NMR; ++i) red[((wave - 1) * 64 + lane) * NMR + i] = tot[i];
+    }
     __syncthreads();
     if (wave == 0) {
-      if (g == 0) v = ((v + red[j]) + red[16 + j]) + red[32 + j];
-      else v = 0.0f;
-      // finish() reduces over the lane groups again: only lanes g == 0 carry the sum
-      finish(v, ek, blockIdx.x * 16);
+#pragma unroll
+      for (int i = 0; i < NMR; ++i)
+        tot[i] = ((tot[i] + red[lane * NMR + i]) + red[(64 + lane) * NMR + i]) + red[(128 + lane) * NMR + i];
+      finish(tot, ek, blockIdx.x * 16);
     }
   }
 }
+
+// Launches stream_gemv_kernel for p.M <= 16 rows (defined with the decode launchers); `ns` is
+// stream_group_span of the shape, and stream_rows_ok must hold for p.M > 1.
+void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t stream);
 
 }  // namespace lb

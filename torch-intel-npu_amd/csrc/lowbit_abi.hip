@@ -11,6 +11,7 @@
 #include "../../include/lowbit_hip.h"
 #include "abi_util.h"
 #include "fused_launch.h"
+#include "lb_stream.h"
 #include "lb_gemm.h"
 #include "lb_kernels.h"
 #include "lb_variants.h"
@@ -20,7 +21,7 @@ using namespace lb::abi;
 
 namespace {
 
-enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3 };
+enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4 };
 enum Variant { VAR_PLAIN = 0, VAR_COMPACT = 1, VAR_W8A8 = 2 };
 constexpr int kCompactMaxGroups = 32;
 constexpr int64_t kW8A8MaxK = 131072;  // |sum| <= K * 128 * 127 stays inside int32
@@ -155,6 +156,17 @@ bool row_eligible(const lb_linear_args *a) {
   return true;
 }
 
+#ifndef LB_STREAM_ROWS_MIN_BYTES
+#define LB_STREAM_ROWS_MIN_BYTES (64ll << 20)  // weights from which 2..16-row calls take stream_gemv_kernel
+#endif
+
+// Several activation rows, no correction, a long enough weight the stream kernel takes.
+bool stream_rows_eligible(const lb_linear_args *a) {
+  if (a->rank > 0 || !stream_rows_ok((int)a->format, a->M, a->K, a->group_size)) return false;
+  const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
+  return bytes >= LB_STREAM_ROWS_MIN_BYTES;
+}
+
 // Workspace and kernel path of the compact_groups and W8A8 variants.
 Plan make_variant_plan(const lb_linear_args *a, int variant) {
   Plan pl;
@@ -195,13 +207,15 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
   Plan pl;
   const int fmt = (int)a->format;
   if (a->flags & LB_FLAG_FORCE_STREAM) {  // validated: the stream kernel takes the shape
-    pl.path = PATH_ROW;
+    pl.path = a->M == 1 ? PATH_ROW : PATH_STREAM;
   } else if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) {
     pl.path = PATH_GENERIC;
   } else if (a->flags & LB_FLAG_FORCE_GEMM) {
     pl.path = PATH_GEMM;
   } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && row_eligible(a)) {
     pl.path = PATH_ROW;
+  } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && stream_rows_eligible(a)) {
+    pl.path = PATH_STREAM;
   } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) {
     pl.path = PATH_GEMV;
   } else {
@@ -290,12 +304,14 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
   if (__builtin_popcount(a->flags & kForce) > 1)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: at most one LB_FLAG_FORCE_* flag");
   if (a->flags & LB_FLAG_FORCE_STREAM) {
-    if ((a->flags & (LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8)) || a->M != 1 || a->rank > 0 ||
-        stream_group_span((int)a->format, a->K, a->group_size) == 0 || !aligned(a->codes, 16) || !aligned(a->x, 16))
+    const bool shape = a->M == 1 ? stream_group_span((int)a->format, a->K, a->group_size) != 0
+                                 : stream_rows_ok((int)a->format, a->M, a->K, a->group_size);
+    if ((a->flags & (LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8)) || a->rank > 0 || !shape || !aligned(a->codes, 16) ||
+        !aligned(a->x, 16) || a->ldx % 8 != 0)
       return fail(LB_UNSUPPORTED,
-                  "lb_linear: LB_FLAG_FORCE_STREAM needs M == 1, int4/int8 codes, no correction or variant, "
-                  "K <= 16384 (a multiple of 32 / 16), groups spanning whole 128 / 64-code pieces, "
-                  "16-byte aligned codes/x");
+                  "lb_linear: LB_FLAG_FORCE_STREAM needs int4/int8 codes, no correction or variant, 16-byte aligned "
+                  "codes/x rows, and M == 1 with K <= 16384 (a multiple of 32 / 16) and groups spanning whole "
+                  "128 / 64-code pieces, or 2 <= M <= 16 with K <= 4096 and longer groups as M grows");
   }
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {
@@ -607,6 +623,24 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     }
     for (FusedProblem &r : fp.prob) r.tiles_end = tiles;
     launch_fused(fp, fmt, scaled, a->rank > 0, tiles, s);
+    return launch_status("lb_linear");
+  }
+  if (plan.path == PATH_STREAM) {
+    StreamParams sp{};
+    sp.x = p.x;
+    sp.codes = p.codes;
+    sp.scales = p.scales;
+    sp.y = p.y;
+    sp.bias = p.bias;
+    sp.M = p.M;
+    sp.N = p.N;
+    sp.K = p.K;
+    sp.G = p.G;
+    sp.group_shift = p.group_shift;
+    sp.ldx = p.ldx;
+    sp.ldy = p.ldy;
+    sp.tiles = (int)((a->N + 15) / 16);
+    launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
     return launch_status("lb_linear");
   }
   uint8_t *ws = static_cast<uint8_t *>(a->workspace);

@@ -216,5 +216,193 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
     }
 }
 
+// 256 x 256 prefill GEMM (large problems).  WAVES = 4 or 8 waves in a 2 x (WAVES / 2) grid;
+// a wave owns a 128 x (512 / WAVES) block of v_mfma_f32_32x32x16_f16 tiles (4 x TN), whose fp32
+// accumulators live in AGPRs.  Per K step of 64 and 16-deep substep, a wave reads 4 A and TN B
+// fragments for its 4 TN MFMAs.  LDS holds two stages of A (fp16 activations) and B (decoded fp16
+// weights), 256 rows x 64 halves each, without padding: the 16-byte chunk c of row r is stored at
+// chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.  The next step's
+// activations and packed weights are loaded into registers one step ahead; they are decoded and
+// written to the other LDS stage between the MFMA groups of the current step, and one barrier per
+// step separates the stages.  Fragment reads of substep kk + 1 are issued before the MFMAs of
+// substep kk.
+template <int FMT, bool SCALED, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int NT = 64 * WAVES;
+  constexpr int WN = WAVES / 2;                     // waves along N
+  constexpr int TN = 8 / WN;                        // 32-column MFMA tiles per wave
+  constexpr int WCOLS = 32 * TN;                    // columns per wave
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  constexpr int CODES = 16 * 8 / BITS;              // codes per 16-byte B chunk
+  constexpr int B_ROW_CHUNKS = BK / CODES;          // packed chunks per B row per step
+  constexpr int B_PER = BN * B_ROW_CHUNKS / NT;     // packed B chunks per thread per step
+  constexpr int A_PER = BM * (BK / 8) / NT;         // A chunks per thread per step
+  constexpr int STAGE = BM * BK;                    // halves per operand per stage
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert((WAVES == 4 || WAVES == 8) && B_PER >= 1, "tile constants");
+  __shared__ __align__(16) f16 As[2 * STAGE];
+  __shared__ __align__(16) f16 Bs[2 * STAGE];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  select_slice(p);
+
+  const int rows_a = min(BM, p.M - bm), rows_b = min(BN, p.N - bn);
+  const int row_bytes = p.code_ld;
+  const __amdgpu_buffer_rsrc_t xbuf =
+      buffer_rsrc(p.x + (size_t)bm * p.ldx, rows_a > 0 ? ((size_t)(rows_a - 1) * p.ldx + p.K) * 2 : 0);
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(p.codes + (size_t)bn * row_bytes, (size_t)rows_b * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      buffer_rsrc(SCALED ? p.scales + (size_t)bn * p.G : p.scales, SCALED ? (size_t)rows_b * p.G * 2 : 0);
+
+  // Global byte offsets at k = 0 and LDS slots of this thread's chunks.
+  int a_off[A_PER], a_lds[A_PER], b_off[B_PER], s_off[B_PER], b_row[B_PER], b_code[B_PER];
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int c = tid + NT * i, r = c >> 3, lc = c & 7;
+    a_off[i] = r < rows_a ? (r * p.ldx + 8 * lc) * 2 : kOutOfRange;
+    a_lds[i] = r * BK + 8 * (lc ^ (r & 7));
+  }
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) {
+    const int c = tid + NT * i, r = c / B_ROW_CHUNKS, kc = (c % B_ROW_CHUNKS) * CODES;
+    const bool ok = r < rows_b;
+    b_off[i] = ok ? r * row_bytes + kc * BITS / 8 : kOutOfRange;
+    s_off[i] = ok ? r * p.G * 2 : kOutOfRange;
+    b_row[i] = r;
+    b_code[i] = kc;
+  }
+  u4 ra[A_PER], rb[B_PER];
+  f16 rs[B_PER];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i)
+      ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, a_off[i] + k0 * 2, 0, 0));
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, b_off[i] + k0 * BITS / 8, 0, 0));
+      if constexpr (SCALED)
+        rs[i] = __builtin_bit_cast(
+            f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, s_off[i] + (((k0 + b_code[i]) >> p.group_shift) << 1), 0, 0));
+    }
+  };
+  auto store_a = [&](int st) {
+    f16 *dst = As + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      asm volatile("" : "+v"(ra[i]));
+      *reinterpret_cast<u4 *>(dst + a_lds[i]) = ra[i];
+    }
+  };
+  auto store_b = [&](int st) {
+    f16 *dst = Bs + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      asm volatile("" : "+v"(rb[i]));
+      const int r = b_row[i];
+      const h2 s2 = SCALED ? h2{rs[i], rs[i]} : h2{(f16)1.0f, (f16)1.0f};
+      constexpr int HALF_CHUNKS = CODES / 8;  // LDS chunks one packed chunk decodes to
+#pragma unroll
+      for (int q = 0; q < HALF_CHUNKS; ++q) {
+        const int lc = b_code[i] / 8 + q;
+        h8 v;
+        if constexpr (BITS == 4) v = decode8_natural<FMT, SCALED>(rb[i][q], 0u, s2, nf4_table);
+        else if constexpr (BITS == 8) v = decode8_natural<FMT, SCALED>(rb[i][2 * q], rb[i][2 * q + 1], s2, nf4_table);
+        else v = __builtin_bit_cast(h8, rb[i]);
+        *reinterpret_cast<h8 *>(dst + r * BK + 8 * (lc ^ (r & 7))) = v;
+      }
+    }
+  };
+
+  f16x acc[4][TN];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
+
+  // Fragment of tile row `row` (lane row lane & 31) at logical chunk 2 kk + lane / 32.
+  const int fr = lane & 31, fh = lane >> 5;
+  auto frag = [&](const f16 *base, int row, int kk) -> h8 {
+    const int lc = 2 * kk + fh;
+    return *reinterpret_cast<const h8 *>(base + row * BK + 8 * (lc ^ (row & 7)));
+  };
+
+  const int steps = p.K / BK;
+  load(0);
+  store_a(0);
+  store_b(0);
+  if (steps > 1) load(BK);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int st = s & 1;
+    const f16 *a_base = As + st * STAGE;
+    const f16 *b_base = Bs + st * STAGE;
+    h8 fa[2][4], fb[2][TN];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[0][i] = frag(a_base, wm * 128 + i * 32 + fr, 0);
+#pragma unroll
+    for (int jj = 0; jj < TN; ++jj) fb[0][jj] = frag(b_base, wn * WCOLS + jj * 32 + fr, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int cur = kk & 1;
+      if (kk < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[cur ^ 1][i] = frag(a_base, wm * 128 + i * 32 + fr, kk + 1);
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj) fb[cur ^ 1][jj] = frag(b_base, wn * WCOLS + jj * 32 + fr, kk + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][jj], acc[i][jj], 0, 0, 0);
+      // The next step's operands go to the other stage between the MFMA groups.
+      if (s + 1 < steps) {
+        if (kk == 1) store_a(st ^ 1);
+        if (kk == 2) {
+          store_b(st ^ 1);
+          if (s + 2 < steps) load((s + 2) * BK);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  // One call per tile keeps every accumulator index compile-time (the tiles stay in AGPRs).
+  auto emit = [&](const f16x &v, int i, int jj) {
+    const int n = bn + wn * WCOLS + jj * 32 + (lane & 31);
+    if (n >= p.N) return;
+    const float rs = p.per_row ? (float)p.scales[n] : 1.0f;
+    const float b = p.bias ? (float)p.bias[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = bm + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (m >= p.M) continue;
+      f16 h = (f16)(v[r] * rs);
+      if (p.bias) h = (f16)((float)h + b);
+      if (p.delta) h = (f16)((float)h + (float)p.delta[(size_t)m * p.N + n]);
+      p.y[(size_t)m * p.ldy + n] = h;
+    }
+  };
+  emit(acc[0][0], 0, 0); emit(acc[0][1], 0, 1);
+  emit(acc[1][0], 1, 0); emit(acc[1][1], 1, 1);
+  emit(acc[2][0], 2, 0); emit(acc[2][1], 2, 1);
+  emit(acc[3][0], 3, 0); emit(acc[3][1], 3, 1);
+  if constexpr (TN == 4) {
+    emit(acc[0][2], 0, 2); emit(acc[0][3], 0, 3);
+    emit(acc[1][2], 1, 2); emit(acc[1][3], 1, 3);
+    emit(acc[2][2], 2, 2); emit(acc[2][3], 2, 3);
+    emit(acc[3][2], 3, 2); emit(acc[3][3], 3, 3);
+  }
+}
+
 }  // namespace lb
 

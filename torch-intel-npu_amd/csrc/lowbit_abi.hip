@@ -414,13 +414,26 @@ void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kg, int kc, hi
 #ifndef LB_GEMM_BK
 #define LB_GEMM_BK 64
 #endif
-// Large tiles when they alone give every CU a workgroup, else 64 x 64 tiles (k steps of 64
-// where K allows, else 32).
+#ifndef LB_GEMM_BIG_MIN
+#define LB_GEMM_BIG_MIN 256  // large tiles from this many workgroups
+#endif
+#ifndef LB_GEMM4_WAVES
+#define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
+#endif
+#ifndef LB_GEMM4_MIN_TILES
+#define LB_GEMM4_MIN_TILES 192  // 256 x 256 tiles from this many workgroups
+#endif
+// 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs, else 128 x 128 tiles when they
+// alone give every CU a workgroup, else 64 x 64 tiles (k steps of 64 where K allows, else 32).
 template <int FMT, bool SCALED>
 void launch_gemm_t(const LinearParams &p, hipStream_t s) {
   constexpr int BM = LB_GEMM_BM, BN = LB_GEMM_BN, BK = LB_GEMM_BK;
+  const int64_t huge = ((p.M + 255) / 256) * ((p.N + 255) / 256) * p.slices;
   const int64_t big = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * p.slices;
-  if (big >= 256 && p.K % BK == 0) {
+  if (huge >= LB_GEMM4_MIN_TILES && p.K % 64 == 0) {
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, p.slices),
+                       dim3(64 * LB_GEMM4_WAVES), 0, s, p);
+  } else if (big >= LB_GEMM_BIG_MIN && p.K % BK == 0) {
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>),
                        dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, p.slices), dim3(256), 0, s, p);
   } else if (p.K % 64 == 0) {

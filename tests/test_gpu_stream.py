@@ -100,10 +100,10 @@ def test_stream_activation_magnitudes(device, xscale):
     check(p, run(p, device, STREAM), f'stream xscale {xscale}')
 
 
-@pytest.mark.parametrize('fmt,group', [('int4', 64), ('int8', 576)])
+@pytest.mark.parametrize('fmt,group', [('int4', 64), ('int4', 576)])
 def test_stream_residual_through_fused_linear(device, fmt, group):
-    """One problem without prologue or correction in lb_fused_linear, above the size threshold:
-    y = fp16(residual + fp16(x W^T)).  Random codes; the oracle checks row slices."""
+    """One INT4 problem without prologue or correction in lb_fused_linear, above the size
+    threshold: y = fp16(residual + fp16(x W^T)).  Random codes; the oracle checks row slices."""
     n, k = 262144 if fmt == 'int4' else 131072, 576
     announce('stream residual', fmt, group)
     rng = np.random.default_rng(21)

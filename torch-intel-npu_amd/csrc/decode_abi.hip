@@ -144,9 +144,10 @@ bool launch_rows(const FusedParams &p, int tiles, hipStream_t s) {
   return false;
 }
 
-// stream_gemv_kernel takes one-row calls with rows longer than LB_STREAM_MIN_K or at least
-// LB_STREAM_MIN_BYTES of weights (measured on MI355X: below both, the single-tile kernels, whose
-// workgroups issue every load at once, finish first).
+// stream_gemv_kernel takes one-row INT4 calls with rows longer than LB_STREAM_MIN_K or at least
+// LB_STREAM_MIN_BYTES of weights, and INT8 rows longer than the single-tile kernel holds (measured
+// on MI355X: otherwise the single-tile kernels, whose workgroups issue every load at once, finish
+// first).
 #ifndef LB_STREAM_MIN_BYTES
 #define LB_STREAM_MIN_BYTES (64ll << 20)
 #endif
@@ -161,6 +162,9 @@ bool launch_rows(const FusedParams &p, int tiles, hipStream_t s) {
 #endif
 #ifndef LB_STREAM_PD
 #define LB_STREAM_PD 2                 // chunks in flight per wave
+#endif
+#ifndef LB_STREAM_CH
+#define LB_STREAM_CH 8                 // 16-byte loads per lane per chunk (rows longer than 640 codes)
 #endif
 
 // Compute units of the current device (cached per device ordinal).
@@ -182,7 +186,7 @@ constexpr int stream_waves() { return KSPLIT == 4 || MP <= 4 ? 4 : MP == 8 ? 8 :
 
 template <int FMT, bool SCALED, int NS, int KMAX, int KSPLIT, int MP>
 void launch_stream_k(const StreamParams &p, int grid, hipStream_t s) {
-  constexpr int CH = KMAX <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
+  constexpr int CH = KMAX <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : MP == 1 ? LB_STREAM_CH : 8;
   constexpr int WAVES = stream_waves<MP, KSPLIT>();
   hipLaunchKernelGGL((stream_gemv_kernel<FMT, SCALED, NS, KMAX, CH, LB_STREAM_PD, KSPLIT, MP, WAVES>), dim3(grid),
                      dim3(64 * WAVES), 0, s, p);
@@ -198,7 +202,7 @@ void launch_stream_m(StreamParams p, hipStream_t s) {
   constexpr int CPL = StreamTraits<FMT>::CPL, CPW = 4 * CPL;
   const int cus = device_cus();
   const int kmax = MP > 1 ? 4096 : p.K <= 640 ? 640 : p.K <= 4096 ? 4096 : 16384;
-  const int ch = kmax <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : 8;
+  const int ch = kmax <= 640 ? (FMT == FMT_INT4 ? 5 : 10) : MP == 1 ? LB_STREAM_CH : 8;
   p.chunks = (p.K + ch * CPW - 1) / (ch * CPW);
   if constexpr (MP <= 4) {  // more rows stage too much per workgroup for one tile each
     if (kmax > 640 && p.chunks >= 4 && p.tiles < LB_STREAM_SPLIT_TILES_PER_CU * cus) {
@@ -254,8 +258,9 @@ bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
     const int ns = stream_group_span(FMT, p.K, SCALED ? p.K / p.G : p.K);
     if (ns == 0) return false;
     const int64_t weight_bytes = (int64_t)q.N * p.K * StreamTraits<FMT>::BITS / 8;
-    if (!p.force_stream && p.K <= fused_kmax_limit(FMT) && weight_bytes < LB_STREAM_MIN_BYTES &&
-        p.K <= LB_STREAM_MIN_K)
+    // INT8 rows the single-tile kernel holds stay there (it measured faster at every size).
+    if (!p.force_stream && p.K <= fused_kmax_limit(FMT) &&
+        (FMT == FMT_INT8 || (weight_bytes < LB_STREAM_MIN_BYTES && p.K <= LB_STREAM_MIN_K)))
       return false;
     StreamParams sp{};
     sp.x = p.x;

@@ -13,6 +13,8 @@
 // register is never copied before its load completes).  The epilogue is the linear path's
 // (store_output): per-row scale, fp16, bias, correction.
 #pragma once
+#include <type_traits>
+
 #include "lb_kernels.h"
 
 namespace lb {
@@ -20,6 +22,11 @@ namespace lb {
 #ifndef LB_GEMM_IGLP
 #define LB_GEMM_IGLP 0
 #endif
+// LDS swizzle of the 256 x 256 GEMM: row r stores chunk c at c ^ LB_G4_SWZ(r).
+#ifndef LB_GEMM4_SWZ_SHIFT
+#define LB_GEMM4_SWZ_SHIFT 0
+#endif
+#define LB_G4_SWZ(r) (((r) >> LB_GEMM4_SWZ_SHIFT) & 7)
 #ifndef LB_GEMM_IGLP_VALU
 #define LB_GEMM_IGLP_VALU 4
 #endif
@@ -266,7 +273,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   for (int i = 0; i < A_PER; ++i) {
     const int c = tid + NT * i, r = c >> 3, lc = c & 7;
     a_off[i] = r < rows_a ? (r * p.ldx + 8 * lc) * 2 : kOutOfRange;
-    a_lds[i] = r * BK + 8 * (lc ^ (r & 7));
+    a_lds[i] = r * BK + 8 * (lc ^ LB_G4_SWZ(r));
   }
 #pragma unroll
   for (int i = 0; i < B_PER; ++i) {
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
         if constexpr (BITS == 4) v = decode8_natural<FMT, SCALED>(rb[i][q], 0u, s2, nf4_table);
         else if constexpr (BITS == 8) v = decode8_natural<FMT, SCALED>(rb[i][2 * q], rb[i][2 * q + 1], s2, nf4_table);
         else v = __builtin_bit_cast(h8, rb[i]);
-        *reinterpret_cast<h8 *>(dst + r * BK + 8 * (lc ^ (r & 7))) = v;
+        *reinterpret_cast<h8 *>(dst + r * BK + 8 * (lc ^ LB_G4_SWZ(r))) = v;
       }
     }
   };
@@ -327,12 +334,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
 
-  // Fragment of tile row `row` (lane row lane & 31) at logical chunk 2 kk + lane / 32.
+  // Fragment reads: lane row fr = lane & 31 of a tile at logical chunk 2 kk + lane / 32.  Every
+  // tile row is fr plus a multiple of 8, so the swizzle (chunk ^ (row & 7)) is a per-lane constant
+  // and a read is a per-lane base plus compile-time offsets (tile, stage) and one of four chunk
+  // offsets.
   const int fr = lane & 31, fh = lane >> 5;
-  auto frag = [&](const f16 *base, int row, int kk) -> h8 {
-    const int lc = 2 * kk + fh;
-    return *reinterpret_cast<const h8 *>(base + row * BK + 8 * (lc ^ (row & 7)));
-  };
+  int koff[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) koff[kk] = 8 * ((2 * kk + fh) ^ LB_G4_SWZ(fr));
+  const f16 *a_lane = As + (wm * 128 + fr) * BK;
+  const f16 *b_lane = Bs + (wn * WCOLS + fr) * BK;
 
   const int steps = p.K / BK;
   load(0);
@@ -340,23 +351,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   store_b(0);
   if (steps > 1) load(BK);
   __syncthreads();
-  for (int s = 0; s < steps; ++s) {
-    const int st = s & 1;
-    const f16 *a_base = As + st * STAGE;
-    const f16 *b_base = Bs + st * STAGE;
+  // One K step on LDS stage ST (compile-time, so every LDS offset is an immediate).
+  auto step = [&](auto stage, int s) {
+    constexpr int ST = decltype(stage)::value;
+    const f16 *a_base = a_lane + ST * STAGE;
+    const f16 *b_base = b_lane + ST * STAGE;
     h8 fa[2][4], fb[2][TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[0][i] = frag(a_base, wm * 128 + i * 32 + fr, 0);
+    for (int i = 0; i < 4; ++i) fa[0][i] = *reinterpret_cast<const h8 *>(a_base + i * 32 * BK + koff[0]);
 #pragma unroll
-    for (int jj = 0; jj < TN; ++jj) fb[0][jj] = frag(b_base, wn * WCOLS + jj * 32 + fr, 0);
+    for (int jj = 0; jj < TN; ++jj) fb[0][jj] = *reinterpret_cast<const h8 *>(b_base + jj * 32 * BK + koff[0]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int cur = kk & 1;
       if (kk < 3) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fa[cur ^ 1][i] = frag(a_base, wm * 128 + i * 32 + fr, kk + 1);
+        for (int i = 0; i < 4; ++i)
+          fa[cur ^ 1][i] = *reinterpret_cast<const h8 *>(a_base + i * 32 * BK + koff[kk + 1]);
 #pragma unroll
-        for (int jj = 0; jj < TN; ++jj) fb[cur ^ 1][jj] = frag(b_base, wn * WCOLS + jj * 32 + fr, kk + 1);
+        for (int jj = 0; jj < TN; ++jj)
+          fb[cur ^ 1][jj] = *reinterpret_cast<const h8 *>(b_base + jj * 32 * BK + koff[kk + 1]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -365,14 +379,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
           acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][jj], acc[i][jj], 0, 0, 0);
       // The next step's operands go to the other stage between the MFMA groups.
       if (s + 1 < steps) {
-        if (kk == 1) store_a(st ^ 1);
+        if (kk == 1) store_a(ST ^ 1);
         if (kk == 2) {
-          store_b(st ^ 1);
+          store_b(ST ^ 1);
           if (s + 2 < steps) load((s + 2) * BK);
         }
       }
     }
     __syncthreads();
+  };
+  for (int s = 0; s < steps; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < steps) step(std::integral_constant<int, 1>{}, s + 1);
   }
 
   // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.

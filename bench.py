@@ -19,6 +19,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cp
        python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
        python bench.py --decode-only      (config-4 decode leg alone, for rocprofv3 --kernel-trace)
        python bench.py --profile-gemm     (prefill GEMMs + hipBLASLt fp16 of the same shapes, for --pmc)
+       python bench.py --profile-stream   (config-5 128256x4096 INT4 GEMV at M=1 + a copy, for rocprofv3)
 """
 import argparse
 import json
@@ -318,9 +319,10 @@ def decode_leg(device, steps, cpu_steps):
     return out
 
 
-def profile_kernel(device, stream):
-    """Dominant kernel (lm_head INT4 GEMV, M=1) over its replica pool, then a known-size copy."""
-    name, n, k, g = SMOL_SHAPES[-1]
+def profile_kernel(device, stream, shape=None):
+    """One M=1 INT4 GEMV over its replica pool (default: the dominant kernel, the config-2 lm_head),
+    then a known-size copy (the PMC calibration kernel)."""
+    name, n, k, g = shape or SMOL_SHAPES[-1]
     lin = Linear(make_weight('int4', n, k, g, 107), 1, copies_for(algorithmic_bytes('int4', 0, n, k, g)),
                  device, 207)
     for _ in range(4):
@@ -331,7 +333,7 @@ def profile_kernel(device, stream):
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps(dict(profile='lm_head int4 g64 M=1', launches=4 * len(lin.calls),
+    print(json.dumps(dict(profile=f'{name} {n}x{k} int4 g{g} M=1', launches=4 * len(lin.calls),
                           algorithmic_bytes=lin.bytes, copy_bytes=src.numel())), flush=True)
 
 
@@ -370,6 +372,8 @@ def main():
     ap.add_argument('--decode-steps', type=int, default=128)
     ap.add_argument('--decode-only', action='store_true', help='only the config-4 decode leg (for tracing)')
     ap.add_argument('--profile-gemm', action='store_true', help='prefill GEMMs alone (for rocprofv3 --pmc)')
+    ap.add_argument('--profile-stream', action='store_true',
+                    help='the config-5 128256x4096 INT4 GEMV (M=1, stream kernel) alone, for rocprofv3')
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -389,6 +393,9 @@ def main():
         return
     if args.profile_gemm:
         profile_gemm(device, stream)
+        return
+    if args.profile_stream:
+        profile_kernel(device, stream, LLAMA_SHAPES[-1])
         return
     if args.decode_only:
         decode = decode_leg(device, args.decode_steps, 0)
@@ -448,7 +455,9 @@ def main():
             'hbm_frac_of_pass': round(head['gbs'] / HBM_PEAK_GBS, 4),
         },
         'roofline': {
-            'kernel': 'fused_gemv_kernel<INT4> (one-row lb_linear) lm_head 49152x576 g64, M=1',
+            'kernel': 'rows_gemv_kernel<INT4, KMAX 640, 4 tiles per workgroup> (one-row lb_linear) '
+                      'lm_head 49152x576 g64, M=1',
+            'profile': 'profiles/rows_gemv_int4_lm_head_49152x576_m1.md',
             'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
             'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_per_launch(),
             'algorithmic_bytes_per_launch': lm.bytes, 'avg_launch_us': dominant['us'],

@@ -190,6 +190,22 @@ def test_compact_random(device, fmt, m, k, n, group, path):
     assert np.mean(bits(got) == bits(want)) >= 0.95
 
 
+@pytest.mark.parametrize('fmt', ['int4', 'int8'])
+def test_compact_large_grid_slices(device, fmt):
+    """Grid slices of a compact call large enough for the 256 x 256 GEMM (2 x 24 tiles x 4 groups)."""
+    m, k, n, group = 512, 512, 6144, 128
+    announce('compact large', fmt)
+    rng = np.random.default_rng(513)
+    data, scales = o.quantize(rng.standard_normal((n, k)) / 8, fmt, group)
+    x = (rng.standard_normal((m, k)) / 8).astype(np.float16)
+    got = run(device, x, fmt, (n, k), group, data, scales, flags=lowbit_hip.FLAG_COMPACT_GROUPS)
+    assert np.isfinite(got).all()
+    reference_gate(x, fmt, (n, k), group, data, scales, got, None)
+    want = o.compact_linear(x, fmt, (n, k), group, data, scales)
+    assert o.rel_l2(got, want) <= 1e-3
+    assert np.mean(bits(got) == bits(want)) >= 0.95
+
+
 def test_compact_two_layer_network(device):
     """torch_npu_lowbit_group_demo.py:197-204: a 64->32->7 ReLU MLP of compact layers."""
     announce('compact mlp')

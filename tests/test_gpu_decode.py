@@ -221,6 +221,34 @@ def test_decode_attention_matches_oracle(device, pos):
     assert torch.equal(dv[:, :, others].cpu(), values[:, :, others])
 
 
+@pytest.mark.parametrize('pos,cap,poison', [(100, 384, True), (383, 384, False), (700, 1024, True), (1023, 1024, False)])
+def test_decode_attention_masks_slots_past_the_position(device, pos, cap, poison):
+    """Slots past the position may hold anything (here NaN / Inf when `poison`): the kernel loads the
+    first 512 slots before it reads the position, and must select them away; capacities above 512
+    take further load rounds."""
+    announce('decode attention mask', pos, cap, poison)
+    keys, values, q, k, v, cos, sin = attention_case(pos, cap, pos + cap)
+    if poison:
+        keys[:, :, pos + 1:] = float('nan')
+        values[:, :, pos + 1::2] = float('inf')
+        values[:, :, pos + 2::2] = float('nan')
+    c, s = cos[pos:pos + 1][None, None], sin[pos:pos + 1][None, None]
+    qr = so.OracleLayer._rotate(q.view(1, 1, 9, 64).transpose(1, 2), c, s)
+    kr = so.OracleLayer._rotate(k.view(1, 1, 3, 64).transpose(1, 2), c, s)
+    ks = torch.cat((keys[:, :, :pos], kr), dim=2)
+    vs = torch.cat((values[:, :, :pos], v.view(1, 1, 3, 64).transpose(1, 2)), dim=2)
+    want = so.OracleLayer._attend(qr, ks, vs, torch.zeros(1, pos + 1)).reshape(576)
+    dk, dv = keys.to(device), values.to(device)
+    out = torch.full((576,), float('nan'), dtype=torch.float16, device=device)
+    position = torch.tensor([pos], dtype=torch.int64, device=device)
+    lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
+                         out, heads=9, kv_heads=3).run()
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert bool(torch.isfinite(got).all())
+    assert rel_l2(got, want) <= 1e-3
+
+
 def test_decode_attention_full_cache_is_a_no_op(device):
     cap = 16
     keys, values, q, k, v, cos, sin = attention_case(0, cap, 3)

@@ -106,6 +106,15 @@ def test_workspace_sizes():
     status, size, _ = workspace(args(M=256, rank=32, down=0x5000000, up=0x6000000, up_ld=32,
                                      x=0x1000000, y=0x2000000))
     assert status == 0 and size == 256 * 32 * 2 + 256 * 64 * 2
+    # a prefill GEMM of few 64 x 64 tiles splits K: fp32 partials [splits, M, N] (960 x 2560 at
+    # M = 512: 120 tiles, 40 k steps -> 4 slices)
+    status, size, _ = workspace(args(format=2, M=512, N=960, K=2560, group_size=64, ldx=2560, ldy=960,
+                                     x=0x1000000, y=0x2000000, scales=0x3000000, codes=0x4000000))
+    assert status == 0 and size == 4 * 512 * 960 * 4
+    # enough tiles: no split, no workspace
+    status, size, _ = workspace(args(format=2, M=512, N=2560, K=960, group_size=64, ldx=960, ldy=2560,
+                                     x=0x1000000, y=0x2000000, scales=0x3000000, codes=0x4000000))
+    assert status == 0 and size == 0
 
 
 def test_missing_workspace_is_rejected_by_lb_linear():

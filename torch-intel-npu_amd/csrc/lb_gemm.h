@@ -11,9 +11,11 @@
 //     into the other buffer.
 // The loop is unrolled by two so each register stage keeps its own registers (a loaded
 // register is never copied before its load completes).  The epilogue is the linear path's
-// (store_output): per-row scale, fp16, bias, correction.
+// (store_output): per-row scale, fp16, bias, correction; with split-K the fp32 sums of each
+// K slice go to p.partial and splitk_reduce_kernel applies it.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 #include "lb_kernels.h"
 
@@ -184,25 +186,27 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
   // Step s computes on buffer s % 2; the register stage holding step s + 1 (loaded two steps
   // earlier) is decoded into the other buffer, and step s + 3 is loaded into the stage just
   // emptied.  Loads are unconditional (steps past K read out of range): the waits stay exact.
-  // Loads of steps past the last one re-read the last step (in range, unused).
-  const int steps = p.K / BK;
-  const int klast = (steps - 1) * BK;
+  // Loads of steps past the last one re-read the last step (in range, unused).  With split-K
+  // (p.splits > 1, grid z = split) the workgroup covers k in [z * kslice, z * kslice + kslice).
+  const int kbeg = p.splits > 1 ? (int)blockIdx.z * p.kslice : 0;
+  const int steps = (min(p.K, kbeg + (p.splits > 1 ? p.kslice : p.K)) - kbeg) / BK;
+  const int klast = kbeg + (steps - 1) * BK;
   Stage r0, r1;
-  load(r0, 0);
-  load(r1, min(BK, klast));
+  load(r0, kbeg);
+  load(r1, min(kbeg + BK, klast));
   store(r0, 0);
-  load(r0, min(2 * BK, klast));
+  load(r0, min(kbeg + 2 * BK, klast));
   __syncthreads();
   int s = 0;
   for (; s + 2 <= steps; s += 2) {
     compute(0);                 // step s; r1 = step s + 1, r0 = step s + 2
     store(r1, 1);
-    load(r1, min((s + 3) * BK, klast));
+    load(r1, min(kbeg + (s + 3) * BK, klast));
     interleave();
     __syncthreads();
     compute(1);                 // step s + 1; r0 = step s + 2, r1 = step s + 3
     store(r0, 0);
-    load(r0, min((s + 4) * BK, klast));
+    load(r0, min(kbeg + (s + 4) * BK, klast));
     interleave();
     __syncthreads();
   }
@@ -218,38 +222,56 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = bm + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < p.M) store_output(p, m, n, acc[i][jj][r]);
+        if (m >= p.M) continue;
+        if (p.splits > 1) p.partial[((size_t)blockIdx.z * p.M + m) * p.N + n] = acc[i][jj][r];
+        else store_output(p, m, n, acc[i][jj][r]);
       }
     }
 }
 
-// 256 x 256 prefill GEMM (large problems).  WAVES = 4 or 8 waves in a 2 x (WAVES / 2) grid;
-// a wave owns a 128 x (512 / WAVES) block of v_mfma_f32_32x32x16_f16 tiles (4 x TN), whose fp32
-// accumulators live in AGPRs.  Per K step of 64 and 16-deep substep, a wave reads 4 A and TN B
-// fragments for its 4 TN MFMAs.  LDS holds two stages of A (fp16 activations) and B (decoded fp16
-// weights), 256 rows x 64 halves each, without padding: the 16-byte chunk c of row r is stored at
-// chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.  The next step's
-// activations and packed weights are loaded into registers one step ahead; they are decoded and
-// written to the other LDS stage between the MFMA groups of the current step, and one barrier per
-// step separates the stages.  Fragment reads of substep kk + 1 are issued before the MFMAs of
-// substep kk.
-template <int FMT, bool SCALED, int WAVES>
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices, so register
+// arrays indexed by them stay in registers).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// BM x BN prefill GEMM (BM, BN = 128 or 256) with WAVES = 4 or 8 waves in a 2 x (WAVES / 2)
+// grid; a wave owns a (BM / 2) x (BN / (WAVES / 2)) block of v_mfma_f32_32x32x16_f16 tiles
+// (TM x TN), whose fp32 accumulators live in AGPRs.  Per K step of 64 and 16-deep substep, a wave
+// reads TM A and TN B fragments for its TM TN MFMAs.  LDS holds two stages of A (fp16 activations)
+// and B (decoded fp16 weights), BM (BN) rows x 64 halves each, without padding: the 16-byte chunk c
+// of row r is stored at chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.
+// The next step's activations and packed weights are loaded into registers one step ahead; they
+// are decoded and written to the other LDS stage between the MFMA groups of the current step, and
+// one barrier per step separates the stages.  Fragment reads of substep kk + 1 are issued before
+// the MFMAs of substep kk.  With split-K (p.splits > 1, grid z = split) a workgroup covers
+// k in [z * kslice, z * kslice + kslice) and writes fp32 sums to p.partial.
+template <int FMT, bool SCALED, int WAVES, int BM = 256, int BN = 256>
 __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
-  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int BK = 64;
   constexpr int NT = 64 * WAVES;
   constexpr int WN = WAVES / 2;                     // waves along N
-  constexpr int TN = 8 / WN;                        // 32-column MFMA tiles per wave
-  constexpr int WCOLS = 32 * TN;                    // columns per wave
+  constexpr int WROWS = BM / 2;                     // rows per wave
+  constexpr int TM = WROWS / 32;                    // 32-row MFMA tiles per wave
+  constexpr int WCOLS = BN / WN;                    // columns per wave
+  constexpr int TN = WCOLS / 32;                    // 32-column MFMA tiles per wave
   constexpr int BITS = FormatTraits<FMT>::BITS;
   constexpr int CODES = 16 * 8 / BITS;              // codes per 16-byte B chunk
   constexpr int B_ROW_CHUNKS = BK / CODES;          // packed chunks per B row per step
   constexpr int B_PER = BN * B_ROW_CHUNKS / NT;     // packed B chunks per thread per step
   constexpr int A_PER = BM * (BK / 8) / NT;         // A chunks per thread per step
-  constexpr int STAGE = BM * BK;                    // halves per operand per stage
+  constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK;  // halves per operand per stage
   constexpr int kOutOfRange = (int)0x80000000u;
-  static_assert((WAVES == 4 || WAVES == 8) && B_PER >= 1, "tile constants");
-  __shared__ __align__(16) f16 As[2 * STAGE];
-  __shared__ __align__(16) f16 Bs[2 * STAGE];
+  static_assert((WAVES == 4 || WAVES == 8) && TM >= 1 && TN >= 1 && B_PER >= 1 && A_PER >= 1 &&
+                    BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0,
+                "tile constants");
+  __shared__ __align__(16) f16 As[2 * STAGE_A];
+  __shared__ __align__(16) f16 Bs[2 * STAGE_B];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -299,7 +321,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
     }
   };
   auto store_a = [&](int st) {
-    f16 *dst = As + st * STAGE;
+    f16 *dst = As + st * STAGE_A;
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
       asm volatile("" : "+v"(ra[i]));
@@ -307,7 +329,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
     }
   };
   auto store_b = [&](int st) {
-    f16 *dst = Bs + st * STAGE;
+    f16 *dst = Bs + st * STAGE_B;
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
       asm volatile("" : "+v"(rb[i]));
@@ -326,9 +348,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
     }
   };
 
-  f16x acc[4][TN];
+  f16x acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int jj = 0; jj < TN; ++jj)
 #pragma unroll
@@ -342,23 +364,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   int koff[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) koff[kk] = 8 * ((2 * kk + fh) ^ LB_G4_SWZ(fr));
-  const f16 *a_lane = As + (wm * 128 + fr) * BK;
+  const f16 *a_lane = As + (wm * WROWS + fr) * BK;
   const f16 *b_lane = Bs + (wn * WCOLS + fr) * BK;
 
-  const int steps = p.K / BK;
-  load(0);
+  const int kbeg = p.splits > 1 ? (int)blockIdx.z * p.kslice : 0;
+  const int steps = (min(p.K, kbeg + (p.splits > 1 ? p.kslice : p.K)) - kbeg) / BK;
+  load(kbeg);
   store_a(0);
   store_b(0);
-  if (steps > 1) load(BK);
+  if (steps > 1) load(kbeg + BK);
   __syncthreads();
   // One K step on LDS stage ST (compile-time, so every LDS offset is an immediate).
   auto step = [&](auto stage, int s) {
     constexpr int ST = decltype(stage)::value;
-    const f16 *a_base = a_lane + ST * STAGE;
-    const f16 *b_base = b_lane + ST * STAGE;
-    h8 fa[2][4], fb[2][TN];
+    const f16 *a_base = a_lane + ST * STAGE_A;
+    const f16 *b_base = b_lane + ST * STAGE_B;
+    h8 fa[2][TM], fb[2][TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[0][i] = *reinterpret_cast<const h8 *>(a_base + i * 32 * BK + koff[0]);
+    for (int i = 0; i < TM; ++i) fa[0][i] = *reinterpret_cast<const h8 *>(a_base + i * 32 * BK + koff[0]);
 #pragma unroll
     for (int jj = 0; jj < TN; ++jj) fb[0][jj] = *reinterpret_cast<const h8 *>(b_base + jj * 32 * BK + koff[0]);
 #pragma unroll
@@ -366,14 +389,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
       const int cur = kk & 1;
       if (kk < 3) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TM; ++i)
           fa[cur ^ 1][i] = *reinterpret_cast<const h8 *>(a_base + i * 32 * BK + koff[kk + 1]);
 #pragma unroll
         for (int jj = 0; jj < TN; ++jj)
           fb[cur ^ 1][jj] = *reinterpret_cast<const h8 *>(b_base + jj * 32 * BK + koff[kk + 1]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int jj = 0; jj < TN; ++jj)
           acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][jj], acc[i][jj], 0, 0, 0);
@@ -382,7 +405,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
         if (kk == 1) store_a(ST ^ 1);
         if (kk == 2) {
           store_b(ST ^ 1);
-          if (s + 2 < steps) load((s + 2) * BK);
+          if (s + 2 < steps) load(kbeg + (s + 2) * BK);
         }
       }
     }
@@ -394,32 +417,30 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   }
 
   // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-  // One call per tile keeps every accumulator index compile-time (the tiles stay in AGPRs).
-  auto emit = [&](const f16x &v, int i, int jj) {
-    const int n = bn + wn * WCOLS + jj * 32 + (lane & 31);
-    if (n >= p.N) return;
-    const float rs = p.per_row ? (float)p.scales[n] : 1.0f;
-    const float b = p.bias ? (float)p.bias[n] : 0.0f;
+  // Tile indices are compile-time (static_for), so the accumulators stay in AGPRs.
+  static_for<TM>([&](auto i) {
+    static_for<TN>([&](auto jj) {
+      const f16x &v = acc[decltype(i)::value][decltype(jj)::value];
+      const int n = bn + wn * WCOLS + decltype(jj)::value * 32 + (lane & 31);
+      if (n >= p.N) return;
+      const bool split = p.splits > 1;
+      const float rs = !split && p.per_row ? (float)p.scales[n] : 1.0f;
+      const float b = !split && p.bias ? (float)p.bias[n] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = bm + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (m >= p.M) continue;
-      f16 h = (f16)(v[r] * rs);
-      if (p.bias) h = (f16)((float)h + b);
-      if (p.delta) h = (f16)((float)h + (float)p.delta[(size_t)m * p.N + n]);
-      p.y[(size_t)m * p.ldy + n] = h;
-    }
-  };
-  emit(acc[0][0], 0, 0); emit(acc[0][1], 0, 1);
-  emit(acc[1][0], 1, 0); emit(acc[1][1], 1, 1);
-  emit(acc[2][0], 2, 0); emit(acc[2][1], 2, 1);
-  emit(acc[3][0], 3, 0); emit(acc[3][1], 3, 1);
-  if constexpr (TN == 4) {
-    emit(acc[0][2], 0, 2); emit(acc[0][3], 0, 3);
-    emit(acc[1][2], 1, 2); emit(acc[1][3], 1, 3);
-    emit(acc[2][2], 2, 2); emit(acc[2][3], 2, 3);
-    emit(acc[3][2], 3, 2); emit(acc[3][3], 3, 3);
-  }
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm * WROWS + decltype(i)::value * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m >= p.M) continue;
+        if (split) {
+          p.partial[((size_t)blockIdx.z * p.M + m) * p.N + n] = v[r];
+          continue;
+        }
+        f16 h = (f16)(v[r] * rs);
+        if (p.bias) h = (f16)((float)h + b);
+        if (p.delta) h = (f16)((float)h + (float)p.delta[(size_t)m * p.N + n]);
+        p.y[(size_t)m * p.ldy + n] = h;
+      }
+    });
+  });
 }
 
 }  // namespace lb

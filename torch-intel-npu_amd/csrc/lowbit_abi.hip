@@ -140,6 +140,93 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
   return gs;
 }
 
+#ifndef LB_GEMM_BM
+#define LB_GEMM_BM 128
+#endif
+#ifndef LB_GEMM_BN
+#define LB_GEMM_BN 128
+#endif
+#ifndef LB_GEMM_BK
+#define LB_GEMM_BK 64
+#endif
+#ifndef LB_GEMM_BIG_MIN
+#define LB_GEMM_BIG_MIN 256  // large tiles from this many workgroups
+#endif
+#ifndef LB_GEMM4_WAVES
+#define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
+#endif
+#ifndef LB_GEMM4_MIN_TILES
+#define LB_GEMM4_MIN_TILES 192  // 256 x 256 tiles from this many workgroups
+#endif
+#ifndef LB_GEMM_SPLIT_WGS
+#define LB_GEMM_SPLIT_WGS 256   // split K while the tile grid has fewer workgroups than this
+#endif
+#ifndef LB_GEMM_SPLIT_MAX
+#define LB_GEMM_SPLIT_MAX 4     // K slices at most
+#endif
+#ifndef LB_GEMM_SPLIT128_BELOW
+#define LB_GEMM_SPLIT128_BELOW 128  // 128 x 128 grids below this many tiles may split along K
+#endif
+#ifndef LB_GEMM_SPLIT_LONG_STEPS
+#define LB_GEMM_SPLIT_LONG_STEPS 16  // k steps per slice of a split 128 x 128 grid at least
+#endif
+#ifndef LB_GEMM_SPLIT_MIN_STEPS
+#define LB_GEMM_SPLIT_MIN_STEPS 8  // k steps per slice at least
+#endif
+
+enum { GEMM_256 = 0, GEMM_128 = 1, GEMM_64 = 2, GEMM_64_K32 = 3 };
+struct GemmShape {
+  int kind = GEMM_64;
+  int splits = 1;
+  int kslice = 0;
+};
+
+// Tile kernel and K split of a prefill GEMM:
+//   - 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs;
+//   - else 128 x 128 tiles (gemm2_kernel) when they alone give every CU a workgroup;
+//   - else, for a small 128 x 128 grid (< LB_GEMM_SPLIT128_BELOW tiles) over long rows, 128 x 128
+//     tiles split along K into slices of at least LB_GEMM_SPLIT_LONG_STEPS k steps, when the
+//     slices fill the CUs;
+//   - else 64 x 64 tiles (k steps of 64 where K allows, else 32), split along K when the grid has
+//     fewer than LB_GEMM_SPLIT_WGS workgroups, into slices of at least LB_GEMM_SPLIT_MIN_STEPS
+//     k steps, aiming at two workgroups per CU.
+// Every split is at most LB_GEMM_SPLIT_MAX slices; the fp32 partials [splits, M, N] go to the
+// workspace and splitk_reduce_kernel sums them in a fixed order and applies the epilogue.  The
+// launcher recomputes the kind with allow_split = (p.splits > 1), which gives the planned one.
+GemmShape gemm_shape(int64_t M, int64_t N, int64_t K, int64_t slices, bool allow_split) {
+  GemmShape gs;
+  const int64_t huge = ((M + 255) / 256) * ((N + 255) / 256) * slices;
+  const int64_t big = ((M + LB_GEMM_BM - 1) / LB_GEMM_BM) * ((N + LB_GEMM_BN - 1) / LB_GEMM_BN) * slices;
+  const int64_t small = ((M + 63) / 64) * ((N + 63) / 64) * slices;
+  const bool can_split = allow_split && slices == 1;
+  const int64_t s128 = std::min<int64_t>(LB_GEMM_SPLIT_MAX, K / LB_GEMM_BK / LB_GEMM_SPLIT_LONG_STEPS);
+  gs.kslice = (int)K;
+  int64_t s = 1;
+  int bk = K % 64 == 0 ? 64 : 32;
+  if (huge >= LB_GEMM4_MIN_TILES && K % 64 == 0) {
+    gs.kind = GEMM_256;
+  } else if (big >= LB_GEMM_BIG_MIN && K % LB_GEMM_BK == 0) {
+    gs.kind = GEMM_128;
+  } else if (can_split && K % LB_GEMM_BK == 0 && big < LB_GEMM_SPLIT128_BELOW && s128 > 1 &&
+             big * s128 >= LB_GEMM_BIG_MIN) {
+    gs.kind = GEMM_128;
+    bk = LB_GEMM_BK;
+    s = s128;
+  } else {
+    gs.kind = bk == 64 ? GEMM_64 : GEMM_64_K32;
+    if (can_split && small < LB_GEMM_SPLIT_WGS)
+      s = std::min<int64_t>(std::min<int64_t>(LB_GEMM_SPLIT_MAX, (2 * LB_GEMM_SPLIT_WGS + small - 1) / small),
+                            K / bk / LB_GEMM_SPLIT_MIN_STEPS);
+  }
+  if (s > 1) {
+    const int64_t steps = K / bk;
+    const int64_t ks = (steps + s - 1) / s * bk;
+    gs.splits = (int)((K + ks - 1) / ks);
+    gs.kslice = (int)ks;
+  }
+  return gs;
+}
+
 // One activation row: the single-tile kernel (all of a workgroup's loads in flight at once,
 // correction z computed inside each workgroup for K <= kFusedMaxK) needs no workspace.
 bool row_eligible(const lb_linear_args *a) {
@@ -230,6 +317,16 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
       pl.d_off = off;
       pl.d_bytes = (size_t)a->M * a->N * 2;
       off = round_up(off + pl.d_bytes, 256);
+    }
+  }
+  if (pl.path == PATH_GEMM) {
+    const GemmShape gs = gemm_shape(a->M, a->N, a->K, 1, true);
+    pl.splits = gs.splits;
+    pl.kslice = gs.kslice;
+    if (pl.splits > 1) {
+      pl.part_off = off;
+      pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
+      off = round_up(off + pl.part_bytes, 256);
     }
   }
   if (pl.path == PATH_GEMV) {
@@ -405,43 +502,24 @@ void launch_gemv(int fmt, bool scaled, const LinearParams &p, int kg, int kc, hi
   }
 }
 
-#ifndef LB_GEMM_BM
-#define LB_GEMM_BM 128
-#endif
-#ifndef LB_GEMM_BN
-#define LB_GEMM_BN 128
-#endif
-#ifndef LB_GEMM_BK
-#define LB_GEMM_BK 64
-#endif
-#ifndef LB_GEMM_BIG_MIN
-#define LB_GEMM_BIG_MIN 256  // large tiles from this many workgroups
-#endif
-#ifndef LB_GEMM4_WAVES
-#define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
-#endif
-#ifndef LB_GEMM4_MIN_TILES
-#define LB_GEMM4_MIN_TILES 192  // 256 x 256 tiles from this many workgroups
-#endif
-// 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs, else 128 x 128 tiles when they
-// alone give every CU a workgroup, else 64 x 64 tiles (k steps of 64 where K allows, else 32).
+// Launches the GEMM of p (p.splits > 1: grid z runs over the K slices, then the reduction).
 template <int FMT, bool SCALED>
 void launch_gemm_t(const LinearParams &p, hipStream_t s) {
   constexpr int BM = LB_GEMM_BM, BN = LB_GEMM_BN, BK = LB_GEMM_BK;
-  const int64_t huge = ((p.M + 255) / 256) * ((p.N + 255) / 256) * p.slices;
-  const int64_t big = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * p.slices;
-  if (huge >= LB_GEMM4_MIN_TILES && p.K % 64 == 0) {
-    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, p.slices),
+  const int kind = gemm_shape(p.M, p.N, p.K, p.slices, p.splits > 1).kind;
+  const unsigned gz = (unsigned)(p.splits > 1 ? p.splits : p.slices);
+  if (kind == GEMM_256) {
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, gz),
                        dim3(64 * LB_GEMM4_WAVES), 0, s, p);
-  } else if (big >= LB_GEMM_BIG_MIN && p.K % BK == 0) {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>),
-                       dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, p.slices), dim3(256), 0, s, p);
-  } else if (p.K % 64 == 0) {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64, p.slices),
+  } else if (kind == GEMM_128) {
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),
                        dim3(256), 0, s, p);
+  } else if (kind == GEMM_64) {
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
+                       0, s, p);
   } else {
-    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64, p.slices),
-                       dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
+                       0, s, p);
   }
 }
 
@@ -451,6 +529,10 @@ void launch_gemm(int fmt, bool scaled, const LinearParams &p, hipStream_t s) {
     case FMT_INT4: launch_gemm_t<FMT_INT4, true>(p, s); break;
     case FMT_NF4: launch_gemm_t<FMT_NF4, true>(p, s); break;
     default: launch_gemm_t<FMT_FP16, false>(p, s); break;
+  }
+  if (p.splits > 1) {
+    const size_t count = (size_t)p.M * p.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p);
   }
 }
 
@@ -681,6 +763,9 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     p.partial = reinterpret_cast<float *>(ws + plan.part_off);
     launch_gemv(fmt, scaled, p, plan.kg, plan.kc, s);
   } else if (plan.path == PATH_GEMM) {
+    p.splits = plan.splits;
+    p.kslice = plan.kslice;
+    p.partial = reinterpret_cast<float *>(ws + plan.part_off);
     launch_gemm(fmt, scaled, p, s);
   } else {
     launch_generic(fmt, p, s);

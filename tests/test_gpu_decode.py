@@ -52,6 +52,10 @@ CASES = [
     ('fp16', None, 576, 'rmsnorm', (49152,), 0, False, False),
     ('int8', None, 1536, 'silu_mul', (32768,), 0, True, True),
     ('int4', 64, 576, 'none', (16400,), 0, True, False),
+    # four tiles per workgroup: a partial last tile and idle waves after it, every epilogue
+    # operand, both prologues, the 1536-long staged row
+    ('int4', 64, 576, 'silu_mul', (49160,), 0, True, True),
+    ('int4', 128, 1536, 'rmsnorm', (32768,), 0, False, False),
 ]
 
 

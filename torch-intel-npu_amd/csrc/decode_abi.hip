@@ -304,6 +304,46 @@ lb_status launch_status(const char *what) {
 }  // namespace
 
 namespace lb {
+#ifndef LB_STREAM_ROWS_CH
+#define LB_STREAM_ROWS_CH 8  // 16-byte loads per lane per chunk of stream_rows_kernel
+#endif
+
+// stream_rows_kernel with the staged row length for K (smaller rows leave LDS for more
+// workgroups per CU; a workgroup that fills the CU's LDS alone has sixteen waves).
+template <int FMT, bool SCALED, int MP, int KMAX>
+void launch_stream_rows_k(const StreamParams &p0, hipStream_t s) {
+  constexpr int CH = LB_STREAM_ROWS_CH, PD = 2;
+  constexpr int KC = CH * 4 * FormatTraits<FMT>::CPL;
+  constexpr int KP = (KMAX + KC - 1) / KC * KC;
+  constexpr int LDS = (MP + 1) * KP * 2 + (FMT == FMT_NF4 ? 1024 : 0);
+  constexpr int PER_CU = 163840 / LDS < 1 ? 1 : (163840 / LDS > 4 ? 4 : 163840 / LDS);
+  constexpr int WAVES = PER_CU == 1 ? 16 : 8;
+  StreamParams p = p0;
+  p.chunks = (p.K + KC - 1) / KC;
+  const int grid = std::min((p.tiles + WAVES - 1) / WAVES, device_cus() * PER_CU);
+  hipLaunchKernelGGL((stream_rows_kernel<FMT, SCALED, MP, KMAX, CH, PD, WAVES>), dim3(grid), dim3(64 * WAVES), 0, s, p);
+}
+
+template <int FMT, bool SCALED, int MP>
+void launch_stream_rows_mp(const StreamParams &p, hipStream_t s) {
+  if (p.K <= 1024) launch_stream_rows_k<FMT, SCALED, MP, 1024>(p, s);
+  else if (p.K <= 2048) launch_stream_rows_k<FMT, SCALED, MP, 2048>(p, s);
+  else launch_stream_rows_k<FMT, SCALED, MP, 4096>(p, s);
+}
+
+template <int FMT, bool SCALED>
+void launch_stream_rows_f(const StreamParams &p, hipStream_t s) {
+  if (p.M <= 8) launch_stream_rows_mp<FMT, SCALED, 8>(p, s);
+  else launch_stream_rows_mp<FMT, SCALED, 16>(p, s);
+}
+
+void launch_stream_rows(const StreamParams &p, int format, bool scaled, hipStream_t s) {
+  if (format == FMT_INT4) launch_stream_rows_f<FMT_INT4, true>(p, s);
+  else if (format == FMT_NF4) launch_stream_rows_f<FMT_NF4, true>(p, s);
+  else if (scaled) launch_stream_rows_f<FMT_INT8, true>(p, s);
+  else launch_stream_rows_f<FMT_INT8, false>(p, s);
+}
+
 void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t s) {
   if (format == FMT_INT4) launch_stream_f<FMT_INT4, true>(p, ns, s);
   else if (scaled) launch_stream_f<FMT_INT8, true>(p, ns, s);

@@ -364,6 +364,169 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemv_kernel(StreamParams p)
   }
 }
 
+// Streaming GEMV for 2 .. MP activation rows (MP = 8 or 16) with the reference's weights: each
+// code is decoded to fp16(q * s) in registers (decode8, as in the single-tile kernels), so the
+// MFMA accumulates the whole row of a tile and nothing is flushed before the tile's end:
+// y[m, n] = fp16(sum_k x[m, k] * fp16(q[n, k] * s)) (+ bias), the products the other GEMV paths
+// form.  A rows 0 .. M-1 are the activation rows (staged in the decode8 slot order); rows M .. 15
+// read a zero row.  A wave streams 16-row tiles chunk by chunk (CH 16-byte loads per lane per
+// chunk, PD chunks in flight), persistent over the grid like stream_gemv_kernel; a lane's 16-byte
+// load holds CPL codes of one group (groups are >= 32 codes, powers of two, or one per row).
+template <int FMT, bool SCALED, int MP, int KMAX, int CH, int PD, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void stream_rows_kernel(StreamParams p) {
+  constexpr int CPL = FormatTraits<FMT>::CPL, BITS = FormatTraits<FMT>::BITS, T8 = CPL / 8;
+  constexpr int CPW = 4 * CPL;                       // codes per load position (four lane groups)
+  constexpr int KC = CH * CPW;                       // codes per chunk
+  constexpr int KP = (KMAX + KC - 1) / KC * KC;      // staged row length (zero past K)
+  constexpr int NB = KP / 8;                         // 8-code blocks of a staged row
+  constexpr int NT = 64 * WAVES;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert(MP == 8 || MP == 16, "MP is 8 or 16");
+  __shared__ __align__(16) f16 xs[(MP + 1) * KP];    // activation rows 0 .. MP-1, then a zero row
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int K = p.K, C = p.chunks;
+  const int row_bytes = K * BITS / 8;
+
+  // fp16 operands are kept as 32-bit words (raw bits): arrays of 16-bit values would be packed
+  // through scratch memory.
+  struct Buf {
+    u4 w[CH];
+    uint32_t s[SCALED ? CH : 1];
+    uint32_t e[2];  // bias and per-row scale of row n0 + j
+  };
+  // Loads of one chunk: the scales and epilogue operands first, then the CH weight loads.
+  auto issue = [&](Buf &b, int tile, int chunk) {
+    const int n0 = tile * 16;
+    const int rows = tile < p.tiles ? min(16, p.N - n0) : 0;
+    if constexpr (SCALED) {
+      const __amdgpu_buffer_rsrc_t sb =
+          buffer_rsrc(p.scales + (size_t)(rows > 0 ? n0 : 0) * p.G, (size_t)rows * p.G * 2);
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int k = (chunk * CH + u) * CPW + g * CPL;
+        const int off = k < K ? (j * p.G + (k >> p.group_shift)) * 2 : kOutOfRange;
+        b.s[u] = __builtin_amdgcn_raw_buffer_load_b16(sb, off, 0, 0);
+      }
+    }
+    const int eoff = j < rows ? (n0 + j) * 2 : kOutOfRange;
+    const size_t nb = (size_t)p.N * 2;
+    b.e[0] = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? nb : 0), eoff, 0, 0);
+    b.e[1] = SCALED ? 0u : __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.scales, nb), eoff, 0, 0);
+    const __amdgpu_buffer_rsrc_t wb =
+        buffer_rsrc(p.codes + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)rows * row_bytes);
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int k = (chunk * CH + u) * CPW + g * CPL;
+      const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
+      b.w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, off, 0, 0));
+    }
+  };
+
+  // Work list of this wave: (tile, chunk) items, tiles gw, gw + W, ...
+  const int gw = blockIdx.x * WAVES + wave, W = gridDim.x * WAVES;
+  int it_tile = gw, it_chunk = 0, c_tile = gw, c_chunk = 0;
+  const int items = gw < p.tiles ? ((p.tiles - 1 - gw) / W + 1) * C : 0;
+  auto advance = [&](int &tile, int &chunk) {
+    if (++chunk == C) { chunk = 0; tile += W; }
+  };
+
+  Buf buf[PD];
+#pragma unroll
+  for (int s = 0; s < PD - 1; ++s) {
+    issue(buf[s], it_tile, it_chunk);
+    advance(it_tile, it_chunk);
+  }
+
+  // ---- stage the activation rows in the decode8 slot order, and the zero row.  Loads go out XU
+  // per thread at a time, so a batch costs one memory round trip. ----
+  {
+    constexpr int TOTAL = (MP + 1) * NB;
+    constexpr int ITER = (TOTAL + NT - 1) / NT;
+    constexpr int XU = ITER < 8 ? ITER : 8;
+    for (int base = 0; base < ITER; base += XU) {
+      h8 xv[XU];
+#pragma unroll
+      for (int i = 0; i < XU; ++i) {
+        const int idx = (base + i) * NT + t;
+        const int m = idx / NB, b = idx - m * NB;
+        const bool live = base + i < ITER && idx < TOTAL && m < p.M && 8 * b < K;
+        xv[i] = __builtin_bit_cast(
+            h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x + (size_t)(live ? m : 0) * p.ldx, (size_t)K * 2),
+                                                      live ? b * 16 : kOutOfRange, 0, 0));
+      }
+#pragma unroll
+      for (int i = 0; i < XU; ++i) {
+        const int idx = (base + i) * NT + t;
+        const int m = idx / NB, b = idx - m * NB;
+        if (base + i < ITER && idx < TOTAL && (m < p.M || m == MP))
+          *reinterpret_cast<h8 *>(xs + m * KP + 8 * b) = permute_block<FMT>(xv[i]);
+      }
+    }
+  }
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  __syncthreads();
+
+  const f16 *abase = xs + (j < p.M ? j : MP) * KP + g * CPL;
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](Buf &b, int chunk) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int kb = (chunk * CH + u) * CPW;
+      if (kb >= K) break;  // wave-uniform
+      asm volatile("" : "+v"(b.w[u]));  // decode here, not at the load
+      h2 s2 = {(f16)1.0f, (f16)1.0f};
+      if constexpr (SCALED) {
+        const f16 sv = __builtin_bit_cast(f16, (unsigned short)b.s[u]);
+        s2 = h2{sv, sv};
+      }
+#pragma unroll
+      for (int q = 0; q < T8; ++q) {
+        const h8 a = *reinterpret_cast<const h8 *>(abase + kb + 8 * q);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, decode8<FMT, !SCALED>(b.w[u], q, s2, nf4_table), acc, 0, 0, 0);
+      }
+    }
+  };
+  // Lane (j, g) holds rows 4g .. 4g+3 (activation rows) of column j (weight row n0 + j).
+  auto finish = [&](uint32_t ebits, uint32_t rbits, int n0) {
+    const f16 ebias = __builtin_bit_cast(f16, (unsigned short)ebits);
+    const f16 erow = __builtin_bit_cast(f16, (unsigned short)rbits);
+    if (n0 + j < p.N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * g + r;
+        if (m >= p.M) continue;
+        float v = acc[r];
+        if constexpr (!SCALED) v *= (float)erow;
+        f16 h = (f16)v;
+        if (p.bias) h = (f16)((float)h + (float)ebias);
+        p.y[(size_t)m * p.ldy + n0 + j] = h;
+      }
+    }
+    acc = f4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  for (int done = 0; done < items; done += PD) {
+#pragma unroll
+    for (int s = 0; s < PD; ++s) {
+      issue(buf[(s + PD - 1) % PD], it_tile, it_chunk);
+      advance(it_tile, it_chunk);
+      if (done + s < items) {
+        consume(buf[s], c_chunk);
+        if (c_chunk == C - 1) finish(buf[s].e[0], buf[s].e[1], c_tile * 16);
+        advance(c_tile, c_chunk);
+      }
+    }
+  }
+}
+
+// Launches stream_rows_kernel for 2 <= p.M <= 16 rows (K <= 4096, groups of at least 32 codes
+// that are powers of two, or one per row).
+void launch_stream_rows(const StreamParams &p, int format, bool scaled, hipStream_t stream);
+
 // Launches stream_gemv_kernel for p.M <= 16 rows (defined with the decode launchers); `ns` is
 // stream_group_span of the shape, and stream_rows_ok must hold for p.M > 1.
 void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t stream);

@@ -243,6 +243,9 @@ bool row_eligible(const lb_linear_args *a) {
   return true;
 }
 
+#ifndef LB_STREAM_ROWS_DECODE_MIN_M
+#define LB_STREAM_ROWS_DECODE_MIN_M 5  // stream path from this many rows: stream_rows_kernel, below: stream_gemv_kernel
+#endif
 #ifndef LB_STREAM_ROWS_MIN_BYTES
 #define LB_STREAM_ROWS_MIN_BYTES (64ll << 20)  // weights from which 2..16-row calls take stream_gemv_kernel
 #endif
@@ -735,7 +738,8 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     sp.ldx = p.ldx;
     sp.ldy = p.ldy;
     sp.tiles = (int)((a->N + 15) / 16);
-    launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
+    if (a->M >= LB_STREAM_ROWS_DECODE_MIN_M) launch_stream_rows(sp, fmt, !p.per_row, s);
+    else launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
     return launch_status("lb_linear");
   }
   uint8_t *ws = static_cast<uint8_t *>(a->workspace);

@@ -63,14 +63,15 @@ typedef enum lb_format {
 #define LB_FLAG_FORCE_GEMV    0x1u /* decode-regime kernel regardless of M (M <= 32) */
 #define LB_FLAG_FORCE_GEMM    0x2u /* prefill-regime MFMA GEMM regardless of M */
 #define LB_FLAG_FORCE_GENERIC 0x4u /* shape-agnostic fallback kernel (any N, K, group) */
-/* Streaming GEMV (the kernel one-row calls over long rows or >= 64 MB of INT4 weights, and 2..16-row
- * calls over >= 64 MB, take by themselves) regardless of size: INT4/INT8 codes, no correction or
- * variant, 16-byte aligned codes and x rows, K a multiple of 32 (INT4) or 16 (INT8), groups of one
- * per row or a power of two, each 128-code (INT4) / 64-code (INT8) piece of a row spanning 1, 2 or 4
- * whole groups; M == 1 with K <= 16384, or 2 <= M <= 16 with K <= 4096 and, as M grows, longer
- * groups (INT4: >= 64 codes up to 8 rows, >= 128 beyond; INT8: >= 64 codes).  Its sums use the
- * exact q * s weights (the reference's rounding-budget gate bounds the difference to fp16(q * s)).
- * LB_UNSUPPORTED otherwise.  No counterpart in the reference: the path choice is internal there. */
+/* Streaming GEMVs (the kernels one-row calls over long rows or >= 64 MB of INT4 weights, and
+ * 2..32-row calls over >= 64 MB, take by themselves) regardless of size: INT4/INT8 codes, no
+ * correction or variant, 16-byte aligned codes and x rows, K a multiple of 32 (INT4) or 16 (INT8),
+ * groups of one per row or a power of two, each 128-code (INT4) / 64-code (INT8) piece of a row
+ * spanning 1, 2 or 4 whole groups; M == 1 or 17 <= M <= 32 with K <= 16384, or 2 <= M <= 16 with
+ * K <= 4096 and, as M grows, longer groups (INT4: >= 64 codes up to 8 rows, >= 128 beyond; INT8:
+ * >= 64 codes).  Up to 4 rows the sums use the exact q * s weights (the reference's rounding-budget
+ * gate bounds the difference to fp16(q * s)); from 5 rows, fp16(q * s).  LB_UNSUPPORTED otherwise.
+ * No counterpart in the reference: the path choice is internal there. */
 #define LB_FLAG_FORCE_STREAM  0x20u
 /* One fp16 product per group of K, summed by a balanced fp16 add tree (neighbours pair up,
  * an odd last piece moves up unpaired), then + bias: the compact_groups graph of the

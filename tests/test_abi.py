@@ -258,7 +258,7 @@ S = lowbit_hip.FLAG_FORCE_STREAM
 @pytest.mark.parametrize('over,status,needle', [
     (dict(flags=S | lowbit_hip.FLAG_FORCE_GEMV), lowbit_hip.INVALID_ARGUMENT, 'at most one'),
     (dict(flags=S, M=2), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),        # two rows need groups >= 64
-    (dict(flags=S, M=17, group_size=128, ldy=64), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
+    (dict(flags=S, M=33, group_size=128, ldy=64), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),  # at most 32 rows
     (dict(flags=S, M=9, group_size=64), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),  # 9..16 rows: >= 128
     (dict(flags=S, M=2, K=8192, ldx=8192, group_size=128, N=1, ldy=1), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),
     (dict(flags=S, format=2), lowbit_hip.UNSUPPORTED, 'FORCE_STREAM'),   # nf4
@@ -278,7 +278,8 @@ def test_force_stream_argument_errors(over, status, needle):
 
 @pytest.mark.parametrize('over', [dict(), dict(group_size=64), dict(group_size=128), dict(K=4096, ldx=4096, group_size=4096),
                                   dict(format=0, group_size=16), dict(format=0, K=576, ldx=576, group_size=576),
-                                  dict(M=8, group_size=64), dict(M=16, group_size=128), dict(M=3, format=0, group_size=64)])
+                                  dict(M=8, group_size=64), dict(M=16, group_size=128), dict(M=3, format=0, group_size=64),
+                                  dict(M=17, group_size=128), dict(M=32, group_size=32), dict(M=24, format=0, group_size=16)])
 def test_force_stream_accepts_and_needs_no_workspace(over):
     status, size, message = workspace(args(flags=S, **over))
     assert (status, size) == (0, 0), message

@@ -166,6 +166,10 @@ ROWS_CASES = [
     ('int4', 4, 16400, 576, 64),
     ('int8', 2, 1040, 4096, 4096), ('int8', 7, 1040, 2048, 2048), ('int8', 16, 1040, 4096, 4096),
     ('int8', 3, 1040, 4096, 64), ('int8', 12, 16400, 1024, 128),
+    # 17 .. 32 rows (K-outer chunks): ragged N, groups of 32, K past 4096, per-row and grouped int8
+    ('int4', 17, 1040, 4096, 128), ('int4', 25, 1000, 4096, 128), ('int4', 24, 2064, 1024, 32),
+    ('int4', 32, 16400, 2048, 64), ('int4', 32, 1040, 8192, 128), ('int4', 29, 1040, 576, 64),
+    ('int8', 20, 1040, 4096, 4096), ('int8', 32, 1040, 2048, 64),
 ]
 
 
@@ -214,7 +218,8 @@ def test_stream_rows_identity_is_bit_exact(device):
         np.testing.assert_array_equal(y[r].view(np.uint16), w[:, c].view(np.uint16), err_msg=f'row {r}')
 
 
-@pytest.mark.parametrize('spec', [('int4', 8, 32768, 4096, 128), ('int8', 3, 16384, 4096, 4096)],
+@pytest.mark.parametrize('spec', [('int4', 8, 32768, 4096, 128), ('int8', 3, 16384, 4096, 4096),
+                                  ('int4', 32, 32768, 4096, 128), ('int8', 20, 32768, 4096, 4096)],
                          ids=lambda s: '-'.join(map(str, s)))
 def test_stream_rows_unforced(device, spec):
     """Several rows over >= 64 MB of weights take the stream kernel without a flag; random codes,

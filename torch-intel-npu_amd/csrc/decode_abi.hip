@@ -344,6 +344,31 @@ void launch_stream_rows(const StreamParams &p, int format, bool scaled, hipStrea
   else launch_stream_rows_f<FMT_INT8, false>(p, s);
 }
 
+#ifndef LB_STREAM_WIDE_TPW
+#define LB_STREAM_WIDE_TPW 1  // 16-row tiles per wave of stream_wide_kernel
+#endif
+#ifndef LB_STREAM_WIDE_WAVES
+#define LB_STREAM_WIDE_WAVES 8  // waves per workgroup of stream_wide_kernel
+#endif
+
+// stream_wide_kernel: chunks of four 16-byte loads per lane per tile.
+template <int FMT, bool SCALED>
+void launch_stream_wide_f(const StreamParams &p0, hipStream_t s) {
+  constexpr int KC = 4 * 4 * FormatTraits<FMT>::CPL;
+  constexpr int TPW = LB_STREAM_WIDE_TPW, WAVES = LB_STREAM_WIDE_WAVES;
+  StreamParams p = p0;
+  p.chunks = (p.K + KC - 1) / KC;
+  const int grid = (p.tiles + WAVES * TPW - 1) / (WAVES * TPW);
+  hipLaunchKernelGGL((stream_wide_kernel<FMT, SCALED, KC, TPW, WAVES>), dim3(grid), dim3(64 * WAVES), 0, s, p);
+}
+
+void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t s) {
+  if (format == FMT_INT4) launch_stream_wide_f<FMT_INT4, true>(p, s);
+  else if (format == FMT_NF4) launch_stream_wide_f<FMT_NF4, true>(p, s);
+  else if (scaled) launch_stream_wide_f<FMT_INT8, true>(p, s);
+  else launch_stream_wide_f<FMT_INT8, false>(p, s);
+}
+
 void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t s) {
   if (format == FMT_INT4) launch_stream_f<FMT_INT4, true>(p, ns, s);
   else if (scaled) launch_stream_f<FMT_INT8, true>(p, ns, s);

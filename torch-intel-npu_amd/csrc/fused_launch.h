@@ -53,13 +53,16 @@ inline int stream_group_span(int format, long long K, long long group) {
   return (int)(cpw / group);
 }
 
-// Whether stream_gemv_kernel takes M activation rows (2 <= M <= 16) of such a shape: the rows
-// are staged whole (K <= 4096), and with more rows each MFMA A row spans more code blocks, so the
-// groups must be longer (INT4: <= 2 groups per 128-code load up to 8 rows, 1 for 16; INT8: one
-// scale per 64-code load or one per row).
+// Whether the streaming GEMVs take M activation rows (2 <= M <= 32) of such a shape: up to 16 rows
+// are staged whole (K <= 4096), and with more rows each MFMA A row of stream_gemv_kernel spans
+// more code blocks, so the groups must be longer (INT4: <= 2 groups per 128-code load up to 8
+// rows, 1 for 16; INT8: one scale per 64-code load or one per row); 17 .. 32 rows run in
+// stream_wide_kernel, which stages K in chunks.
 inline bool stream_rows_ok(int format, long long M, long long K, long long group) {
   const int span = stream_group_span(format, K, group);
-  if (span == 0 || M < 2 || M > 16 || K > 4096) return false;
+  if (span == 0 || M < 2 || M > 32) return false;
+  if (M > 16) return true;  // stream_wide_kernel: K-outer chunks, the scale looked up per 16-byte load
+  if (K > 4096) return false;
   if (format == FMT_INT4) return M <= 8 ? span <= 2 : span == 1;
   return span == 1;
 }

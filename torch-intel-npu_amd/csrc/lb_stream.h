@@ -523,6 +523,169 @@ __global__ __launch_bounds__(64 * WAVES) void stream_rows_kernel(StreamParams p)
   }
 }
 
+// Streaming GEMV for 17 .. 32 activation rows (two 16-row halves of the MFMA A operand) with the
+// reference's weights fp16(q * s) decoded in registers; each decoded B fragment feeds both halves.
+// 32 staged rows of a long K do not fit in LDS, so the loop is K-outer: a workgroup owns WAVES *
+// TPW consecutive 16-row tiles (TPW per wave, accumulators in registers) and walks K in chunks of
+// KC codes; per chunk every row's KC activations are staged in one of two LDS stages (the next
+// chunk's weights and activations are loaded during the current chunk), one barrier per chunk.
+// A rows past M read a zero row.
+template <int FMT, bool SCALED, int KC, int TPW, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void stream_wide_kernel(StreamParams p) {
+  constexpr int CPL = FormatTraits<FMT>::CPL, BITS = FormatTraits<FMT>::BITS, T8 = CPL / 8;
+  constexpr int CPW = 4 * CPL;                       // codes per load position (four lane groups)
+  constexpr int CH = KC / CPW;                       // loads per lane per tile per chunk
+  constexpr int NT = 64 * WAVES;
+  constexpr int XCH = 32 * KC / 8;                   // 16-byte activation pieces per stage
+  constexpr int XP = (XCH + NT - 1) / NT;            // per thread
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert(KC % CPW == 0 && CH >= 1, "chunk of whole loads");
+  __shared__ __align__(16) f16 xs[2 * 32 * KC + KC];  // two stages of 32 rows, then a zero row
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int K = p.K, C = p.chunks;
+  const int row_bytes = K * BITS / 8;
+  const int tile0 = (blockIdx.x * WAVES + wave) * TPW;  // this wave's first tile
+
+  // fp16 operands are kept as 32-bit words (raw bits): arrays of 16-bit values would be packed
+  // through scratch memory.
+  struct Buf {
+    u4 w[TPW][CH];
+    uint32_t s[TPW][SCALED ? CH : 1];
+  };
+  auto issue = [&](Buf &b, int chunk) {
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      const int n0 = (tile0 + tt) * 16;
+      const int rows = tile0 + tt < p.tiles ? min(16, p.N - n0) : 0;
+      if constexpr (SCALED) {
+        const __amdgpu_buffer_rsrc_t sb =
+            buffer_rsrc(p.scales + (size_t)(rows > 0 ? n0 : 0) * p.G, (size_t)rows * p.G * 2);
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+          const int k = chunk * KC + u * CPW + g * CPL;
+          b.s[tt][u] = __builtin_amdgcn_raw_buffer_load_b16(sb, k < K ? (j * p.G + (k >> p.group_shift)) * 2 : kOutOfRange, 0, 0);
+        }
+      }
+      const __amdgpu_buffer_rsrc_t wb =
+          buffer_rsrc(p.codes + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)rows * row_bytes);
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int k = chunk * KC + u * CPW + g * CPL;
+        b.w[tt][u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange, 0, 0));
+      }
+    }
+  };
+  // Activation pieces of a chunk: piece i = (row m, 8-code block b); rows past M and codes past K
+  // read zeros.
+  auto load_x = [&](h8 (&xv)[XP], int chunk) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int idx = i * NT + t;
+      const int m = idx / (KC / 8), b = idx % (KC / 8);
+      const int k = chunk * KC + 8 * b;
+      const bool live = idx < XCH && m < p.M && k < K;
+      xv[i] = __builtin_bit_cast(
+          h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x + (size_t)(live ? m : 0) * p.ldx, (size_t)K * 2),
+                                                    live ? k * 2 : kOutOfRange, 0, 0));
+    }
+  };
+  auto store_x = [&](const h8 (&xv)[XP], int st) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int idx = i * NT + t;
+      if (idx < XCH) *reinterpret_cast<h8 *>(xs + st * 32 * KC + idx * 8) = permute_block<FMT>(xv[i]);
+    }
+  };
+
+  Buf buf[2];
+  h8 xv[XP];
+  issue(buf[0], 0);
+  load_x(xv, 0);
+  for (int i = t; i < KC / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * KC + i * 8) = h8{};
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  store_x(xv, 0);
+  __syncthreads();
+
+  f4 acc[TPW][2];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) acc[tt][0] = acc[tt][1] = f4{0.f, 0.f, 0.f, 0.f};
+  // A operand of lane (j, g) for the two row halves: rows j and 16 + j (or the zero row).
+  const int a_lo = (j < p.M ? j * KC : 2 * 32 * KC) + g * CPL;
+  const int a_hi = (16 + j < p.M ? (16 + j) * KC : 2 * 32 * KC) + g * CPL;
+
+  auto step = [&](auto stage) {
+    constexpr int ST = decltype(stage)::value;
+    Buf &b = buf[ST];
+    const int sx = ST * 32 * KC;  // this stage's activation offset (rows past M use the zero row)
+    const f16 *alo = xs + a_lo + (j < p.M ? sx : 0);
+    const f16 *ahi = xs + a_hi + (16 + j < p.M ? sx : 0);
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        asm volatile("" : "+v"(b.w[tt][u]));  // decode here, not at the load
+        h2 s2 = {(f16)1.0f, (f16)1.0f};
+        if constexpr (SCALED) {
+          const f16 sv = __builtin_bit_cast(f16, (unsigned short)b.s[tt][u]);
+          s2 = h2{sv, sv};
+        }
+#pragma unroll
+        for (int q = 0; q < T8; ++q) {
+          const h8 bw = decode8<FMT, !SCALED>(b.w[tt][u], q, s2, nf4_table);
+          const h8 x0 = *reinterpret_cast<const h8 *>(alo + u * CPW + 8 * q);
+          const h8 x1 = *reinterpret_cast<const h8 *>(ahi + u * CPW + 8 * q);
+          acc[tt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, bw, acc[tt][0], 0, 0, 0);
+          acc[tt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, bw, acc[tt][1], 0, 0, 0);
+        }
+      }
+    }
+  };
+  // Chunk c uses stage c % 2; chunk c + 1 is loaded meanwhile and stored into the other stage.
+  for (int c = 0; c < C; c += 2) {
+    if (c + 1 < C) {
+      issue(buf[1], c + 1);
+      load_x(xv, c + 1);
+    }
+    step(std::integral_constant<int, 0>{});
+    if (c + 1 < C) store_x(xv, 1);
+    __syncthreads();
+    if (c + 1 >= C) break;
+    if (c + 2 < C) {
+      issue(buf[0], c + 2);
+      load_x(xv, c + 2);
+    }
+    step(std::integral_constant<int, 1>{});
+    if (c + 2 < C) store_x(xv, 0);
+    __syncthreads();
+  }
+
+  // Lane (j, g) holds rows h * 16 + 4g .. + 3 of column j (weight row n0 + j) in acc[tt][h].
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int n0 = (tile0 + tt) * 16;
+    if (tile0 + tt >= p.tiles || n0 + j >= p.N) continue;
+    const float rs = SCALED ? 1.0f : (float)p.scales[n0 + j];
+    const float bias = p.bias ? (float)p.bias[n0 + j] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * h + 4 * g + r;
+        if (m >= p.M) continue;
+        f16 y = (f16)(acc[tt][h][r] * rs);
+        if (p.bias) y = (f16)((float)y + bias);
+        p.y[(size_t)m * p.ldy + n0 + j] = y;
+      }
+  }
+}
+
+// Launches stream_wide_kernel for 17 <= p.M <= 32 rows.
+void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t stream);
+
 // Launches stream_rows_kernel for 2 <= p.M <= 16 rows (K <= 4096, groups of at least 32 codes
 // that are powers of two, or one per row).
 void launch_stream_rows(const StreamParams &p, int format, bool scaled, hipStream_t stream);

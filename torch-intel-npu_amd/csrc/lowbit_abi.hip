@@ -250,9 +250,14 @@ bool row_eligible(const lb_linear_args *a) {
 #define LB_STREAM_ROWS_MIN_BYTES (64ll << 20)  // weights from which 2..16-row calls take stream_gemv_kernel
 #endif
 
-// Several activation rows, no correction, a long enough weight the stream kernel takes.
+#ifndef LB_STREAM_WIDE_MIN_N
+#define LB_STREAM_WIDE_MIN_N 32768  // 17..32 rows: stream_wide_kernel needs this many rows to fill the CUs
+#endif
+
+// Several activation rows, no correction, a long enough weight the stream kernels take.
 bool stream_rows_eligible(const lb_linear_args *a) {
   if (a->rank > 0 || !stream_rows_ok((int)a->format, a->M, a->K, a->group_size)) return false;
+  if (a->M > 16 && a->N < LB_STREAM_WIDE_MIN_N) return false;
   const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
   return bytes >= LB_STREAM_ROWS_MIN_BYTES;
 }
@@ -410,8 +415,8 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
         !aligned(a->x, 16) || a->ldx % 8 != 0)
       return fail(LB_UNSUPPORTED,
                   "lb_linear: LB_FLAG_FORCE_STREAM needs int4/int8 codes, no correction or variant, 16-byte aligned "
-                  "codes/x rows, and M == 1 with K <= 16384 (a multiple of 32 / 16) and groups spanning whole "
-                  "128 / 64-code pieces, or 2 <= M <= 16 with K <= 4096 and longer groups as M grows");
+                  "codes/x rows, and M == 1 or 17 <= M <= 32 with K <= 16384 (a multiple of 32 / 16) and groups "
+                  "spanning whole 128 / 64-code pieces, or 2 <= M <= 16 with K <= 4096 and longer groups as M grows");
   }
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {
@@ -738,7 +743,8 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     sp.ldx = p.ldx;
     sp.ldy = p.ldy;
     sp.tiles = (int)((a->N + 15) / 16);
-    if (a->M >= LB_STREAM_ROWS_DECODE_MIN_M) launch_stream_rows(sp, fmt, !p.per_row, s);
+    if (a->M > 16) launch_stream_wide(sp, fmt, !p.per_row, s);
+    else if (a->M >= LB_STREAM_ROWS_DECODE_MIN_M) launch_stream_rows(sp, fmt, !p.per_row, s);
     else launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
     return launch_status("lb_linear");
   }

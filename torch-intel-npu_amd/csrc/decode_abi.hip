@@ -369,6 +369,29 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
   else launch_stream_wide_f<FMT_INT8, false>(p, s);
 }
 
+// tile_rows_kernel: one workgroup per 16-row tile, the staged row length for K.
+template <int FMT, bool SCALED, int MP>
+void launch_tile_rows_mp(const StreamParams &p, hipStream_t s) {
+  const dim3 grid((p.N + 15) / 16);
+  if (p.K <= 640) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP>), grid, dim3(256), 0, s, p);
+  else if (MP == 16 || p.K <= 2048) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP>), grid, dim3(256), 0, s, p);
+  else if constexpr (MP < 16) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP>), grid, dim3(256), 0, s, p);
+}
+
+template <int FMT, bool SCALED>
+void launch_tile_rows_f(const StreamParams &p, hipStream_t s) {
+  if (p.M <= 4) launch_tile_rows_mp<FMT, SCALED, 4>(p, s);
+  else if (p.M <= 8) launch_tile_rows_mp<FMT, SCALED, 8>(p, s);
+  else launch_tile_rows_mp<FMT, SCALED, 16>(p, s);
+}
+
+void launch_tile_rows(const StreamParams &p, int format, bool scaled, hipStream_t s) {
+  if (format == FMT_INT4) launch_tile_rows_f<FMT_INT4, true>(p, s);
+  else if (format == FMT_NF4) launch_tile_rows_f<FMT_NF4, true>(p, s);
+  else if (scaled) launch_tile_rows_f<FMT_INT8, true>(p, s);
+  else launch_tile_rows_f<FMT_INT8, false>(p, s);
+}
+
 void launch_stream(const StreamParams &p, int format, bool scaled, int ns, hipStream_t s) {
   if (format == FMT_INT4) launch_stream_f<FMT_INT4, true>(p, ns, s);
   else if (scaled) launch_stream_f<FMT_INT8, true>(p, ns, s);

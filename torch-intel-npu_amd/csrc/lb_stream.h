@@ -686,6 +686,145 @@ __global__ __launch_bounds__(64 * WAVES) void stream_wide_kernel(StreamParams p)
 // Launches stream_wide_kernel for 17 <= p.M <= 32 rows.
 void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t stream);
 
+// One 16-row tile per workgroup for 2 .. MP activation rows (MP = 4, 8 or 16), the multi-row
+// form of the single-tile one-row kernels: the four waves split K (wave w takes k steps w, w + 4,
+// ...), every weight load of a lane is issued straight-line before the first wait (up to 32 x 16
+// bytes), the M activation rows are staged once in LDS in the decode8 slot order (zero from K on,
+// and a zero row that A rows past M read), the scales of the tile's 16 rows too.  The reference's
+// weights fp16(q * s) (decode8); the waves' partial sums are added in a fixed order through LDS.
+// y[m, n] = fp16(sum) (* per-row scale before rounding for per-row int8) (+ bias, fp16).
+template <int FMT, bool SCALED, int KMAX, int MP>
+__global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
+  constexpr int CPL = FormatTraits<FMT>::CPL, BITS = FormatTraits<FMT>::BITS, T8 = CPL / 8;
+  constexpr int KSTEP = 4 * CPL, KG = 4, WSTEP = KG * KSTEP;
+  constexpr int D = (KMAX + WSTEP - 1) / WSTEP;      // weight loads per lane
+  static_assert(D <= 32, "KMAX too long for one tile per workgroup");
+  constexpr int XLD = KMAX + KSTEP + 8;              // staged row pitch (halves)
+  constexpr int NBR = KMAX / 8;                      // 8-code blocks per staged row
+  constexpr int XT = (MP * NBR + 255) / 256;         // activation loads per thread
+  static_assert(XT <= 16, "the staged rows are loaded in one batch");
+  constexpr int GMAX = KMAX / 32;                    // groups per row at most (groups >= 32)
+  constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert(MP == 4 || MP == 8 || MP == 16, "MP is 4, 8 or 16");
+  __shared__ __align__(16) f16 xs[(MP + 1) * XLD];   // MP rows, then the zero row
+  __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
+  __shared__ float red[(KG - 1) * 64 * 4];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int K = p.K;
+  const int n0 = blockIdx.x * 16;
+  const int rows = min(16, p.N - n0);
+  const int row_bytes = K * BITS / 8;
+  const int blocks = K >> 3;
+
+  // Epilogue operands of row n0 + j (lanes of group 0): bias, per-row scale.
+  const int eoff = g == 0 && j < rows ? (n0 + j) * 2 : kOutOfRange;
+  const size_t nb = (size_t)p.N * 2;
+  const uint32_t ebias = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? nb : 0), eoff, 0, 0);
+  const uint32_t erow = SCALED ? 0u : __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.scales, nb), eoff, 0, 0);
+  // Activation rows, issued before the weights (a wait for them leaves the weights in flight):
+  // piece i = (row m, 8-code block b); blocks past K read zeros.
+  h8 xv[XT];
+#pragma unroll
+  for (int i = 0; i < XT; ++i) {
+    const int idx = i * 256 + t;
+    const int m = idx / NBR, b = idx - m * NBR;
+    const bool live = m < p.M && b < blocks;
+    xv[i] = __builtin_bit_cast(
+        h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x + (size_t)(live ? m : 0) * p.ldx, (size_t)K * 2),
+                                                  live ? b * 16 : kOutOfRange, 0, 0));
+  }
+  // Scales of the tile's rows (16 x G halves), weights of this wave's k steps.
+  uint32_t sreg[SC > 0 ? SC : 1];
+  if constexpr (SCALED) {
+    const __amdgpu_buffer_rsrc_t sb = buffer_rsrc(p.scales + (size_t)n0 * p.G, (size_t)rows * p.G * 2);
+#pragma unroll
+    for (int i = 0; i < SC; ++i) sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, (t + 256 * i) * 2, 0, 0);
+  }
+  const __amdgpu_buffer_rsrc_t wb = buffer_rsrc(p.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  u4 w[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int k = (wave + KG * u) * KSTEP + g * CPL;
+    w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
+#pragma unroll
+  for (int i = 0; i < XT; ++i) {
+    const int idx = i * 256 + t;
+    const int m = idx / NBR, b = idx - m * NBR;
+    if (m < p.M) *reinterpret_cast<h8 *>(xs + m * XLD + 8 * b) = permute_block<FMT>(xv[i]);
+  }
+  // Zero tails (k from KMAX on) of the staged rows and the whole zero row.
+  for (int i = t; i < MP * ((XLD - KMAX) / 8); i += 256) {
+    const int m = i / ((XLD - KMAX) / 8), b = i - m * ((XLD - KMAX) / 8);
+    if (m < p.M) *reinterpret_cast<h8 *>(xs + m * XLD + KMAX + 8 * b) = h8{};
+  }
+  for (int i = t; i < XLD / 8; i += 256) *reinterpret_cast<h8 *>(xs + MP * XLD + 8 * i) = h8{};
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      if (t + 256 * i < 16 * GMAX) ss[t + 256 * i] = __builtin_bit_cast(f16, (unsigned short)sreg[i]);
+    if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;
+  }
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  __syncthreads();
+
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const f16 *a0 = xs + (j < p.M ? j : MP) * XLD + g * CPL;
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int kb = (wave + KG * u) * KSTEP;
+    if (kb >= K) break;  // wave-uniform
+    asm volatile("" : "+v"(w[u]));  // decode here, not at the load
+    h2 s2 = {(f16)1.0f, (f16)1.0f};
+    if constexpr (SCALED) {
+      // past K the scale is zero (index past the row's groups reads the next row or the pad,
+      // and the codes there are zero: only the zero scale makes fp16(q * s) zero for every format)
+      const f16 sc = kb + g * CPL < K ? ss[j * p.G + ((kb + g * CPL) >> p.group_shift)] : (f16)0.0f;
+      s2 = h2{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < T8; ++q) {
+      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, decode8<FMT, !SCALED>(w[u], q, s2, nf4_table), acc, 0, 0, 0);
+    }
+  }
+  // Partial sums of waves 1..3 through LDS; wave 0 adds them in order and writes the tile.
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((wave - 1) * 64 + lane) * 4 + r] = acc[r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    acc[r] = ((acc[r] + red[lane * 4 + r]) + red[(64 + lane) * 4 + r]) + red[(128 + lane) * 4 + r];
+  // Lane (j, g) holds rows 4g .. 4g+3 of column j (weight row n0 + j).  The bias / per-row
+  // scale of column j sit in lane j (group 0).
+  const f16 bias = __builtin_bit_cast(f16, (unsigned short)__shfl((int)ebias, j, 64));
+  const f16 rowscale = __builtin_bit_cast(f16, (unsigned short)__shfl((int)erow, j, 64));
+  if (j >= rows) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * g + r;
+    if (m >= p.M) continue;
+    float v = acc[r];
+    if constexpr (!SCALED) v *= (float)rowscale;
+    f16 h = (f16)v;
+    if (p.bias) h = (f16)((float)h + (float)bias);
+    p.y[(size_t)m * p.ldy + n0 + j] = h;
+  }
+}
+
+// Launches tile_rows_kernel for 2 <= p.M <= 16 rows with M * K <= 32768 (K <= 4096): the staged
+// rows are loaded in one batch of at most 16 loads per thread.
+void launch_tile_rows(const StreamParams &p, int format, bool scaled, hipStream_t stream);
+
 // Launches stream_rows_kernel for 2 <= p.M <= 16 rows (K <= 4096, groups of at least 32 codes
 // that are powers of two, or one per row).
 void launch_stream_rows(const StreamParams &p, int format, bool scaled, hipStream_t stream);

@@ -21,7 +21,7 @@ using namespace lb::abi;
 
 namespace {
 
-enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4 };
+enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4, PATH_TILE = 5 };
 enum Variant { VAR_PLAIN = 0, VAR_COMPACT = 1, VAR_W8A8 = 2 };
 constexpr int kCompactMaxGroups = 32;
 constexpr int64_t kW8A8MaxK = 131072;  // |sum| <= K * 128 * 127 stays inside int32
@@ -262,6 +262,23 @@ bool stream_rows_eligible(const lb_linear_args *a) {
   return bytes >= LB_STREAM_ROWS_MIN_BYTES;
 }
 
+#ifndef LB_TILE_ROWS
+#define LB_TILE_ROWS 1  // 2..16 rows below the streaming sizes: tile_rows_kernel (one workgroup per tile)
+#endif
+#ifndef LB_TILE_ROWS_MAX_X_BYTES
+#define LB_TILE_ROWS_MAX_X_BYTES (32ll << 20)  // activation bytes all tiles stage together, at most
+#endif
+
+// Several activation rows, no correction, rows the one-tile kernel stages whole (K <= 4096, and
+// K <= 2048 beyond 8 rows), int4 / nf4 / int8 codes.  Every tile stages all M rows, so the tiles
+// together read the activations (N / 16) times: past LB_TILE_ROWS_MAX_X_BYTES of those reads the
+// tiled GEMV, whose workgroups share the staged rows over more tiles, measured faster.
+bool tile_rows_eligible(const lb_linear_args *a) {
+  if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16 || a->K > 4096 || (a->M > 8 && a->K > 2048)) return false;
+  if ((a->N + 15) / 16 * a->M * a->K * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
+  return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
+}
+
 // Workspace and kernel path of the compact_groups and W8A8 variants.
 Plan make_variant_plan(const lb_linear_args *a, int variant) {
   Plan pl;
@@ -311,6 +328,8 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     pl.path = PATH_ROW;
   } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && stream_rows_eligible(a)) {
     pl.path = PATH_STREAM;
+  } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && tile_rows_eligible(a)) {
+    pl.path = PATH_TILE;
   } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) {
     pl.path = PATH_GEMV;
   } else {
@@ -728,7 +747,7 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     launch_fused(fp, fmt, scaled, a->rank > 0, tiles, s);
     return launch_status("lb_linear");
   }
-  if (plan.path == PATH_STREAM) {
+  if (plan.path == PATH_STREAM || plan.path == PATH_TILE) {
     StreamParams sp{};
     sp.x = p.x;
     sp.codes = p.codes;
@@ -743,7 +762,8 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     sp.ldx = p.ldx;
     sp.ldy = p.ldy;
     sp.tiles = (int)((a->N + 15) / 16);
-    if (a->M > 16) launch_stream_wide(sp, fmt, !p.per_row, s);
+    if (plan.path == PATH_TILE) launch_tile_rows(sp, fmt, !p.per_row, s);
+    else if (a->M > 16) launch_stream_wide(sp, fmt, !p.per_row, s);
     else if (a->M >= LB_STREAM_ROWS_DECODE_MIN_M) launch_stream_rows(sp, fmt, !p.per_row, s);
     else launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
     return launch_status("lb_linear");

@@ -20,6 +20,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cp
        python bench.py --decode-only      (config-4 decode leg alone, for rocprofv3 --kernel-trace)
        python bench.py --profile-gemm     (prefill GEMMs + hipBLASLt fp16 of the same shapes, for --pmc)
        python bench.py --profile-stream   (config-5 128256x4096 INT4 GEMV at M=1 + a copy, for rocprofv3)
+       python bench.py --profile-multirow (multi-row GEMVs and a split-K GEMM, for rocprofv3 --kernel-trace)
 """
 import argparse
 import json
@@ -358,6 +359,26 @@ def profile_gemm(device, stream):
                               flops_per_launch=2 * m * n * k)), flush=True)
 
 
+MULTIROW_PROFILE_SHAPES = [('int4', 8, 4096, 4096, 128), ('int4', 16, 128256, 4096, 128),
+                           ('int4', 32, 128256, 4096, 128), ('nf4', 512, 960, 2560, 64)]
+
+
+def profile_multirow(device, stream):
+    """The multi-row GEMV paths and a split-K prefill GEMM on their default dispatch, 16 launches
+    each over the replica pool (for rocprofv3 --kernel-trace): one-tile rows (config 5 at M=8),
+    streaming rows (M=16), K-outer streaming rows (M=32), split-K NF4 down projection (M=512)."""
+    for i, (fmt, m, n, k, g) in enumerate(MULTIROW_PROFILE_SHAPES):
+        wb = algorithmic_bytes(fmt, 0, n, k, g)
+        lin = Linear(make_weight(fmt, n, k, g, 700 + i), m, copies_for(wb, cap=16), device, 800 + i)
+        for r in range(16):
+            lin.calls[r % len(lin.calls)].run()
+        torch.cuda.synchronize()
+        print(json.dumps(dict(profile='multirow', fmt=fmt, M=m, N=n, K=k, group=g, launches=16,
+                              algorithmic_bytes=lin.bytes, flops_per_launch=2 * m * n * k)), flush=True)
+        del lin
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -372,6 +393,8 @@ def main():
     ap.add_argument('--decode-steps', type=int, default=128)
     ap.add_argument('--decode-only', action='store_true', help='only the config-4 decode leg (for tracing)')
     ap.add_argument('--profile-gemm', action='store_true', help='prefill GEMMs alone (for rocprofv3 --pmc)')
+    ap.add_argument('--profile-multirow', action='store_true',
+                    help='multi-row GEMV paths and a split-K prefill GEMM alone (for rocprofv3 --kernel-trace)')
     ap.add_argument('--profile-stream', action='store_true',
                     help='the config-5 128256x4096 INT4 GEMV (M=1, stream kernel) alone, for rocprofv3')
     args = ap.parse_args()
@@ -396,6 +419,9 @@ def main():
         return
     if args.profile_stream:
         profile_kernel(device, stream, LLAMA_SHAPES[-1])
+        return
+    if args.profile_multirow:
+        profile_multirow(device, stream)
         return
     if args.decode_only:
         decode = decode_leg(device, args.decode_steps, 0)

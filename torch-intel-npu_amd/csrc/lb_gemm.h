@@ -29,6 +29,18 @@ namespace lb {
 #define LB_GEMM4_SWZ_SHIFT 0
 #endif
 #define LB_G4_SWZ(r) (((r) >> LB_GEMM4_SWZ_SHIFT) & 7)
+#ifndef LB_GEMM4_SCHED
+#define LB_GEMM4_SCHED 1  // interleave each MFMA with a share of the step's other instructions
+#endif
+#ifndef LB_GEMM4_ADMA
+#define LB_GEMM4_ADMA 1  // activations straight from memory to LDS (buffer_load ... lds)
+#endif
+#ifndef LB_GEMM4_SCHED_VALU
+#define LB_GEMM4_SCHED_VALU 8
+#endif
+#ifndef LB_GEMM4_SCHED_DSR
+#define LB_GEMM4_SCHED_DSR 1
+#endif
 #ifndef LB_GEMM_IGLP_VALU
 #define LB_GEMM_IGLP_VALU 4
 #endif
@@ -246,10 +258,14 @@ __device__ __forceinline__ void static_for(F &&f) {
 // reads TM A and TN B fragments for its TM TN MFMAs.  LDS holds two stages of A (fp16 activations)
 // and B (decoded fp16 weights), BM (BN) rows x 64 halves each, without padding: the 16-byte chunk c
 // of row r is stored at chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.
-// The next step's activations and packed weights are loaded into registers one step ahead; they
-// are decoded and written to the other LDS stage between the MFMA groups of the current step, and
-// one barrier per step separates the stages.  Fragment reads of substep kk + 1 are issued before
-// the MFMAs of substep kk.  With split-K (p.splits > 1, grid z = split) a workgroup covers
+// The next step's activations go straight from memory to the other LDS stage (buffer_load ...
+// lds; the two stages are separate arrays so the compiler sees no alias with the stage being
+// read), issued at the start of the step and complete before its closing barrier; the packed
+// weights of the step after it are loaded into registers and decoded into the other B stage
+// between the MFMA groups.  Each MFMA of a substep is followed by a share of the other work (one
+// LDS read, up to 8 VALU, one LDS write, one global load: sched_group_barrier), so the MFMA pipe
+// is fed while the decode and the transfers proceed.  Fragment reads of substep kk + 1 are issued
+// before the MFMAs of substep kk.  With split-K (p.splits > 1, grid z = split) a workgroup covers
 // k in [z * kslice, z * kslice + kslice) and writes fp32 sums to p.partial.
 template <int FMT, bool SCALED, int WAVES, int BM = 256, int BN = 256>
 __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
@@ -270,7 +286,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   static_assert((WAVES == 4 || WAVES == 8) && TM >= 1 && TN >= 1 && B_PER >= 1 && A_PER >= 1 &&
                     BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0,
                 "tile constants");
-  __shared__ __align__(16) f16 As[2 * STAGE_A];
+  // The two activation stages are separate arrays, so the compiler sees that a transfer into one
+  // does not alias reads of the other.
+  __shared__ __align__(16) f16 As0[STAGE_A];
+  __shared__ __align__(16) f16 As1[STAGE_A];
   __shared__ __align__(16) f16 Bs[2 * STAGE_B];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
@@ -309,9 +328,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   u4 ra[A_PER], rb[B_PER];
   f16 rs[B_PER];
   auto load = [&](int k0) {
+#if !LB_GEMM4_ADMA
 #pragma unroll
     for (int i = 0; i < A_PER; ++i)
       ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, a_off[i] + k0 * 2, 0, 0));
+#endif
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
       rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, b_off[i] + k0 * BITS / 8, 0, 0));
@@ -320,14 +341,39 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
             f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, s_off[i] + (((k0 + b_code[i]) >> p.group_shift) << 1), 0, 0));
     }
   };
-  auto store_a = [&](int st) {
-    f16 *dst = As + st * STAGE_A;
+  auto astage = [&](auto st) -> f16 * {
+    if constexpr (decltype(st)::value == 0) return As0;
+    else return As1;
+  };
+  auto store_a = [&](auto st) {
+    f16 *dst = astage(st);
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
       asm volatile("" : "+v"(ra[i]));
       *reinterpret_cast<u4 *>(dst + a_lds[i]) = ra[i];
     }
   };
+#if LB_GEMM4_ADMA
+  // Activations straight to LDS (buffer_load ... lds): block i of a stage is the 1 KB of rows
+  // 8i .. 8i+7; lane L of the wave writes its chunk position L & 7 of row 8i + L / 8, so it loads
+  // the row's chunk (L & 7) ^ swizzle(row).  Wave w moves blocks w, w + WAVES, ...
+  constexpr int ABLK = BM / 8 / WAVES;  // 1 KB blocks per wave per stage
+  int adma_off[ABLK];
+#pragma unroll
+  for (int i = 0; i < ABLK; ++i) {
+    const int r = 8 * (wave + WAVES * i) + (lane >> 3), pc = lane & 7;
+    adma_off[i] = r < rows_a ? (r * p.ldx + 8 * (pc ^ LB_G4_SWZ(r))) * 2 : kOutOfRange;
+  }
+  auto dma_a = [&](auto st, int k0) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address space exists in the device pass only
+#pragma unroll
+    for (int i = 0; i < ABLK; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xbuf, (__attribute__((address_space(3))) void *)(astage(st) + (wave + WAVES * i) * 512), 16,
+          adma_off[i] + k0 * 2, 0, 0, 0);
+#endif
+  };
+#endif
   auto store_b = [&](int st) {
     f16 *dst = Bs + st * STAGE_B;
 #pragma unroll
@@ -364,20 +410,34 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   int koff[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) koff[kk] = 8 * ((2 * kk + fh) ^ LB_G4_SWZ(fr));
-  const f16 *a_lane = As + (wm * WROWS + fr) * BK;
+  const int a_lane = (wm * WROWS + fr) * BK;
   const f16 *b_lane = Bs + (wn * WCOLS + fr) * BK;
 
   const int kbeg = p.splits > 1 ? (int)blockIdx.z * p.kslice : 0;
   const int steps = (min(p.K, kbeg + (p.splits > 1 ? p.kslice : p.K)) - kbeg) / BK;
+#if LB_GEMM4_ADMA
+  // vmcnt-only wait: all but the last n vector-memory operations of this wave are complete.
+  auto wait_vm = [](auto n) {
+    constexpr int N = decltype(n)::value;
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  };
+  dma_a(std::integral_constant<int, 0>{}, kbeg);
+  __builtin_amdgcn_sched_barrier(0);
   load(kbeg);
-  store_a(0);
+  store_b(0);
+  load(kbeg + min(1, steps - 1) * BK);
+  wait_vm(std::integral_constant<int, 0>{});
+#else
+  load(kbeg);
+  store_a(std::integral_constant<int, 0>{});
   store_b(0);
   if (steps > 1) load(kbeg + BK);
+#endif
   __syncthreads();
   // One K step on LDS stage ST (compile-time, so every LDS offset is an immediate).
   auto step = [&](auto stage, int s) {
     constexpr int ST = decltype(stage)::value;
-    const f16 *a_base = a_lane + ST * STAGE_A;
+    const f16 *a_base = astage(stage) + a_lane;
     const f16 *b_base = b_lane + ST * STAGE_B;
     h8 fa[2][TM], fb[2][TN];
 #pragma unroll
@@ -401,20 +461,67 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
         for (int jj = 0; jj < TN; ++jj)
           acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][jj], acc[i][jj], 0, 0, 0);
       // The next step's operands go to the other stage between the MFMA groups.
+#if LB_GEMM4_ADMA
+      // Activations of step s + 1 go straight to the other stage (free since the last barrier);
+      // packed weights of step s + 2 to registers.  Past the last step both re-read it (in range).
+      if (kk == 0) {
+        dma_a(std::integral_constant<int, ST ^ 1>{}, kbeg + min(s + 1, steps - 1) * BK);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kk == 2) {
+        store_b(ST ^ 1);
+        load(kbeg + min(s + 2, steps - 1) * BK);
+      }
+#if LB_GEMM4_SCHED
+#pragma unroll
+      for (int i = 0; i < TM * TN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, LB_GEMM4_SCHED_DSR, 0);   // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x002, LB_GEMM4_SCHED_VALU, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // one LDS write
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // one global load
+      }
+#endif
+#elif LB_GEMM4_SCHED
+      // One basic block per step (past the last step the loads re-read the last step, in range,
+      // and the stores fill the idle stage), and each MFMA followed by a share of the other work.
+      if (kk == 1) store_a(std::integral_constant<int, ST ^ 1>{});
+      if (kk == 2) {
+        store_b(ST ^ 1);
+        load(kbeg + min(s + 2, steps - 1) * BK);
+      }
+#pragma unroll
+      for (int i = 0; i < TM * TN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, LB_GEMM4_SCHED_VALU, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // one LDS write
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // one global load
+      }
+#else
       if (s + 1 < steps) {
-        if (kk == 1) store_a(ST ^ 1);
+        if (kk == 1) store_a(std::integral_constant<int, ST ^ 1>{});
         if (kk == 2) {
           store_b(ST ^ 1);
           if (s + 2 < steps) load(kbeg + (s + 2) * BK);
         }
       }
+#endif
     }
+#if LB_GEMM4_ADMA
+    // The activations moved this step are complete (only the weight loads issued after them,
+    // B_PER codes plus B_PER scales, may be outstanding) before the barrier publishes them.
+    wait_vm(std::integral_constant<int, SCALED ? 2 * B_PER : B_PER>{});
+#endif
     __syncthreads();
   };
   for (int s = 0; s < steps; s += 2) {
     step(std::integral_constant<int, 0>{}, s);
     if (s + 1 < steps) step(std::integral_constant<int, 1>{}, s + 1);
   }
+#if LB_GEMM4_ADMA
+  __builtin_amdgcn_s_waitcnt(0);  // no transfer into LDS outlives the loop
+#endif
 
   // D layout of the 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   // Tile indices are compile-time (static_for), so the accumulators stay in AGPRs.

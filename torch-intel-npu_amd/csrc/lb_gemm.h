@@ -36,7 +36,7 @@ namespace lb {
 #define LB_GEMM4_ADMA 1  // activations straight from memory to LDS (buffer_load ... lds)
 #endif
 #ifndef LB_GEMM4_SCHED_VALU
-#define LB_GEMM4_SCHED_VALU 8
+#define LB_GEMM4_SCHED_VALU 0  // VALU instructions after each MFMA (0: 8 with eight waves, 4 with four)
 #endif
 #ifndef LB_GEMM4_SCHED_DSR
 #define LB_GEMM4_SCHED_DSR 1
@@ -283,6 +283,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   constexpr int A_PER = BM * (BK / 8) / NT;         // A chunks per thread per step
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK;  // halves per operand per stage
   constexpr int kOutOfRange = (int)0x80000000u;
+  constexpr int SCHED_VALU = LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (WAVES == 8 ? 8 : 4);
   static_assert((WAVES == 4 || WAVES == 8) && TM >= 1 && TN >= 1 && B_PER >= 1 && A_PER >= 1 &&
                     BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0,
                 "tile constants");
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
       for (int i = 0; i < TM * TN; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, LB_GEMM4_SCHED_DSR, 0);   // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x002, LB_GEMM4_SCHED_VALU, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, SCHED_VALU, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // one LDS write
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // one global load
       }
@@ -494,7 +495,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
       for (int i = 0; i < TM * TN; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // one LDS read
-        __builtin_amdgcn_sched_group_barrier(0x002, LB_GEMM4_SCHED_VALU, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, SCHED_VALU, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // one LDS write
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // one global load
       }

@@ -150,13 +150,16 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM_BK 64
 #endif
 #ifndef LB_GEMM_BIG_MIN
-#define LB_GEMM_BIG_MIN 256  // large tiles from this many workgroups
+#define LB_GEMM_BIG_MIN 160  // 128 x 128 tiles from this many workgroups
 #endif
 #ifndef LB_GEMM4_WAVES
 #define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
 #endif
 #ifndef LB_GEMM4_MIN_TILES
 #define LB_GEMM4_MIN_TILES 192  // 256 x 256 tiles from this many workgroups
+#endif
+#ifndef LB_GEMM_MID
+#define LB_GEMM_MID 1  // 128 x 128 tiles: 1 gemm4_kernel with four waves, 0 gemm2_kernel
 #endif
 #ifndef LB_GEMM_SPLIT_WGS
 #define LB_GEMM_SPLIT_WGS 256   // split K while the tile grid has fewer workgroups than this
@@ -183,7 +186,7 @@ struct GemmShape {
 
 // Tile kernel and K split of a prefill GEMM:
 //   - 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs;
-//   - else 128 x 128 tiles (gemm2_kernel) when they alone give every CU a workgroup;
+//   - else 128 x 128 tiles (gemm4_kernel with four waves) from LB_GEMM_BIG_MIN workgroups on;
 //   - else, for a small 128 x 128 grid (< LB_GEMM_SPLIT128_BELOW tiles) over long rows, 128 x 128
 //     tiles split along K into slices of at least LB_GEMM_SPLIT_LONG_STEPS k steps, when the
 //     slices fill the CUs;
@@ -539,8 +542,13 @@ void launch_gemm_t(const LinearParams &p, hipStream_t s) {
     hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, gz),
                        dim3(64 * LB_GEMM4_WAVES), 0, s, p);
   } else if (kind == GEMM_128) {
+#if LB_GEMM_MID
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, BM, BN>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),
+                       dim3(256), 0, s, p);
+#else
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),
                        dim3(256), 0, s, p);
+#endif
   } else if (kind == GEMM_64) {
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
                        0, s, p);

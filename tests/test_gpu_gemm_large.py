@@ -1,7 +1,8 @@
 """GPU parity of the 256 x 256 prefill GEMM (gemm4_kernel) against the CPU oracle.
 
-Prefill calls whose 256 x 256 tiles give at least 192 workgroups (K a multiple of 64) run
-there.  Same bars as every linear path: rel-L2 <= 1e-3 against the oracle and the reference's
+Prefill calls whose 256 x 256 tiles give at least 160 workgroups (K a multiple of 64) run
+there; calls with fewer, whose 256 x 128 tiles give 192 to 256 (rows past M adding at most an
+eighth), run its four-wave 256 x 128 form.  Same bars as every linear path: rel-L2 <= 1e-3 against the oracle and the reference's
 rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for identity-like inputs with
 power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover every format, partial
 tiles in M and N, bias, per-row int8 scales and the rank-32 correction.
@@ -19,6 +20,7 @@ pytestmark = pytest.mark.gpu
 LARGE = [
     ('int4', 2048, 6144, 256, 128), ('int4', 2000, 6100, 192, 64), ('int4', 1792, 7168, 128, 32),
     ('nf4', 2048, 6144, 128, 64), ('int8', 2048, 6144, 256, 256), ('int8', 1800, 6400, 128, 64),
+    ('int4', 768, 14000, 128, 64), ('nf4', 700, 14336, 64, 64),
 ]
 
 
@@ -29,6 +31,30 @@ def test_gemm4_matches_oracle(device, spec):
     rng = np.random.default_rng(m + n + k + group)
     p = problem(rng, fmt, m, n, k, group)
     check(p, run(p, device), f'gemm4 {spec}')
+
+
+# 256 x 128 tiles: fewer than 160 tiles of 256 x 256, 192 to 256 of 256 x 128.
+TALL = [
+    ('int4', 512, 12500, 256, 128), ('nf4', 480, 13000, 128, 64), ('int8', 1000, 6200, 192, 64),
+    ('int8', 512, 12800, 128, 128),
+]
+
+
+@pytest.mark.parametrize('spec', TALL, ids=lambda s: '-'.join(map(str, s)))
+def test_gemm4_tall_tiles_match_oracle(device, spec):
+    fmt, m, n, k, group = spec
+    announce('gemm4 256x128', spec)
+    rng = np.random.default_rng(m + n + k + group + 1)
+    p = problem(rng, fmt, m, n, k, group)
+    check(p, run(p, device), f'gemm4 256x128 {spec}')
+
+
+def test_gemm4_tall_tiles_bias_and_correction(device):
+    spec = ('int4', 512, 12544, 128, 64)
+    announce('gemm4 256x128 bias+correction', spec)
+    rng = np.random.default_rng(77)
+    p = problem(rng, *spec, rank=32, bias=True)
+    check(p, run(p, device), f'gemm4 256x128 correction {spec}')
 
 
 def test_gemm4_fp16_weights(device):

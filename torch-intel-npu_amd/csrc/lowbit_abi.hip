@@ -156,7 +156,13 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
 #endif
 #ifndef LB_GEMM4_MIN_TILES
-#define LB_GEMM4_MIN_TILES 192  // 256 x 256 tiles from this many workgroups
+#define LB_GEMM4_MIN_TILES 160  // 256 x 256 tiles from this many workgroups
+#endif
+#ifndef LB_GEMM_TALL_MIN
+#define LB_GEMM_TALL_MIN 192  // 256 x 128 tiles (four waves) from this many workgroups ...
+#endif
+#ifndef LB_GEMM_TALL_MAX
+#define LB_GEMM_TALL_MAX 256  // ... up to this many (one workgroup per CU)
 #endif
 #ifndef LB_GEMM_MID
 #define LB_GEMM_MID 1  // 128 x 128 tiles: 1 gemm4_kernel with four waves, 0 gemm2_kernel
@@ -177,7 +183,7 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM_SPLIT_MIN_STEPS 8  // k steps per slice at least
 #endif
 
-enum { GEMM_256 = 0, GEMM_128 = 1, GEMM_64 = 2, GEMM_64_K32 = 3 };
+enum { GEMM_256 = 0, GEMM_128 = 1, GEMM_64 = 2, GEMM_64_K32 = 3, GEMM_256x128 = 4 };
 struct GemmShape {
   int kind = GEMM_64;
   int splits = 1;
@@ -186,6 +192,8 @@ struct GemmShape {
 
 // Tile kernel and K split of a prefill GEMM:
 //   - 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs;
+//   - else 256 x 128 tiles (gemm4_kernel with four waves) when they fill the CUs in one round
+//     (LB_GEMM_TALL_MIN to LB_GEMM_TALL_MAX workgroups) and the rows past M add at most an eighth;
 //   - else 128 x 128 tiles (gemm4_kernel with four waves) from LB_GEMM_BIG_MIN workgroups on;
 //   - else, for a small 128 x 128 grid (< LB_GEMM_SPLIT128_BELOW tiles) over long rows, 128 x 128
 //     tiles split along K into slices of at least LB_GEMM_SPLIT_LONG_STEPS k steps, when the
@@ -201,6 +209,7 @@ GemmShape gemm_shape(int64_t M, int64_t N, int64_t K, int64_t slices, bool allow
   const int64_t huge = ((M + 255) / 256) * ((N + 255) / 256) * slices;
   const int64_t big = ((M + LB_GEMM_BM - 1) / LB_GEMM_BM) * ((N + LB_GEMM_BN - 1) / LB_GEMM_BN) * slices;
   const int64_t small = ((M + 63) / 64) * ((N + 63) / 64) * slices;
+  const int64_t tall = ((M + 255) / 256) * ((N + 127) / 128) * slices;
   const bool can_split = allow_split && slices == 1;
   const int64_t s128 = std::min<int64_t>(LB_GEMM_SPLIT_MAX, K / LB_GEMM_BK / LB_GEMM_SPLIT_LONG_STEPS);
   gs.kslice = (int)K;
@@ -208,6 +217,9 @@ GemmShape gemm_shape(int64_t M, int64_t N, int64_t K, int64_t slices, bool allow
   int bk = K % 64 == 0 ? 64 : 32;
   if (huge >= LB_GEMM4_MIN_TILES && K % 64 == 0) {
     gs.kind = GEMM_256;
+  } else if (tall >= LB_GEMM_TALL_MIN && tall <= LB_GEMM_TALL_MAX && K % 64 == 0 &&
+             (M + 255) / 256 * 256 * 8 <= 9 * M) {
+    gs.kind = GEMM_256x128;
   } else if (big >= LB_GEMM_BIG_MIN && K % LB_GEMM_BK == 0) {
     gs.kind = GEMM_128;
   } else if (can_split && K % LB_GEMM_BK == 0 && big < LB_GEMM_SPLIT128_BELOW && s128 > 1 &&
@@ -541,6 +553,9 @@ void launch_gemm_t(const LinearParams &p, hipStream_t s) {
   if (kind == GEMM_256) {
     hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, gz),
                        dim3(64 * LB_GEMM4_WAVES), 0, s, p);
+  } else if (kind == GEMM_256x128) {
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, 256, 128>), dim3((p.N + 127) / 128, (p.M + 255) / 256, gz),
+                       dim3(256), 0, s, p);
   } else if (kind == GEMM_128) {
 #if LB_GEMM_MID
     hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, BM, BN>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),

@@ -241,6 +241,8 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
     }
 }
 
+typedef uint32_t u2w __attribute__((ext_vector_type(2)));
+
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices, so register
 // arrays indexed by them stay in registers).
 template <class F, int... I>
@@ -252,8 +254,8 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// BM x BN prefill GEMM (BM, BN = 128 or 256) with WAVES = 4 or 8 waves in a 2 x (WAVES / 2)
-// grid; a wave owns a (BM / 2) x (BN / (WAVES / 2)) block of v_mfma_f32_32x32x16_f16 tiles
+// BM x BN prefill GEMM (BM, BN = 128 or 256) with WAVES = 4 or 8 waves in a WM x (WAVES / WM)
+// grid; a wave owns a (BM / WM) x (BN / (WAVES / WM)) block of v_mfma_f32_32x32x16_f16 tiles
 // (TM x TN), whose fp32 accumulators live in AGPRs.  Per K step of 64 and 16-deep substep, a wave
 // reads TM A and TN B fragments for its TM TN MFMAs.  LDS holds two stages of A (fp16 activations)
 // and B (decoded fp16 weights), BM (BN) rows x 64 halves each, without padding: the 16-byte chunk c
@@ -267,25 +269,28 @@ __device__ __forceinline__ void static_for(F &&f) {
 // is fed while the decode and the transfers proceed.  Fragment reads of substep kk + 1 are issued
 // before the MFMAs of substep kk.  With split-K (p.splits > 1, grid z = split) a workgroup covers
 // k in [z * kslice, z * kslice + kslice) and writes fp32 sums to p.partial.
-template <int FMT, bool SCALED, int WAVES, int BM = 256, int BN = 256>
+template <int FMT, bool SCALED, int WAVES, int BM = 256, int BN = 256, int WM = 2>
 __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   constexpr int BK = 64;
   constexpr int NT = 64 * WAVES;
-  constexpr int WN = WAVES / 2;                     // waves along N
-  constexpr int WROWS = BM / 2;                     // rows per wave
+  constexpr int WN = WAVES / WM;                    // waves along N
+  constexpr int WROWS = BM / WM;                    // rows per wave
   constexpr int TM = WROWS / 32;                    // 32-row MFMA tiles per wave
   constexpr int WCOLS = BN / WN;                    // columns per wave
   constexpr int TN = WCOLS / 32;                    // 32-column MFMA tiles per wave
   constexpr int BITS = FormatTraits<FMT>::BITS;
-  constexpr int CODES = 16 * 8 / BITS;              // codes per 16-byte B chunk
+  // Packed B chunks of 16 bytes, or of 8 where 16-byte chunks would leave threads without one
+  // (4-bit codes, BN * 2 < NT): every thread then decodes an equal share.
+  constexpr int CB = BN * (BK * BITS / 8 / 16) < NT ? 8 : 16;
+  constexpr int CODES = CB * 8 / BITS;              // codes per B chunk
   constexpr int B_ROW_CHUNKS = BK / CODES;          // packed chunks per B row per step
   constexpr int B_PER = BN * B_ROW_CHUNKS / NT;     // packed B chunks per thread per step
   constexpr int A_PER = BM * (BK / 8) / NT;         // A chunks per thread per step
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK;  // halves per operand per stage
   constexpr int kOutOfRange = (int)0x80000000u;
-  constexpr int SCHED_VALU = LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (WAVES == 8 ? 8 : 4);
-  static_assert((WAVES == 4 || WAVES == 8) && TM >= 1 && TN >= 1 && B_PER >= 1 && A_PER >= 1 &&
-                    BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0,
+  constexpr int SCHED_VALU = LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (WAVES >= 8 ? 8 : 4);
+  static_assert((WAVES == 4 || WAVES == 8 || WAVES == 16) && WAVES % WM == 0 && TM >= 1 && TN >= 1 && B_PER >= 1 &&
+                    A_PER >= 1 && BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0 && (CB == 16 || BITS == 4),
                 "tile constants");
   // The two activation stages are separate arrays, so the compiler sees that a transfer into one
   // does not alias reads of the other.
@@ -336,7 +341,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
 #endif
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
-      rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, b_off[i] + k0 * BITS / 8, 0, 0));
+      if constexpr (CB == 16) {
+        rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, b_off[i] + k0 * BITS / 8, 0, 0));
+      } else {
+        const u2w h = __builtin_bit_cast(u2w, __builtin_amdgcn_raw_buffer_load_b64(wbuf, b_off[i] + k0 * BITS / 8, 0, 0));
+        rb[i] = u4{h[0], h[1], 0u, 0u};
+      }
       if constexpr (SCALED)
         rs[i] = __builtin_bit_cast(
             f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, s_off[i] + (((k0 + b_code[i]) >> p.group_shift) << 1), 0, 0));

@@ -155,11 +155,23 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #ifndef LB_GEMM4_WAVES
 #define LB_GEMM4_WAVES 8        // waves per 256 x 256 tile (4: 128 x 128 per wave; 8: 128 x 64)
 #endif
+#ifndef LB_GEMM4_WM
+#define LB_GEMM4_WM 2           // waves along M of a 256 x 256 tile
+#endif
+#ifndef LB_GEMM_MID_WAVES
+#define LB_GEMM_MID_WAVES 8     // waves per 128 x 128 tile ...
+#endif
+#ifndef LB_GEMM_MID_WM
+#define LB_GEMM_MID_WM 2        // ... and along its M
+#endif
 #ifndef LB_GEMM4_MIN_TILES
 #define LB_GEMM4_MIN_TILES 160  // 256 x 256 tiles from this many workgroups
 #endif
 #ifndef LB_GEMM_TALL_MIN
-#define LB_GEMM_TALL_MIN 192  // 256 x 128 tiles (four waves) from this many workgroups ...
+#define LB_GEMM_TALL_MIN 160  // 256 x 128 tiles (four waves) from this many workgroups ...
+#endif
+#ifndef LB_GEMM_TALL_WAVES
+#define LB_GEMM_TALL_WAVES 8  // 256 x 128 tiles: 8 waves of 64 x 64, or 4 of 128 x 64
 #endif
 #ifndef LB_GEMM_TALL_MAX
 #define LB_GEMM_TALL_MAX 256  // ... up to this many (one workgroup per CU)
@@ -551,15 +563,16 @@ void launch_gemm_t(const LinearParams &p, hipStream_t s) {
   const int kind = gemm_shape(p.M, p.N, p.K, p.slices, p.splits > 1).kind;
   const unsigned gz = (unsigned)(p.splits > 1 ? p.splits : p.slices);
   if (kind == GEMM_256) {
-    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES>), dim3((p.N + 255) / 256, (p.M + 255) / 256, gz),
-                       dim3(64 * LB_GEMM4_WAVES), 0, s, p);
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM4_WAVES, 256, 256, LB_GEMM4_WM>),
+                       dim3((p.N + 255) / 256, (p.M + 255) / 256, gz), dim3(64 * LB_GEMM4_WAVES), 0, s, p);
   } else if (kind == GEMM_256x128) {
-    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, 256, 128>), dim3((p.N + 127) / 128, (p.M + 255) / 256, gz),
-                       dim3(256), 0, s, p);
+    constexpr int TW = LB_GEMM_TALL_WAVES;
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, TW, 256, 128, TW / 2>),
+                       dim3((p.N + 127) / 128, (p.M + 255) / 256, gz), dim3(64 * TW), 0, s, p);
   } else if (kind == GEMM_128) {
 #if LB_GEMM_MID
-    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, BM, BN>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),
-                       dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, LB_GEMM_MID_WAVES, BM, BN, LB_GEMM_MID_WM>),
+                       dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz), dim3(64 * LB_GEMM_MID_WAVES), 0, s, p);
 #else
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, BM, BN, BK>), dim3((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, gz),
                        dim3(256), 0, s, p);

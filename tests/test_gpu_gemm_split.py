@@ -26,6 +26,7 @@ SPLIT = [
     ('int4', 64, 1536, 2048, 64, 32, True, 4),    # rank-32 correction delta and bias
     ('int8', 65, 192, 1152, 64, 0, False, 2),     # grouped int8
     ('int4', 256, 4096, 4096, 128, 0, True, 4),   # 128 x 128 tiles split (64 tiles, 64 k steps)
+    ('int4', 512, 4096, 2048, 128, 0, True, 2),   # 128 tiles: two slices fill the CUs
 ]
 
 

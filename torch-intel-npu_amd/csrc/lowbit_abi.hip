@@ -186,7 +186,13 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM_SPLIT_MAX 4     // K slices at most
 #endif
 #ifndef LB_GEMM_SPLIT128_BELOW
-#define LB_GEMM_SPLIT128_BELOW 128  // 128 x 128 grids below this many tiles may split along K
+#define LB_GEMM_SPLIT128_BELOW 160  // 128 x 128 grids below this many tiles may split along K
+#endif
+#ifndef LB_GEMM_SPLIT128_TARGET
+#define LB_GEMM_SPLIT128_TARGET 256  // workgroups a split 128 x 128 grid aims at (0: as many slices as allowed)
+#endif
+#ifndef LB_GEMM_SMALL4
+#define LB_GEMM_SMALL4 1  // 64 x 64 tiles over k steps of 64: 1 gemm4_kernel, 0 gemm2_kernel
 #endif
 #ifndef LB_GEMM_SPLIT_LONG_STEPS
 #define LB_GEMM_SPLIT_LONG_STEPS 16  // k steps per slice of a split 128 x 128 grid at least
@@ -238,7 +244,9 @@ GemmShape gemm_shape(int64_t M, int64_t N, int64_t K, int64_t slices, bool allow
              big * s128 >= LB_GEMM_BIG_MIN) {
     gs.kind = GEMM_128;
     bk = LB_GEMM_BK;
-    s = s128;
+    s = LB_GEMM_SPLIT128_TARGET > 0
+            ? std::max<int64_t>(2, std::min<int64_t>(s128, (LB_GEMM_SPLIT128_TARGET + big - 1) / big))
+            : s128;
   } else {
     gs.kind = bk == 64 ? GEMM_64 : GEMM_64_K32;
     if (can_split && small < LB_GEMM_SPLIT_WGS)
@@ -578,8 +586,13 @@ void launch_gemm_t(const LinearParams &p, hipStream_t s) {
                        dim3(256), 0, s, p);
 #endif
   } else if (kind == GEMM_64) {
+#if LB_GEMM_SMALL4
+    hipLaunchKernelGGL((gemm4_kernel<FMT, SCALED, 4, 64, 64, 2>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
+                       0, s, p);
+#else
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 64>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
                        0, s, p);
+#endif
   } else {
     hipLaunchKernelGGL((gemm2_kernel<FMT, SCALED, 64, 64, 32>), dim3((p.N + 63) / 64, (p.M + 63) / 64, gz), dim3(256),
                        0, s, p);

@@ -36,7 +36,7 @@ namespace lb {
 #define LB_GEMM4_ADMA 1  // activations straight from memory to LDS (buffer_load ... lds)
 #endif
 #ifndef LB_GEMM4_SCHED_VALU
-#define LB_GEMM4_SCHED_VALU 0  // VALU instructions after each MFMA (0: 8 with eight waves, 4 with four)
+#define LB_GEMM4_SCHED_VALU 0  // VALU instructions after each MFMA (0: by block size, below)
 #endif
 #ifndef LB_GEMM4_SCHED_DSR
 #define LB_GEMM4_SCHED_DSR 1
@@ -288,7 +288,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   constexpr int A_PER = BM * (BK / 8) / NT;         // A chunks per thread per step
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK;  // halves per operand per stage
   constexpr int kOutOfRange = (int)0x80000000u;
-  constexpr int SCHED_VALU = LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (WAVES >= 8 ? 8 : 4);
+  // VALU instructions placed after each MFMA: blocks of 8+ MFMA tiles spread the decode thinly,
+  // smaller blocks (fewer MFMAs per substep) take it in larger shares.
+  constexpr int SCHED_VALU =
+      LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (TM * TN >= 8 ? (WAVES >= 8 ? 8 : 4) : 16);
   static_assert((WAVES == 4 || WAVES == 8 || WAVES == 16) && WAVES % WM == 0 && TM >= 1 && TN >= 1 && B_PER >= 1 &&
                     A_PER >= 1 && BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0 && (CB == 16 || BITS == 4),
                 "tile constants");

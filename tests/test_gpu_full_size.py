@@ -11,7 +11,8 @@ size, plus the oracle on row slices.
   arithmetic does not depend on which tile, wave or workgroup computes it.
 - Oracle: the restated reference (rel-L2 <= 1e-3 and its rounding-budget gate) on row slices.
 Shapes: config 5 (Llama-3-8B head 128256x4096 INT4 g128 at M = 1 and 8; 1024x14336x4096 prefill),
-config 3 (NF4 g64 2560x960 at M = 2048) and config 2 (lm_head 49152x576 g64 at M = 4 and 16).
+config 3 (NF4 g64 2560x960 at M = 2048), config 2 (lm_head 49152x576 g64 at M = 4 and 16) and
+the W8 GEMV at M = 1 on the Llama head (per-row int8) and a grouped int8 32768x2048.
 """
 import numpy as np
 import pytest
@@ -24,7 +25,8 @@ from test_gpu_linear import check
 pytestmark = pytest.mark.gpu
 
 FULL = [('int4', 1, 128256, 4096, 128), ('int4', 8, 128256, 4096, 128), ('int4', 1024, 14336, 4096, 128),
-        ('nf4', 2048, 2560, 960, 64), ('int4', 4, 49152, 576, 64), ('int4', 16, 49152, 576, 64)]
+        ('nf4', 2048, 2560, 960, 64), ('int4', 4, 49152, 576, 64), ('int4', 16, 49152, 576, 64),
+        ('int8', 1, 128256, 4096, 4096), ('int8', 1, 32768, 2048, 64)]
 
 
 def packed_random(rng, fmt, n, k, group):

@@ -497,7 +497,8 @@ lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
   p.kv_heads = (int)a->kv_heads;
   p.capacity = (int)a->capacity;
   p.scale = a->scale;
-  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)a->heads), dim3(256), (size_t)a->capacity * sizeof(float),
+  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)a->heads, kAttnDimSlices), dim3(256),
+                     (size_t)a->capacity * sizeof(float),
                      static_cast<hipStream_t>(stream), p);
   return launch_status("lb_decode_attention");
 }

@@ -446,24 +446,32 @@ struct AttnParams {
 };
 
 constexpr int kHeadDim = 64;
-constexpr int kAttnParts = 32;   // position partitions of the P.V product (8 threads per V row)
+constexpr int kAttnDimSlices = 4;                       // workgroups per query head (grid y)
+constexpr int kSliceDims = kHeadDim / kAttnDimSlices;   // output dims per workgroup
+constexpr int kSliceBlocks = kSliceDims / 8;            // 16-byte V blocks per slot and workgroup
+constexpr int kAttnParts = 256 / kSliceBlocks;          // position partitions of the P.V product
 constexpr int kScoreSlots = 2;   // K rows per thread per round: 512 slots per round
-constexpr int kValueSlots = 12;  // V rows per thread per round: 384 slots per round
+constexpr int kValueSlots = 3;   // V blocks per thread per round: 384 slots per round
 
-// One workgroup per query head.  The first query head of each KV group writes the rotated key
-// and the value into the cache; every workgroup uses its own copy of that new row, so no
-// workgroup reads a cache slot another one writes.  The cached K and V rows of the first
-// round (slots < 512) are loaded before anything else, so a step costs one memory round trip
-// plus the on-chip softmax; longer caches loop over further rounds.
+// kAttnDimSlices workgroups per query head, each owning kSliceDims of the output dims.  Every
+// workgroup of a head computes the same scores and softmax (same data, same order, so the same
+// probabilities bit for bit) and P.V for its own dims only, so it reads all cached K rows but a
+// quarter of each V row, and no partial result crosses workgroups.  The first slice of the first
+// query head of each KV group writes the rotated key and the value into the cache; every
+// workgroup uses its own copy of that new row, so no workgroup reads a cache slot another one
+// writes.  The cached K and V rows of the first round (slots < 512 and < 384) are loaded before
+// anything else, so a step costs one memory round trip plus the on-chip softmax; longer caches
+// loop over further rounds.
 __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   extern __shared__ float sc[];  // [capacity] scores, then probabilities
   __shared__ __align__(16) f16 qs[kHeadDim], kn[kHeadDim], vn[kHeadDim];
   __shared__ float wred[4];
-  __shared__ float pv[kAttnParts * kHeadDim];
+  __shared__ float pv[4 * kSliceDims];
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar: buffer bases below are per wave
   const int h = blockIdx.x;
+  const int d0 = (int)blockIdx.y * kSliceDims;  // first output dim of this workgroup
   const int group = p.heads / p.kv_heads;
   const int kvh = h / group;
   const int pos = (int)p.position[0];
@@ -486,7 +494,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
   const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(p.keys + head_base, (size_t)pos * kHeadDim * 2);
   const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(p.values + head_base, (size_t)pos * kHeadDim * 2);
-  const int blk = t & 7, part = t >> 3;
+  const int blk = t % kSliceBlocks, part = t / kSliceBlocks;
   u4 kreg[kScoreSlots][kHeadDim / 8];
   u4 vreg[kValueSlots];
   // Straight-line loads (a load under a branch is waited for at the branch's end); lanes
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
     for (int i = 0; i < kValueSlots; ++i) {
       const int s = base + part + kAttnParts * i;
       vreg[i] = __builtin_bit_cast(
-          u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, s < pos ? (s * kHeadDim + 8 * blk) * 2 : kOutOfRange, 0, 0));
+          u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, s < pos ? (s * kHeadDim + d0 + 8 * blk) * 2 : kOutOfRange, 0, 0));
     }
   };
   load_keys(0);
@@ -522,7 +530,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
     if (wave == 0) qs[d] = r; else kn[d] = r;
   }
   __syncthreads();
-  if (h % group == 0 && t < 2 * kHeadDim) {
+  if (h % group == 0 && blockIdx.y == 0 && t < 2 * kHeadDim) {
     const int d = t & 63;
     f16 *dst = (t < kHeadDim ? p.keys : p.values) + head_base + (size_t)pos * kHeadDim + d;
     *dst = t < kHeadDim ? kn[d] : vn[d];
@@ -573,7 +581,9 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   for (int s = t; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
   __syncthreads();
 
-  // out = fp16(P . V): thread (blk, part) sums 8 dims over slots part, part + 32, ...
+  // out = fp16(P . V) over this workgroup's dims: thread (blk, part) sums 8 dims over slots part,
+  // part + kAttnParts, ...; then the parts of a wave (lane bits above blk) by butterfly, the four
+  // waves through LDS, in a fixed order.
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int base = 0; base <= pos; base += kAttnParts * kValueSlots) {
     if (base > 0) load_values(base);
@@ -582,19 +592,24 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
       const int s = base + part + kAttnParts * i;
       if (base + kAttnParts * i > pos) break;  // wave-uniform
       asm volatile("" : "+v"(vreg[i]));
-      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
+      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + d0 + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
       const float pr = s <= pos ? sc[min(s, pos)] : 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pv[part * kHeadDim + blk * 8 + e] = o[e];
+  for (int off = kSliceBlocks; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off, 64);
+  if (lane < kSliceBlocks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[wave * kSliceDims + lane * 8 + e] = o[e];
+  }
   __syncthreads();
-  if (t < kHeadDim) {
-    float r = 0.0f;
-    for (int q = 0; q < kAttnParts; ++q) r += pv[q * kHeadDim + t];
-    p.out[h * kHeadDim + t] = (f16)r;
+  if (t < kSliceDims) {
+    const float r = ((pv[t] + pv[kSliceDims + t]) + pv[2 * kSliceDims + t]) + pv[3 * kSliceDims + t];
+    p.out[h * kHeadDim + d0 + t] = (f16)r;
   }
 }
 

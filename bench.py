@@ -217,7 +217,7 @@ def sweep(device, stream, quick):
         packed = make_weight(fmt, n, k, g, 300 + i)
         bytes_w = algorithmic_bytes(fmt, 0, n, k, g)
         lin = Linear(packed, m, copies_for(bytes_w, cap=32), device, 400 + i)
-        us = kernel_time_us(lin, stream, replays=4)
+        us = float(np.median([kernel_time_us(lin, stream, replays=4) for _ in range(3)]))  # median of 3 timed graphs
         row = dict(fmt=fmt, M=m, N=n, K=k, group=g, shape=name, us=round(us, 2),
                    gbs=round(lin.bytes / us / 1e3, 1), tflops=round(lin.flops / us / 1e6, 2))
         row['hbm_frac' if m <= 32 else 'mfma_frac'] = round(

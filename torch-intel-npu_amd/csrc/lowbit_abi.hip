@@ -21,6 +21,9 @@ using namespace lb::abi;
 
 namespace {
 
+#ifndef LB_GEMM_FROM_M
+#define LB_GEMM_FROM_M 17  // from this many rows, calls with K >= N that no streaming GEMV takes run
+#endif                     // on the split-K GEMM (measured faster there up to 32 rows; K < N stays on gemv_kernel)
 enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4, PATH_TILE = 5 };
 enum Variant { VAR_PLAIN = 0, VAR_COMPACT = 1, VAR_W8A8 = 2 };
 constexpr int kCompactMaxGroups = 32;
@@ -365,7 +368,7 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     pl.path = PATH_STREAM;
   } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && tile_rows_eligible(a)) {
     pl.path = PATH_TILE;
-  } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) {
+  } else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M < LB_GEMM_FROM_M || (a->M <= kGemvMaxM && a->K < a->N)) {
     pl.path = PATH_GEMV;
   } else {
     pl.path = PATH_GEMM;

@@ -338,7 +338,7 @@ def profile_kernel(device, stream, shape=None):
                           algorithmic_bytes=lin.bytes, copy_bytes=src.numel())), flush=True)
 
 
-GEMM_PROFILE_SHAPES = [('int4', 1024, 14336, 4096, 128), ('nf4', 512, 2560, 960, 64)]
+GEMM_PROFILE_SHAPES = [('int4', 1024, 14336, 4096, 128), ('nf4', 512, 2560, 960, 64), ('int4', 512, 14336, 4096, 128)]
 
 
 def profile_gemm(device, stream):

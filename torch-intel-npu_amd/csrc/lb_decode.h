@@ -446,12 +446,16 @@ struct AttnParams {
 };
 
 constexpr int kHeadDim = 64;
-constexpr int kAttnDimSlices = 4;                       // workgroups per query head (grid y)
+#ifndef LB_ATTN_SLICES
+#define LB_ATTN_SLICES 4
+#endif
+constexpr int kAttnDimSlices = LB_ATTN_SLICES;          // workgroups per query head (grid y)
 constexpr int kSliceDims = kHeadDim / kAttnDimSlices;   // output dims per workgroup
 constexpr int kSliceBlocks = kSliceDims / 8;            // 16-byte V blocks per slot and workgroup
 constexpr int kAttnParts = 256 / kSliceBlocks;          // position partitions of the P.V product
 constexpr int kScoreSlots = 2;   // K rows per thread per round: 512 slots per round
-constexpr int kValueSlots = 3;   // V blocks per thread per round: 384 slots per round
+constexpr int kValueSlots = (384 + kAttnParts - 1) / kAttnParts;  // V blocks per thread per round (>= 384 slots)
+static_assert(kSliceBlocks >= 1 && kHeadDim % kAttnDimSlices == 0, "attention slices");
 
 // kAttnDimSlices workgroups per query head, each owning kSliceDims of the output dims.  Every
 // workgroup of a head computes the same scores and softmax (same data, same order, so the same

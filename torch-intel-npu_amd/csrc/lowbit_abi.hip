@@ -171,7 +171,7 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM4_MIN_TILES 160  // 256 x 256 tiles from this many workgroups
 #endif
 #ifndef LB_GEMM_TALL_MIN
-#define LB_GEMM_TALL_MIN 160  // 256 x 128 tiles (four waves) from this many workgroups ...
+#define LB_GEMM_TALL_MIN 160  // 256 x 128 tiles (LB_GEMM_TALL_WAVES waves) from this many workgroups ...
 #endif
 #ifndef LB_GEMM_TALL_WAVES
 #define LB_GEMM_TALL_WAVES 8  // 256 x 128 tiles: 8 waves of 64 x 64, or 4 of 128 x 64
@@ -180,7 +180,7 @@ GemvShape gemv_shape(int fmt, int64_t M, int64_t N, int64_t K, bool allow_split)
 #define LB_GEMM_TALL_MAX 256  // ... up to this many (one workgroup per CU)
 #endif
 #ifndef LB_GEMM_MID
-#define LB_GEMM_MID 1  // 128 x 128 tiles: 1 gemm4_kernel with four waves, 0 gemm2_kernel
+#define LB_GEMM_MID 1  // 128 x 128 tiles: 1 gemm4_kernel (LB_GEMM_MID_WAVES waves), 0 gemm2_kernel
 #endif
 #ifndef LB_GEMM_SPLIT_WGS
 #define LB_GEMM_SPLIT_WGS 256   // split K while the tile grid has fewer workgroups than this
@@ -213,12 +213,12 @@ struct GemmShape {
 
 // Tile kernel and K split of a prefill GEMM:
 //   - 256 x 256 tiles (gemm4_kernel) when they nearly fill the CUs;
-//   - else 256 x 128 tiles (gemm4_kernel with four waves) when they fill the CUs in one round
+//   - else 256 x 128 tiles (gemm4_kernel, eight waves of 64 x 64) when they fill the CUs in one round
 //     (LB_GEMM_TALL_MIN to LB_GEMM_TALL_MAX workgroups) and the rows past M add at most an eighth;
-//   - else 128 x 128 tiles (gemm4_kernel with four waves) from LB_GEMM_BIG_MIN workgroups on;
+//   - else 128 x 128 tiles (gemm4_kernel, eight waves of 64 x 32) from LB_GEMM_BIG_MIN workgroups on;
 //   - else, for a small 128 x 128 grid (< LB_GEMM_SPLIT128_BELOW tiles) over long rows, 128 x 128
-//     tiles split along K into slices of at least LB_GEMM_SPLIT_LONG_STEPS k steps, when the
-//     slices fill the CUs;
+//     tiles split along K into slices of at least LB_GEMM_SPLIT_LONG_STEPS k steps, as few as give
+//     LB_GEMM_SPLIT128_TARGET workgroups, when the slices fill the CUs;
 //   - else 64 x 64 tiles (k steps of 64 where K allows, else 32), split along K when the grid has
 //     fewer than LB_GEMM_SPLIT_WGS workgroups, into slices of at least LB_GEMM_SPLIT_MIN_STEPS
 //     k steps, aiming at two workgroups per CU.

@@ -117,6 +117,23 @@ def test_workspace_sizes():
     assert status == 0 and size == 0
 
 
+def test_prefill_tile_plan_workspace():
+    """The planner's tile choice shows in the workspace: split grids need fp32 partials."""
+    big = dict(x=0x10000000, y=0x20000000, scales=0x30000000, codes=0x40000000)
+    # 128 x 128 grid of 128 tiles over 32 k steps: two slices give 256 workgroups
+    status, size, _ = workspace(args(M=512, N=4096, K=2048, group_size=128, ldx=2048, ldy=4096, **big))
+    assert status == 0 and size == 2 * 512 * 4096 * 4
+    # 64 tiles over 64 k steps: four slices
+    status, size, _ = workspace(args(M=256, N=4096, K=4096, group_size=128, ldx=4096, ldy=4096, **big))
+    assert status == 0 and size == 4 * 256 * 4096 * 4
+    # 224 tiles of 256 x 128 fill the CUs in one round: no split
+    status, size, _ = workspace(args(M=512, N=14336, K=4096, group_size=128, ldx=4096, ldy=14336, **big))
+    assert status == 0 and size == 0
+    # 168 tiles of 256 x 256: no split
+    status, size, _ = workspace(args(M=768, N=14336, K=4096, group_size=128, ldx=4096, ldy=14336, **big))
+    assert status == 0 and size == 0
+
+
 def test_missing_workspace_is_rejected_by_lb_linear():
     a = args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128, x=0x1000000, y=0x2000000,
              scales=0x3000000, codes=0x4000000, flags=lowbit_hip.FLAG_FORCE_GEMV)

@@ -24,9 +24,11 @@ namespace lb {
 #ifndef LB_GEMM_IGLP
 #define LB_GEMM_IGLP 0
 #endif
-// LDS swizzle of the 256 x 256 GEMM: row r stores chunk c at c ^ LB_G4_SWZ(r).
+// LDS swizzle of gemm4_kernel: row r stores chunk c at c ^ LB_G4_SWZ(r).  Rows are 128 bytes, so
+// two consecutive rows cover the 64 banks once; with the shift of 1 the 16 rows a 16-byte access
+// serves together land on distinct (row parity, chunk) bank groups.
 #ifndef LB_GEMM4_SWZ_SHIFT
-#define LB_GEMM4_SWZ_SHIFT 0
+#define LB_GEMM4_SWZ_SHIFT 1  // chunk c ^ ((r >> 1) & 7): conflict-free 16-row groups over 64 LDS banks
 #endif
 #define LB_G4_SWZ(r) (((r) >> LB_GEMM4_SWZ_SHIFT) & 7)
 #ifndef LB_GEMM4_SCHED
@@ -259,7 +261,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 // (TM x TN), whose fp32 accumulators live in AGPRs.  Per K step of 64 and 16-deep substep, a wave
 // reads TM A and TN B fragments for its TM TN MFMAs.  LDS holds two stages of A (fp16 activations)
 // and B (decoded fp16 weights), BM (BN) rows x 64 halves each, without padding: the 16-byte chunk c
-// of row r is stored at chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.
+// of row r is stored at chunk c ^ LB_G4_SWZ(r), so the rows of a fragment read hit distinct banks.
 // The next step's activations go straight from memory to the other LDS stage (buffer_load ...
 // lds; the two stages are separate arrays so the compiler sees no alias with the stage being
 // read), issued at the start of the step and complete before its closing barrier; the packed

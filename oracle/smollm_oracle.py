@@ -16,10 +16,14 @@ Every fp16 rounding point of the reference is kept:
   logits     fp16(fp32 RMS) * gamma, then F.linear with the tied fp16 embedding (io :57-61)
 
 The decode step is the KV-cached row of the same computation: at position p it reads
-keys/values 0..p and uses the RoPE row p.  Pinning: tests/test_smollm_cpu.py checks
-the decode rows against the full-sequence forward, zero-factor corrections against no
-correction (bitwise), the correction delta at one projection, the 4-bit trace against
-F.linear(norm1, dequantize()), and the tied logits against F.rms_norm.
+keys/values 0..p and uses the RoPE row p.  Pinning (tests/test_smollm_cpu.py): the attention
+outputs and logits of a full forward agree with transformers' LlamaForCausalLM (fp32, eager
+attention, built offline from a local LlamaConfig and loaded with this oracle's effective
+weights) within 5e-3 rel-L2, while interleaved-pair RoPE, the h % 3 head mapping, a missing
+causal mask and theta 1e5 each miss it by more than 0.1; the decode rows reproduce the
+full-sequence forward; zero-factor corrections are bitwise no-ops; the correction delta at
+one projection is exact; the 4-bit trace equals F.linear(norm1, dequantize()); the tied
+logits equal F.rms_norm + F.linear.
 """
 import numpy as np
 import torch

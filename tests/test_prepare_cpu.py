@@ -187,3 +187,106 @@ def test_quantized_linear_option_surface():
     large = PackedWeight((1, 256), 'int8', 256, codes.tobytes(), np.float16(512).tobytes())
     with pytest.raises(ValueError):
         QuantizedLinear(large, activation_scale=1 / 128)
+
+
+# --- the product quantizer against the oracle's restatement (reference torch_npu_lowbit.py:78-105) ---------
+
+def _oracle_quantize(weight, fmt, group):
+    from oracle import lowbit_oracle as lo
+    return lo.quantize(weight.float().numpy(), fmt, group)
+
+
+def test_quantize_weight_matches_oracle_on_ties():
+    """rint's half-to-even ties (int4 / int8) and searchsorted(side='left') at the NF4 midpoints."""
+    from oracle import lowbit_oracle as lo
+    ties = torch.tensor([[7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5]])
+    q = quantize_weight(ties, format='int4')
+    assert (q.data, q.scales) == _oracle_quantize(ties, 'int4', None)
+    assert lo.unpack('int4', q.data, 8).tolist() == [7, 0, 2, 2, 0, -2, -2, 4]
+    ties8 = torch.tensor([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 126.5, -125.5]])
+    q = quantize_weight(ties8, format='int8')
+    assert (q.data, q.scales) == _oracle_quantize(ties8, 'int8', None)
+    assert np.frombuffer(q.data, np.int8).tolist() == [127, 0, 2, 2, 0, -2, 126, -126]
+    mids = ((lo.NF4_F32[:-1] + lo.NF4_F32[1:]) / np.float32(2)).astype(np.float32)
+    values = np.concatenate([[1.0], mids, np.nextafter(mids, np.float32(2)), -np.nextafter(mids, np.float32(-2))])
+    w = torch.from_numpy(values.astype(np.float32)[None, :])
+    q = quantize_weight(w, format='nf4')
+    assert (q.data, q.scales) == _oracle_quantize(w, 'nf4', None)
+    codes = lo.unpack('nf4', q.data, w.numel())
+    assert codes[1:16].tolist() == list(range(15)) and codes[16:31].tolist() == list(range(1, 16))
+
+
+@pytest.mark.parametrize('fmt', ['int4', 'nf4', 'int8'])
+def test_quantize_weight_matches_oracle_random(fmt):
+    """Seeded sweep over shapes, group sizes, dtypes and magnitudes (tiny, zero and odd-count rows)."""
+    g = torch.Generator().manual_seed({'int4': 41, 'nf4': 42, 'int8': 43}[fmt])
+    for n, k, groups in ((3, 64, (None, 1, 8, 32, 64)), (7, 96, (None, 3, 32, 48)), (1, 5, (None, 1, 5)),
+                         (16, 576, (None, 32, 64)), (5, 1536, (None, 128))):
+        for std in (0.02, 1.0, 1e-6):
+            for dtype in (torch.float32, torch.float16):
+                w = (torch.randn(n, k, generator=g) * std).to(dtype)
+                w[0, : k // 2] = 0
+                if n > 2:
+                    w[2] = 0
+                for group in groups:
+                    q = quantize_weight(w, format=fmt, group_size=group)
+                    data, scales = _oracle_quantize(w, fmt, group)
+                    assert q.data == data, (fmt, n, k, group, std, dtype)
+                    assert q.scales == scales, (fmt, n, k, group, std, dtype)
+
+
+# --- GPTQ against a plain OBS column loop (reference torch_npu_lowbit.py:108-152) --------------------------
+
+def _obs_codes(weight, inputs, scales, order_descending=True):
+    """Textbook optimal-brain-surgeon quantization: for each column in activation order,
+    quantize it, spread its error over the remaining columns through the explicit inverse
+    Hessian, then eliminate the column from that inverse (Schur complement).  fp64, no
+    Cholesky factor, no column blocks."""
+    x = inputs.double().numpy()
+    k = x.shape[1]
+    h = x.T @ x / x.shape[0]
+    energy = np.diag(h).copy()
+    order = np.argsort(-energy if order_descending else energy, kind='stable')
+    h = h[np.ix_(order, order)]
+    dead = energy[order] == 0
+    h[dead, dead] = 1.0
+    h += 0.01 * max(np.diag(h).mean(), 1e-20) * np.eye(k)
+    hinv = np.linalg.inv(h)
+    w = weight.double().numpy()[:, order].copy()
+    codes = np.zeros(w.shape, np.int64)
+    for j in range(k):
+        q = np.clip(np.round(w[:, j] / scales), -127, 127)
+        codes[:, j] = q
+        d = hinv[j, j]
+        err = (w[:, j] - q * scales) / d
+        w[:, j + 1:] -= np.outer(err, hinv[j, j + 1:])
+        hinv = hinv - np.outer(hinv[:, j], hinv[j, :]) / d
+    out = np.empty_like(codes)
+    out[:, order] = codes
+    return out
+
+
+def test_calibration_matches_plain_obs_loop():
+    g = torch.Generator().manual_seed(73)
+    n, k = 6, 300                     # three 128-column blocks in the product
+    basis = torch.randn(24, k, generator=g)
+    inputs = (torch.randn(400, 24, generator=g) @ basis + 0.1 * torch.randn(400, k, generator=g)).float()
+    inputs[:, 17] = 0                 # a dead column
+    weight = torch.randn(n, k, generator=g) * 0.05
+    plain = quantize_weight(weight, format='int8')
+    scales = scales_of(plain)
+    tuned = calibrate_int8(weight, inputs)
+    proposed = _obs_codes(weight, inputs, scales)
+    # the product keeps a row's OBS codes exactly where they lower that row's loss, else the plain codes
+    x = inputs.double().numpy()
+    target = x @ weight.double().numpy().T
+
+    def row_loss(c):
+        return (((x @ c.astype(np.float64).T) * scales[None] - target) ** 2).sum(0)
+
+    better = row_loss(proposed) < row_loss(codes_of(plain))
+    assert better.any()
+    expected = np.where(better[:, None], proposed, codes_of(plain))
+    np.testing.assert_array_equal(codes_of(tuned), expected)
+    # a wrong activation order changes the codes: the check is sensitive to it
+    assert (_obs_codes(weight, inputs, scales, order_descending=False) != proposed).any()

@@ -179,3 +179,116 @@ def test_checkpoint_round_trip():
                   str(path / 'model.safetensors'))
         with pytest.raises(ValueError):
             FrozenSmolIO.from_checkpoint(path)
+
+
+# --- independent pin of the oracle's attention half against a textbook Llama ------------------------------
+# transformers' LlamaForCausalLM (built offline from a local LlamaConfig, eager attention, fp32) is the
+# textbook form of the reference's decoder: rotate-half RoPE from theta (torch_npu_smollm.py:113-116,176),
+# GQA by repeat_interleave (:178), scaled causal scores and softmax (:179-182), RMSNorm and the SiLU MLP.
+# Loaded with the oracle's own effective weights (exact q*s plus U.V), it must agree with the staged
+# oracle to fp16-staging accuracy, and each plausible wrong convention of the oracle must not.
+
+def _hf_case(seed=11, layers=2, vocab=256, length=16):
+    """Seeded W8 + rank-8 layers with peaked attention (q/k std 0.08), non-unit norms and 16 ids."""
+    g = torch.Generator().manual_seed(seed)
+    specs = []
+    for _ in range(layers):
+        w = {n: (torch.randn(_SHAPES[n], generator=g) * (.08 if n.split('.')[1] in ('q_proj', 'k_proj') else .03)).half()
+             for n in so.PROJECTIONS}
+        for n in ('input_layernorm.weight', 'post_attention_layernorm.weight'):
+            w[n] = (1 + torch.randn(576, generator=g) * .1).half()
+        packed = {n: quantize_weight(w[n], format='int8') for n in so.PROJECTIONS}
+        corr = {n: ((torch.randn(8, _SHAPES[n][1], generator=g) * .02).half(),
+                    (torch.randn(_SHAPES[n][0], 8, generator=g) * .02).half())
+                for n in ('self_attn.o_proj.weight', 'mlp.down_proj.weight')}
+        specs.append((w, {n: (q.format, q.shape, q.group_size, q.data, q.scales) for n, q in packed.items()}, corr))
+    emb = (torch.randn(vocab, 576, generator=g) * .05).half()
+    norm = (1 + torch.randn(576, generator=g) * .1).half()
+    ids = torch.randint(0, vocab, (1, length), generator=g)
+    return specs, emb, norm, ids
+
+
+def _hf_reference(specs, emb, norm, ids, theta):
+    """(per-layer attention outputs [S,576], logits [S,V]) of transformers' Llama in fp32."""
+    transformers = pytest.importorskip('transformers')
+    from oracle import lowbit_oracle as lo
+    cfg = transformers.LlamaConfig(
+        vocab_size=emb.shape[0], hidden_size=576, intermediate_size=1536, num_hidden_layers=len(specs),
+        num_attention_heads=9, num_key_value_heads=3, head_dim=64, rms_norm_eps=1e-5, rope_theta=theta,
+        tie_word_embeddings=True, max_position_embeddings=64, attention_bias=False, mlp_bias=False,
+        hidden_act='silu', attn_implementation='eager')
+    model = transformers.LlamaForCausalLM(cfg).eval()
+    state = {'model.embed_tokens.weight': emb.float(), 'lm_head.weight': emb.float(), 'model.norm.weight': norm.float()}
+    for i, (w, packed, corr) in enumerate(specs):
+        for n in so.PROJECTIONS:
+            effective = torch.from_numpy(lo.exact_weight(*packed[n]))
+            if n in corr:
+                down, up = corr[n]
+                effective = effective + up.double() @ down.double()
+            state[f'model.layers.{i}.{n}'] = effective.float()
+        for n in ('input_layernorm.weight', 'post_attention_layernorm.weight'):
+            state[f'model.layers.{i}.{n}'] = w[n].float()
+    model.load_state_dict(state, strict=True)
+    attention = []
+    for layer in model.model.layers:
+        layer.self_attn.o_proj.register_forward_pre_hook(lambda _m, args: attention.append(args[0][0].detach()))
+    with torch.no_grad():
+        logits = model(ids).logits[0]
+    return attention, logits
+
+
+def _oracle_run(layer_type, specs, emb, norm, ids, theta):
+    layers = [layer_type(w, packed, corr, theta=theta, capacity=64) for w, packed, corr in specs]
+    model = so.OracleModel(layers, emb, norm)
+    x, attention = model.embed(ids), []
+    for layer in layers:
+        x, trace, _, _ = layer.forward(x)
+        attention.append(trace['attention'][0])
+    return attention, model.logits(x)[0]
+
+
+def _rel(a, b):
+    return float((a.double() - b.double()).norm() / b.double().norm())
+
+
+class _InterleavedRope(so.OracleLayer):
+    """Wrong convention: RoPE on adjacent pairs (2i, 2i+1) instead of rotate-half."""
+
+    @staticmethod
+    def _rotate(v, cos, sin):
+        c, s = cos[..., :32].repeat_interleave(2, -1), sin[..., :32].repeat_interleave(2, -1)
+        rot = torch.stack((-v[..., 1::2], v[..., 0::2]), -1).flatten(-2)
+        return (v * c + rot * s).half()
+
+
+class _TiledHeads(so.OracleLayer):
+    """Wrong GQA mapping: query head h reads KV head h % 3 instead of h // 3."""
+
+    @staticmethod
+    def _attend(q, k, v, mask):
+        k, v = k.repeat(1, 3, 1, 1), v.repeat(1, 3, 1, 1)
+        scores = (q.float() @ k.float().transpose(-1, -2)).half()
+        probs = ((scores * 0.125).half() + mask).float().softmax(-1).half()
+        return (probs.float() @ v.float()).half()
+
+
+class _NoMask(so.OracleLayer):
+    """Wrong masking: every position attends to the whole sequence."""
+
+    @staticmethod
+    def _attend(q, k, v, mask):
+        return so.OracleLayer._attend(q, k, v, torch.zeros_like(mask))
+
+
+def test_oracle_attention_matches_transformers_llama():
+    specs, emb, norm, ids = _hf_case()
+    theta = 10000.0
+    want_att, want_logits = _hf_reference(specs, emb, norm, ids, theta)
+    att, logits = _oracle_run(so.OracleLayer, specs, emb, norm, ids, theta)
+    errs = [_rel(a, b) for a, b in zip(att, want_att)] + [_rel(logits, want_logits)]
+    assert max(errs) <= 5e-3, errs
+    # Each wrong convention is far outside that tolerance, at the first layer's attention already.
+    for layer_type, t in ((_InterleavedRope, theta), (_TiledHeads, theta), (_NoMask, theta), (so.OracleLayer, 1e5)):
+        bad_att, bad_logits = _oracle_run(layer_type, specs, emb, norm, ids, t)
+        assert _rel(bad_att[0], want_att[0]) > 0.1, (layer_type.__name__, t)
+        assert _rel(bad_logits, want_logits) > 0.1, (layer_type.__name__, t)

@@ -19,6 +19,7 @@ from torch_npu_smollm_io import FrozenSmolIO
 PROJECTIONS = ('self_attn.q_proj.weight', 'self_attn.k_proj.weight', 'self_attn.v_proj.weight',
                'self_attn.o_proj.weight', 'mlp.gate_proj.weight', 'mlp.up_proj.weight', 'mlp.down_proj.weight')
 VOCAB = 49152
+QK = ('self_attn.q_proj.weight', 'self_attn.k_proj.weight')
 
 
 def config(theta=10000.0, layers=30):
@@ -28,16 +29,20 @@ def config(theta=10000.0, layers=30):
                 tie_word_embeddings=True, vocab_size=VOCAB)
 
 
-def random_weights(seed=0, layers=30, rank=32, std=0.02, corr_std=0.01):
-    """(per-layer weight dicts, embedding fp32 [V,576], norm [576], per-layer {name: (V, U)} or None)."""
+def random_weights(seed=0, layers=30, rank=32, std=0.02, corr_std=0.01, qk_std=None, embed_std=None):
+    """(per-layer weight dicts, embedding fp32 [V,576], norm [576], per-layer {name: (V, U)} or None).
+
+    qk_std / embed_std (default: std) set the q/k projections' and the embedding's deviation."""
     g = torch.Generator().manual_seed(seed)
+    qk_std = std if qk_std is None else qk_std
+    embed_std = std if embed_std is None else embed_std
     layer_weights = []
     for _ in range(layers):
-        w = {name: torch.randn(_SHAPES[name], generator=g) * std for name in PROJECTIONS}
+        w = {name: torch.randn(_SHAPES[name], generator=g) * (qk_std if name in QK else std) for name in PROJECTIONS}
         w['input_layernorm.weight'] = torch.ones(576)
         w['post_attention_layernorm.weight'] = torch.ones(576)
         layer_weights.append(w)
-    embedding = torch.randn(VOCAB, 576, generator=g) * std
+    embedding = torch.randn(VOCAB, 576, generator=g) * embed_std
     norm = torch.ones(576)
     factors = None
     if rank:
@@ -53,10 +58,11 @@ def random_weights(seed=0, layers=30, rank=32, std=0.02, corr_std=0.01):
     return layer_weights, embedding, norm, factors
 
 
-def build(seed=0, layers=30, rank=32, theta=10000.0, capacity=384, mode='w8a16'):
-    """(FrozenSmolStack, FrozenSmolIO, packed per layer, corrections per layer) for the config."""
+def build(seed=0, layers=30, rank=32, theta=10000.0, capacity=384, mode='w8a16', **scales):
+    """(FrozenSmolStack, FrozenSmolIO, packed per layer, corrections per layer) for the config.
+    `scales` (std, qk_std, embed_std, corr_std) go to random_weights."""
     cfg = config(theta, layers)
-    layer_weights, embedding, norm, factors = random_weights(seed, layers, rank)
+    layer_weights, embedding, norm, factors = random_weights(seed, layers, rank, **scales)
     stack_layers, packed_all, corr_all = [], [], []
     for i, w in enumerate(layer_weights):
         fmt = {'w8a16': 'int8', 'w4a16': 'int4', 'nf4a16': 'nf4'}.get(mode)

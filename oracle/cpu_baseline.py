@@ -2,8 +2,9 @@
 
 Times the reference's CPU path as the reference timed its CPU column
 (torch_npu_lowbit_demo.py:65,71): fp32 torch CPU matmul on pre-dequantized weights,
-fp16 output.  A dequant-inclusive variant adds PackedWeight.dequantize() semantics
-(torch_npu_lowbit.py:67-75) per call.  Protocol (demo :62-71): warmups, then the median
+fp16 output.  A dequant-inclusive variant adds the reference's host dequantization per call:
+the package's PackedWeight.dequantize(), the numpy fp16 restatement of reference
+torch_npu_lowbit.py:67-75 (fp16 codes times fp16 scales, one fp16 rounding).  Protocol (demo :62-71): warmups, then the median
 of interleaved A/B rounds.
 """
 import os
@@ -26,14 +27,17 @@ class CpuPass:
         self.weights = [torch.from_numpy(o.dequantize(fmt, shape, g, data, scales).astype(np.float32))
                         for (_, fmt, shape, g, data, scales) in problems]
         self.inputs = [torch.from_numpy(np.asarray(x, np.float16)).float() for (x, *_) in problems]
+        from torch_npu_lowbit import PackedWeight
+        self.packed = [PackedWeight(tuple(shape), fmt, g, bytes(data), bytes(scales))
+                       for (_, fmt, shape, g, data, scales) in problems]
 
     def run_predequantized(self):
         return [(x @ w.T).half() for x, w in zip(self.inputs, self.weights)]
 
     def run_with_dequant(self):
         out = []
-        for x, (_, fmt, shape, g, data, scales) in zip(self.inputs, self.problems):
-            w = torch.from_numpy(o.dequantize(fmt, shape, g, data, scales).astype(np.float32))
+        for x, packed in zip(self.inputs, self.packed):
+            w = torch.from_numpy(packed.dequantize()).float()
             out.append((x @ w.T).half())
         return out
 

@@ -5,6 +5,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 import lowbit_hip
 
@@ -316,3 +317,53 @@ def test_variant_workspace_sizes():
     # W8A8 on the generic path (K not a multiple of 64) quantizes as it reads: no workspace
     status, size, _ = workspace(args(M=5, **dict(W8, K=96, ldx=96, group_size=96)))
     assert (status, size) == (0, 0)
+
+
+# --- operand checks of the Python binding (before any launch; no GPU needed) ----------------------------
+
+def _operands(**over):
+    n, k, g = 8, 64, 32
+    base = dict(x=torch.zeros(2, k, dtype=torch.float16), codes=torch.zeros(n * k // 2, dtype=torch.uint8),
+                scales=torch.zeros(n, k // g, dtype=torch.float16), format='int4', N=n, K=k, group_size=g,
+                y=torch.zeros(2, n, dtype=torch.float16), bias=torch.zeros(n, dtype=torch.float16),
+                down=torch.zeros(4, k, dtype=torch.float16), up=torch.zeros(n, 4, dtype=torch.float16), rank=4)
+    base.update(over)
+    return base
+
+
+@pytest.mark.parametrize('over, needle', [
+    (dict(codes=torch.zeros(8 * 64 // 2, dtype=torch.float32)), 'codes'),
+    (dict(codes=torch.zeros(8 * 64 // 2 - 1, dtype=torch.uint8)), 'codes'),
+    (dict(codes=torch.zeros(8 * 64, dtype=torch.uint8)[::2]), 'codes'),
+    (dict(scales=torch.zeros(8, 2, dtype=torch.float32)), 'scales'),
+    (dict(scales=torch.zeros(2, 8, dtype=torch.float16).t()), 'scales'),
+    (dict(scales=torch.zeros(8, 1, dtype=torch.float16)), 'scales'),
+    (dict(scales=None), 'scales'),
+    (dict(bias=torch.zeros(8, dtype=torch.float32)), 'bias'),
+    (dict(bias=torch.zeros(16, dtype=torch.float16)[::2]), 'bias'),
+    (dict(down=torch.zeros(4, 32, dtype=torch.float16)), 'down'),
+    (dict(up=torch.zeros(8, 2, dtype=torch.float16)), 'up'),
+    (dict(up=torch.zeros(8, 4, dtype=torch.float32)), 'up'),
+    (dict(y=torch.zeros(2, 9, dtype=torch.float16)), 'out'),
+    (dict(y=torch.zeros(8, 2, dtype=torch.float16).t()), 'out'),
+    (dict(x=torch.zeros(2, 64, dtype=torch.float32)), 'x'),
+    (dict(group_size=48), 'group_size'),
+    (dict(rank=0), 'rank'),
+    (dict(format='fp16'), 'codes'),
+    (dict(format='int5'), 'format'),
+    (dict(N=True), 'N'),
+])
+def test_operand_checks_raise_value_error(over, needle):
+    import lowbit_hip
+    with pytest.raises(ValueError, match=needle):
+        lowbit_hip.check_operands(**_operands(**over))
+
+
+def test_operand_checks_require_the_device():
+    """Well-formed host tensors still fail: every operand must sit on x's ROCm device."""
+    import lowbit_hip
+    with pytest.raises(ValueError, match='ROCm device'):
+        lowbit_hip.check_operands(**_operands())
+    with pytest.raises(ValueError, match='ROCm device'):
+        lowbit_hip.linear(torch.zeros(1, 64, dtype=torch.float16), torch.zeros(256, dtype=torch.uint8),
+                          torch.zeros(8, 2, dtype=torch.float16), format='int4', N=8, K=64, group_size=32)

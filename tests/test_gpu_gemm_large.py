@@ -1,8 +1,8 @@
 """GPU parity of the 256 x 256 prefill GEMM (gemm4_kernel) against the CPU oracle.
 
 Prefill calls whose 256 x 256 tiles give at least 160 workgroups (K a multiple of 64) run
-there; calls with fewer, whose 256 x 128 tiles give 192 to 256 (rows past M adding at most an
-eighth), run its four-wave 256 x 128 form.  Same bars as every linear path: rel-L2 <= 1e-3 against the oracle and the reference's
+there; calls with fewer, whose 256 x 128 tiles give 160 to 256 workgroups (rows past M adding at
+most an eighth), run its eight-wave 256 x 128 form (4 x 2 waves of 64 x 64).  Same bars as every linear path: rel-L2 <= 1e-3 against the oracle and the reference's
 rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for identity-like inputs with
 power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover every format, partial
 tiles in M and N, bias, per-row int8 scales and the rank-32 correction.
@@ -33,7 +33,7 @@ def test_gemm4_matches_oracle(device, spec):
     check(p, run(p, device), f'gemm4 {spec}')
 
 
-# 256 x 128 tiles: fewer than 160 tiles of 256 x 256, 192 to 256 of 256 x 128.
+# 256 x 128 tiles: fewer than 160 tiles of 256 x 256, 160 to 256 of 256 x 128.
 TALL = [
     ('int4', 512, 12500, 256, 128), ('nf4', 480, 13000, 128, 64), ('int8', 1000, 6200, 192, 64),
     ('int8', 512, 12800, 128, 128),

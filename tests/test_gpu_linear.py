@@ -305,3 +305,30 @@ def test_split_k_repeated_calls_reuse_workspace(device, spec):
         if first is None:
             first = got.copy()
         np.testing.assert_array_equal(got.view(np.uint16), first.view(np.uint16))  # deterministic
+
+
+def test_host_or_mismatched_operands_raise_before_launch(device):
+    """A host tensor among device operands is refused with ValueError instead of being read
+    as device memory; so are strided codes/scales views."""
+    announce('operand devices')
+    rng = np.random.default_rng(12)
+    p = problem(rng, 'int4', 2, 64, 128, 32, rank=4, bias=True)
+    x = to_dev(p['x'], device)
+    codes = to_dev(np.frombuffer(p['data'], np.uint8), device)
+    scales = to_dev(np.frombuffer(p['scales'], np.float16), device)
+    kw = dict(format='int4', N=64, K=128, group_size=32)
+    good = dict(bias=to_dev(p['bias'], device), down=to_dev(p['down'], device), up=to_dev(p['up'], device), rank=4)
+    for name in ('bias', 'down', 'up'):
+        with pytest.raises(ValueError, match=name):
+            lowbit_hip.linear(x, codes, scales, **kw, **dict(good, **{name: good[name].cpu()}))
+    with pytest.raises(ValueError, match='scales'):
+        lowbit_hip.linear(x, codes, scales.cpu(), **kw)
+    with pytest.raises(ValueError, match='codes'):
+        lowbit_hip.linear(x, codes.cpu(), scales, **kw)
+    with pytest.raises(ValueError, match='out'):
+        lowbit_hip.linear(x, codes, scales, **kw, out=torch.empty(2, 64, dtype=torch.float16))
+    with pytest.raises(ValueError, match='scales'):
+        wide = torch.zeros(scales.numel() * 2, dtype=torch.float16, device=device)
+        lowbit_hip.linear(x, codes, wide[::2], **kw)
+    y = lowbit_hip.linear(x, codes, scales, **kw, **good)
+    assert o.rel_l2(y.cpu().numpy(), expected(p)) <= REL_L2

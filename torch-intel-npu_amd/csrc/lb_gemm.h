@@ -419,9 +419,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
       for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.0f;
 
   // Fragment reads: lane row fr = lane & 31 of a tile at logical chunk 2 kk + lane / 32.  Every
-  // tile row is fr plus a multiple of 8, so the swizzle (chunk ^ (row & 7)) is a per-lane constant
-  // and a read is a per-lane base plus compile-time offsets (tile, stage) and one of four chunk
-  // offsets.
+  // tile row is fr plus a tile base that is a multiple of 32 (wave block offsets and 32-row MFMA
+  // tiles), so while 32 is a multiple of 8 << LB_GEMM4_SWZ_SHIFT the swizzle LB_G4_SWZ(row) equals
+  // LB_G4_SWZ(fr): a per-lane constant, and a read is a per-lane base plus compile-time offsets
+  // (tile, stage) and one of four chunk offsets.
+  static_assert(LB_GEMM4_SWZ_SHIFT >= 0 && LB_GEMM4_SWZ_SHIFT <= 2 && WROWS % 32 == 0 && WCOLS % 32 == 0,
+                "fragment swizzle needs tile bases that are multiples of 8 << LB_GEMM4_SWZ_SHIFT");
   const int fr = lane & 31, fh = lane >> 5;
   int koff[4];
 #pragma unroll

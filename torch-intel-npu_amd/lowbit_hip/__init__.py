@@ -139,6 +139,67 @@ def _device_tensor(t, name, dtype=None):
     return t
 
 
+def _code_bytes(format, N, K):
+    return N * K * 2 if format == 'fp16' else N * K if format == 'int8' else (N * K + 1) // 2
+
+
+def check_operands(x, codes, scales, *, format, N, K, group_size, y=None, bias=None, down=None, up=None, rank=0):
+    """Every operand of one lb_linear call, before anything reaches the library: dtype, size and
+    layout first (so a wrong operand is named whatever its device), then the device -- all on
+    x's ROCm device.  The C side checks only pointers and alignment, so a host tensor or a
+    strided view caught here would otherwise be read as device memory of the wrong layout."""
+    if format not in FORMATS:
+        raise ValueError(f'unknown format {format!r}')
+    for name, value in (('N', N), ('K', K), ('group_size', group_size), ('rank', rank)):
+        if isinstance(value, bool) or not hasattr(value, '__index__') or value < (0 if name == 'rank' else 1):
+            raise ValueError(f'{name} must be a positive integer')
+    if K % group_size:
+        raise ValueError('group_size must divide K')
+    if not isinstance(x, torch.Tensor) or x.dtype != torch.float16 or x.ndim != 2 or x.shape[1] != K:
+        raise ValueError('x must be fp16 [M, K]')
+    operands = [('x', x)]
+    code_types = (torch.float16,) if format == 'fp16' else (torch.uint8, torch.int8)
+    if not isinstance(codes, torch.Tensor) or codes.dtype not in code_types:
+        raise ValueError(f'codes must be a {" or ".join(map(str, code_types))} tensor for format {format}')
+    if not codes.is_contiguous() or codes.numel() * codes.element_size() < _code_bytes(format, N, K):
+        raise ValueError(f'codes must be contiguous with the packed bytes of a {N}x{K} {format} weight')
+    operands.append(('codes', codes))
+    if format == 'fp16':
+        if scales is not None:
+            raise ValueError('fp16 weights take no scales')
+    else:
+        if not isinstance(scales, torch.Tensor) or scales.dtype != torch.float16:
+            raise ValueError('scales must be an fp16 tensor')
+        if not scales.is_contiguous() or scales.numel() < N * (K // group_size):
+            raise ValueError(f'scales must be contiguous fp16 [N, K/group_size] = [{N}, {K // group_size}]')
+        operands.append(('scales', scales))
+    if y is not None:
+        if (not isinstance(y, torch.Tensor) or y.dtype != torch.float16 or tuple(y.shape) != (x.shape[0], N)
+                or (N > 1 and y.stride(1) != 1)):
+            raise ValueError(f'out must be fp16 [M, N] = [{x.shape[0]}, {N}] with unit column stride')
+        operands.append(('out', y))
+    if bias is not None:
+        if (not isinstance(bias, torch.Tensor) or bias.dtype != torch.float16 or not bias.is_contiguous()
+                or bias.numel() != N):
+            raise ValueError(f'bias must be contiguous fp16 [{N}]')
+        operands.append(('bias', bias))
+    if rank:
+        if (not isinstance(down, torch.Tensor) or down.dtype != torch.float16 or down.ndim != 2
+                or tuple(down.shape) != (rank, K)):
+            raise ValueError(f'down must be fp16 [rank, K] = [{rank}, {K}]')
+        if (not isinstance(up, torch.Tensor) or up.dtype != torch.float16 or up.ndim != 2
+                or up.shape[0] != N or up.shape[1] < rank):
+            raise ValueError(f'up must be fp16 [N, >= rank] = [{N}, >= {rank}]')
+        operands += [('down', down), ('up', up)]
+    elif down is not None or up is not None:
+        raise ValueError('down/up need rank > 0')
+    if x.device.type != 'cuda':
+        raise ValueError('x must be a ROCm device tensor')
+    for name, t in operands:
+        if t.device != x.device:
+            raise ValueError(f'{name} must be on {x.device} with x (found {t.device})')
+
+
 def make_args(x, codes, scales, *, format, N, K, group_size, y, bias=None, down=None, up=None, rank=0,
               flags=0, activation_scale=None):
     """Fill an lb_linear_args for device tensors; x and y are 2-D views with unit column stride."""
@@ -176,9 +237,8 @@ def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, 
     scales: fp16 [N, K/group_size].  down: fp16 [rank,K] (row stride K); up: fp16 [N, >=rank].
     flags may add FLAG_COMPACT_GROUPS; activation_scale (a power of two) selects W8A8.
     """
-    _device_tensor(x, 'x', torch.float16)
-    if x.ndim != 2 or x.shape[1] != K:
-        raise ValueError('x must be [M, K]')
+    check_operands(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out, bias=bias,
+                   down=down, up=up, rank=rank)
     if K > 1 and x.stride(1) != 1:
         x = x.contiguous()
     if rank:
@@ -228,12 +288,15 @@ class PreparedLinear:
 
     def __init__(self, x, codes, scales, *, format, N, K, group_size, out, bias=None, down=None, up=None,
                  rank=0, flags=0, workspace=None, activation_scale=None):
-        _device_tensor(x, 'x', torch.float16)
-        _device_tensor(out, 'out', torch.float16)
-        if x.ndim != 2 or x.shape[1] != K or (K > 1 and x.stride(1) != 1):
+        check_operands(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out, bias=bias,
+                       down=down, up=up, rank=rank)
+        if K > 1 and x.stride(1) != 1:
             raise ValueError('PreparedLinear needs x [M, K] with unit column stride')
-        if out.shape != (x.shape[0], N) or (N > 1 and out.stride(1) != 1):
-            raise ValueError('PreparedLinear needs out [M, N] with unit column stride')
+        if rank:
+            if down.stride(-1) != 1 or down.stride(0) != K:
+                down = down.contiguous()
+            if up.stride(-1) != 1:
+                up = up.contiguous()
         self._keep = [x, codes, scales, out, bias, down, up]
         self.args = make_args(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out,
                               bias=bias, down=down, up=up, rank=rank, flags=flags,

@@ -15,8 +15,9 @@
  *   - Outputs may not alias inputs (reference: backend.cpp:265-272).
  *   - Calls are asynchronous and ordered on `stream` (a hipStream_t; NULL is
  *     the default stream).  No entry point allocates device memory; scratch
- *     comes from a caller workspace sized by lb_workspace_bytes().  Calls that
- *     share one workspace must be ordered (same stream); concurrent calls race.
+ *     comes from a caller workspace sized by lb_workspace_bytes() (or, for
+ *     lb_linear_noalloc, from a library-held array).  Calls that share one
+ *     workspace must be ordered (same stream); concurrent calls race.
  *   - On any status other than LB_OK, lb_last_error() returns a thread-local
  *     message describing the failure, valid until the next call on the same
  *     thread.  Argument errors are detected before anything is launched.
@@ -41,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LB_ABI_VERSION 2
+#define LB_ABI_VERSION 3
 
 typedef enum lb_status {
   LB_OK = 0,
@@ -144,6 +145,24 @@ lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes);
  * (torch_npu_smollm.py:254-258).
  */
 lb_status lb_linear(const lb_linear_args *args, void *stream);
+
+/* Scratch held per GPU by the allocation-free entry point below (bytes). */
+#define LB_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * lb_linear without a caller workspace and without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  args->workspace must be NULL and
+ * workspace_bytes 0; the scratch a call needs (split-K partials, the correction's z and d,
+ * W8A8 activations, compact_groups pieces) comes from a device array of
+ * LB_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the process ends.  A call
+ * needing more (lb_workspace_bytes) is refused with LB_INVALID_ARGUMENT before any launch.
+ * Same kernels, results and stream ordering as lb_linear.  Every call on one GPU shares that
+ * GPU's array and nothing in it needs to start at zero; calls that overlap on one GPU (other
+ * streams, other threads) race on it, so order them on one stream.  The first call on a GPU
+ * looks the array's address up (making that GPU current for the lookup).
+ */
+lb_status lb_linear_noalloc(const lb_linear_args *args, void *stream);
 
 /*
  * Bit-exact decode of packed codes to int8 out[N*K] (row-major):

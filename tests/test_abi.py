@@ -367,3 +367,21 @@ def test_operand_checks_require_the_device():
     with pytest.raises(ValueError, match='ROCm device'):
         lowbit_hip.linear(torch.zeros(1, 64, dtype=torch.float16), torch.zeros(256, dtype=torch.uint8),
                           torch.zeros(8, 2, dtype=torch.float16), format='int4', N=8, K=64, group_size=32)
+
+
+def test_noalloc_entry_refuses_workspace_and_oversized_calls():
+    """lb_linear_noalloc checks everything on the host before touching a device: a caller
+    workspace is refused, and so is a call needing more than the library's scratch."""
+    lib = lowbit_hip.library()
+    a = args(N=1024, K=14336, ldx=14336, ldy=1024, group_size=128, x=0x1000000, y=0x2000000,
+             scales=0x3000000, codes=0x4000000, flags=lowbit_hip.FLAG_FORCE_GEMV, workspace=0x8000000,
+             workspace_bytes=1 << 20)
+    assert lib.lb_linear_noalloc(ctypes.byref(a), None) == lowbit_hip.INVALID_ARGUMENT
+    assert 'workspace' in lib.lb_last_error().decode()
+    big = args(M=64, N=8200, K=1024, group_size=32, ldx=1024, ldy=8200, x=0x10000000, y=0x20000000,
+               scales=0x30000000, codes=0x40000000, flags=lowbit_hip.FLAG_COMPACT_GROUPS)
+    status, need, _ = workspace(big)
+    assert status == 0 and need > lowbit_hip.NOALLOC_SCRATCH_BYTES
+    assert lib.lb_linear_noalloc(ctypes.byref(big), None) == lowbit_hip.INVALID_ARGUMENT
+    assert 'scratch' in lib.lb_last_error().decode()
+    assert lib.lb_linear_noalloc(None, None) == lowbit_hip.INVALID_ARGUMENT

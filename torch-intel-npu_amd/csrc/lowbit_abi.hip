@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/lowbit_hip.h"
@@ -727,6 +728,45 @@ lb_status launch_status(const char *what) {
 
 }  // namespace
 
+// Scratch of lb_linear_noalloc: one array per GPU, held by the loaded code object until the process
+// ends.  In host code the name `scratch` is only a handle for hipGetSymbolAddress; its device
+// address (one per GPU) comes from scratch_address() and is what the kernels receive.
+static __device__ __align__(256) uint8_t scratch[LB_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the stream's GPU, looked up once per GPU with that GPU current.
+lb_status scratch_address(hipStream_t stream, void **out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LB_DEVICE_FAILED, "lb_linear_noalloc: device of the stream: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(LB_UNSUPPORTED, "lb_linear_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    int current = -1;
+    e = hipGetDevice(&current);
+    if (e == hipSuccess && current != dev) e = hipSetDevice(dev);
+    void *ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current >= 0 && current != dev) {
+      const hipError_t back = hipSetDevice(current);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess || !ptr)
+      return fail(LB_DEVICE_FAILED, "lb_linear_noalloc: scratch address on device %d: %s", dev,
+                  e != hipSuccess ? hipGetErrorString(e) : "null");
+    scratch_ptr[dev] = ptr;
+  }
+  *out = scratch_ptr[dev];
+  return LB_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int lb_abi_version(void) { return LB_ABI_VERSION; }
@@ -853,6 +893,27 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     launch_generic(fmt, p, s);
   }
   return launch_status("lb_linear");
+}
+
+lb_status lb_linear_noalloc(const lb_linear_args *a, void *stream) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: args is NULL");
+  if (a->struct_size >= sizeof(lb_linear_args) && (a->workspace || a->workspace_bytes))
+    return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: workspace must be NULL / 0 (the library holds the scratch)");
+  Plan plan;
+  const lb_status st = validate(a, false, &plan);
+  if (st != LB_OK) return st;
+  if (plan.total > LB_NOALLOC_SCRATCH_BYTES)
+    return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: the call needs %zu bytes of scratch; the allocation-free "
+                "entry holds %zu (use lb_linear with a workspace)", plan.total, (size_t)LB_NOALLOC_SCRATCH_BYTES);
+  lb_linear_args b = *a;
+  if (plan.total > 0) {
+    void *ptr = nullptr;
+    const lb_status got = scratch_address(static_cast<hipStream_t>(stream), &ptr);
+    if (got != LB_OK) return got;
+    b.workspace = ptr;
+    b.workspace_bytes = LB_NOALLOC_SCRATCH_BYTES;
+  }
+  return lb_linear(&b, stream);
 }
 
 lb_status lb_unpack_codes(uint32_t format, int64_t N, int64_t K, const void *codes, int8_t *out, void *stream) {

@@ -16,13 +16,14 @@ import torch
 
 LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve().parent.parent / 'liblowbit_hip.so'))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM = 0x1, 0x2, 0x4, 0x20
 FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_workspace_bytes', 'lb_linear',
-           'lb_unpack_codes', 'lb_dequantize')
+           'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
+NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
@@ -92,6 +93,8 @@ def library():
         lib.lb_workspace_bytes.argtypes = [ctypes.POINTER(LinearArgs), ctypes.POINTER(ctypes.c_size_t)]
         lib.lb_linear.restype = ctypes.c_int
         lib.lb_linear.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_void_p]
+        lib.lb_linear_noalloc.restype = ctypes.c_int
+        lib.lb_linear_noalloc.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_void_p]
         lib.lb_unpack_codes.restype = ctypes.c_int
         lib.lb_unpack_codes.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p]
@@ -257,6 +260,26 @@ def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, 
         args.workspace, args.workspace_bytes = _ptr(workspace), workspace.numel()
     _check(library().lb_linear(ctypes.byref(args), _stream(x.device)), 'lb_linear')
     return y
+
+
+def linear_noalloc(x, codes, scales, *, out, format, N, K, group_size, bias=None, down=None, up=None, rank=0,
+                   flags=0, activation_scale=None):
+    """lb_linear_noalloc: the same product as linear() into the caller's `out`, with no device
+    allocation by the library or by this wrapper (the scratch is the library's per-GPU array of
+    NOALLOC_SCRATCH_BYTES).  Operands must already have the layouts the call needs (no copies
+    are made); a call needing more scratch raises ValueError.  Calls overlapping on one GPU race."""
+    check_operands(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out, bias=bias,
+                   down=down, up=up, rank=rank)
+    if out is None:
+        raise ValueError('linear_noalloc writes into a caller-provided out')
+    if K > 1 and x.stride(1) != 1:
+        raise ValueError('linear_noalloc needs x with unit column stride')
+    if rank and (down.stride(-1) != 1 or down.stride(0) != K or up.stride(-1) != 1):
+        raise ValueError('linear_noalloc needs row-major down [rank, K] and up with unit column stride')
+    args = make_args(x, codes, scales, format=format, N=N, K=K, group_size=group_size, y=out, bias=bias,
+                     down=down, up=up, rank=rank, flags=flags, activation_scale=activation_scale)
+    _check(library().lb_linear_noalloc(ctypes.byref(args), _stream(x.device)), 'lb_linear_noalloc')
+    return out
 
 
 def unpack_codes(codes, *, format, N, K):

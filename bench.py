@@ -11,9 +11,11 @@ o, down and lm_head as one launch each (5 launches).  Launches are replayed from
 graphs so host launch cost is not in the timed region; inputs are resident in HBM.
 
 Also reported: the pass with one launch per shape (8 launches), at M=4 and M=16,
-per-launch GB/s, the config-5 roofline
-sweep, prefill GEMM TFLOP/s (configs 3 and 5), and the CPU baseline (the reference's
-CPU path: fp32 torch matmul on pre-dequantized weights) timed on this host.
+per-launch GB/s, config 1 (W8 per-row 1536x576 + rank-32 correction at M=1), the config-5
+roofline sweep (INT4 at M = 1, 8, 32 and W8 per-row at M = 1), prefill GEMM TFLOP/s on the
+config-3 and config-5 cells with hipBLASLt fp16 (no dequantization) beside the M = 512 cells, the
+config-4 decode leg, and the CPU baseline (the reference's CPU path: fp32 torch matmul on
+pre-dequantized weights) timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cpu]
        python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
@@ -200,33 +202,96 @@ def smol_pass(m, device, stream, steps, warmup, grouped=False):
                 gbs=total / (ms / steps) / 1e6, per_kernel=per_kernel, linears=linears)
 
 
+# Config 3 (NF4 g64, SmolLM-360M MLP) and config 5 (INT4 g128, Llama-3-8B) prefill cells, plus the
+# Llama gate/up shape at M = 512 where the M=512 MFMA target is quoted.
+GEMM_SPECS = ([('nf4', m, n, k, 64, name) for m in (128, 512, 2048)
+               for name, n, k in (('smol360m_gate', 2560, 960), ('smol360m_down', 960, 2560))]
+              + [('int4', m, n, k, g, name) for m in (256, 1024) for name, n, k, g in LLAMA_SHAPES]
+              + [('int4', 512, 14336, 4096, 128, '14336x4096'), ('nf4', 512, 14336, 4096, 128, '14336x4096'),
+                 ('int8', 256, 576, 576, 576, 'smol135m_q_prefill')])
+# hipBLASLt fp16 (torch.matmul, no dequantization) on the M = 512 cells: the vendor rate on these shapes.
+VENDOR_SPECS = [(512, 2560, 960, 'smol360m_gate'), (512, 960, 2560, 'smol360m_down'),
+                (512, 14336, 4096, '14336x4096'), (1024, 14336, 4096, '14336x4096')]
+
+
+def sweep_row(lin, stream, fmt, m, n, k, g, name):
+    us = float(np.median([kernel_time_us(lin, stream, replays=4) for _ in range(3)]))  # median of 3 timed graphs
+    row = dict(fmt=fmt, M=m, N=n, K=k, group=g, shape=name, us=round(us, 2),
+               gbs=round(lin.bytes / us / 1e3, 1), tflops=round(lin.flops / us / 1e6, 2))
+    row['hbm_frac' if m <= 32 else 'mfma_frac'] = round(
+        row['gbs'] / HBM_PEAK_GBS if m <= 32 else row['tflops'] / FP16_MFMA_PEAK_TFLOPS, 4)
+    log('sweep', json.dumps(row))
+    return row
+
+
 def sweep(device, stream, quick):
-    rows = []
-    specs = []
-    for m in ((1, 32) if quick else (1, 8, 32)):
-        for name, n, k, g in LLAMA_SHAPES:
-            specs.append(('int4', m, n, k, g, name))
-    gemm = [('nf4', 512, 2560, 960, 64, 'smol360m_gate'), ('nf4', 2048, 2560, 960, 64, 'smol360m_gate'),
-            ('nf4', 512, 960, 2560, 64, 'smol360m_down'), ('int4', 1024, 14336, 4096, 128, '14336x4096'),
-            ('int4', 1024, 4096, 4096, 128, '4096x4096')]
-    if not quick:
-        gemm += [('nf4', 128, 2560, 960, 64, 'smol360m_gate'), ('int4', 256, 14336, 4096, 128, '14336x4096'),
-                 ('int8', 256, 576, 576, 576, 'smol135m_q_prefill')]
-    specs += gemm
-    for i, (fmt, m, n, k, g, name) in enumerate(specs):
-        packed = make_weight(fmt, n, k, g, 300 + i)
+    """Config-5 GEMVs (INT4 at M = 1, 8, 32; W8 per-row at M = 1), the prefill cells of configs 3 and
+    5, and hipBLASLt fp16 on the M = 512 cells.  One packed weight per (format, shape) serves every M."""
+    specs = [('int4', m, n, k, g, name) for m in ((1, 32) if quick else (1, 8, 32)) for name, n, k, g in LLAMA_SHAPES]
+    specs += [('int8', 1, n, k, k, name) for name, n, k, _ in LLAMA_SHAPES]
+    specs += GEMM_SPECS[:4] if quick else GEMM_SPECS
+    order = sorted(range(len(specs)), key=lambda i: (specs[i][0], specs[i][2], specs[i][3]))
+    rows, packed = [None] * len(specs), {}
+    for i in order:
+        fmt, m, n, k, g, name = specs[i]
+        key = (fmt, n, k, g)
+        if key not in packed:
+            packed.clear()
+            torch.cuda.empty_cache()
+            packed[key] = make_weight(fmt, n, k, g, 300 + len(rows) + i)
         bytes_w = algorithmic_bytes(fmt, 0, n, k, g)
-        lin = Linear(packed, m, copies_for(bytes_w, cap=32), device, 400 + i)
-        us = float(np.median([kernel_time_us(lin, stream, replays=4) for _ in range(3)]))  # median of 3 timed graphs
-        row = dict(fmt=fmt, M=m, N=n, K=k, group=g, shape=name, us=round(us, 2),
-                   gbs=round(lin.bytes / us / 1e3, 1), tflops=round(lin.flops / us / 1e6, 2))
-        row['hbm_frac' if m <= 32 else 'mfma_frac'] = round(
-            row['gbs'] / HBM_PEAK_GBS if m <= 32 else row['tflops'] / FP16_MFMA_PEAK_TFLOPS, 4)
-        rows.append(row)
-        log('sweep', json.dumps(row))
+        lin = Linear(packed[key], m, copies_for(bytes_w, cap=32), device, 400 + i)
+        rows[i] = sweep_row(lin, stream, fmt, m, n, k, g, name)
         del lin
         torch.cuda.empty_cache()
+    for m, n, k, name in ([] if quick else VENDOR_SPECS):
+        a = torch.randn(m, k, device=device, dtype=torch.float16)
+        b = [torch.randn(n, k, device=device, dtype=torch.float16) for _ in range(copies_for(2 * n * k, cap=16))]
+        for w in b[:2]:
+            torch.matmul(a, w.t())
+        graph = capture([lambda w=w: torch.matmul(a, w.t()) for w in b], stream)
+        time_graphs([graph], 2, stream)
+        us = float(np.median([1000.0 * time_graphs([graph], 4, stream) / (4 * len(b)) for _ in range(3)]))
+        row = dict(fmt='fp16 hipBLASLt (torch.matmul, no dequantization)', M=m, N=n, K=k, shape=name,
+                   us=round(us, 2), tflops=round(2 * m * n * k / us / 1e6, 2))
+        row['mfma_frac'] = round(row['tflops'] / FP16_MFMA_PEAK_TFLOPS, 4)
+        log('sweep', json.dumps(row))
+        rows.append(row)
+        del a, b, graph
+        torch.cuda.empty_cache()
     return rows
+
+
+def config1_leg(device, stream):
+    """Config 1: W8A16 576->1536 + rank-32 correction at M=1, seed 0.
+    Draw order W [1536,576]*0.02 fp32, x [1,576] fp16, U [1536,32]*0.01 fp16, V [32,576]*0.01 fp16;
+    y = x.(q*s)^T + fp16(fp16(x.V^T).U^T) through one lb_linear (the fused one-row kernel)."""
+    import lowbit_hip
+    from torch_npu_lowbit import quantize_weight
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(1536, 576, generator=g) * 0.02
+    x = torch.randn(1, 576, generator=g).half().to(device)
+    up = (torch.randn(1536, 32, generator=g) * 0.01).half()
+    down = (torch.randn(32, 576, generator=g) * 0.01).half()
+    packed = quantize_weight(w, format='int8')
+    n, k, r = 1536, 576, 32
+    total = algorithmic_bytes('int8', 1, n, k, k) + 2 * r * (n + k)
+    copies = copies_for(total)
+    codes, scales = packed.device_tensors(device)
+    reps = [(codes.clone(), scales.clone(), down.to(device), up.to(device)) for _ in range(copies)]
+    y = torch.empty(1, n, dtype=torch.float16, device=device)
+    calls = [lowbit_hip.PreparedLinear(x, c, s, format='int8', N=n, K=k, group_size=k, out=y, down=d, up=u, rank=r)
+             for c, s, d, u in reps]
+    unit = type('Unit', (), {})()
+    unit.calls = calls
+    for call in calls[:2]:
+        call.run()
+    us = float(np.median([kernel_time_us(unit, stream, replays=8) for _ in range(3)]))
+    row = dict(shape='gate_proj 1536x576', fmt='int8 per-row + rank-32 correction', M=1, us=round(us, 3),
+               algorithmic_bytes=total, gbs=round(total / us / 1e3, 1), replicas=copies)
+    row['hbm_frac'] = round(row['gbs'] / HBM_PEAK_GBS, 4)
+    log('config1', json.dumps(row))
+    return row
 
 
 def cpu_leg(budget_s):
@@ -242,7 +307,8 @@ def cpu_leg(budget_s):
     return dict(value=round(total / pre / 1e9, 3), unit='GB/s', cores=cpu.threads, kind='port',
                 sample=(f'{rounds} interleaved rounds (median) of one M=1 pass over the 8 SmolLM-135M '
                         f'INT4 shapes: fp32 torch CPU matmul on pre-dequantized weights, fp16 out '
-                        f'(reference timing method, torch_npu_lowbit_demo.py:65,71); host {cpu_baseline.cpu_model()}'),
+                        f'(reference timing method, torch_npu_lowbit_demo.py:65,71); the dequant-inclusive '
+                        f'variant adds the fp16 PackedWeight.dequantize() per call; host {cpu_baseline.cpu_model()}'),
                 ms_per_pass=round(pre * 1e3, 3), dequant_inclusive_ms_per_pass=round(deq * 1e3, 3),
                 dequant_inclusive_gbs=round(total / deq / 1e9, 3))
 
@@ -449,6 +515,7 @@ def main():
         others[f'M={m}'] = dict(gbs=round(r['gbs'], 1), us_per_step=round(r['ms_per_step'] * 1e3, 2),
                                 per_kernel=r['per_kernel'])
         torch.cuda.empty_cache()
+    config1 = config1_leg(device, stream)
     rows = [] if args.no_sweep else sweep(device, stream, args.quick)
     cpu = None if args.no_cpu else cpu_leg(args.cpu_seconds)
     decode = None
@@ -489,6 +556,7 @@ def main():
             'algorithmic_bytes_per_launch': lm.bytes, 'avg_launch_us': dominant['us'],
         },
         'cpu_baseline': cpu,
+        'config1_w8_rank32_m1': config1,
         'per_launch_M1': head['per_kernel'],
         'decode_smollm135m_w8_rank32': decode,
         'passes': others,

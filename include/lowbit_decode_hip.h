@@ -84,7 +84,8 @@ typedef struct lb_decode_attention_args {
   const void *k;            /* fp16 [kv_heads, 64] new key row (before RoPE) */
   const void *v;            /* fp16 [kv_heads, 64] new value row */
   const void *cos, *sin;    /* fp16 [capacity, 64] RoPE tables */
-  const int64_t *position;  /* device scalar p: the slot of the new token; the call is a no-op unless 0 <= p < capacity */
+  const int64_t *position;  /* device scalar p: the slot of the new token; outside 0 <= p < capacity the cache is
+                               neither read nor written and every element of out is NaN */
   void *keys, *values;      /* fp16 [kv_heads, capacity, 64]; slot p is written */
   void *out;                /* fp16 [heads, 64] */
   float scale;              /* score scale, applied after the fp16 rounding of q.k (0.125 for head_dim 64) */

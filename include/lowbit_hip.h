@@ -121,6 +121,18 @@ const char *lb_status_name(lb_status status);
 const char *lb_last_error(void);
 
 /*
+ * Process-wide failed state, the counterpart of the reference's failed context
+ * (npunlock-probe/torch-device/backend.cpp:58-60, 280-292, reported as context_failed at :470).
+ * A launch that reports a device error marks the library failed; from then on every entry point
+ * that enqueues work returns LB_DEVICE_FAILED ("restart the process") without launching.
+ * lb_failed() returns 1 in that state.  lb_mark_failed(reason) enters it from the caller's side:
+ * the library never synchronises, so a device fault surfaces at the caller's own synchronisation,
+ * which reports it here.  The state lasts until the process ends.
+ */
+int lb_failed(void);
+void lb_mark_failed(const char *reason);
+
+/*
  * Bytes of device workspace lb_linear needs for these arguments (0 when none).
  * Host-only; validates args.  Replaces nothing in the reference: the NPU graph
  * owned its intermediates (torch_npu_lowbit.py:189-277).

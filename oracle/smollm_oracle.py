@@ -156,12 +156,15 @@ class OracleLayer:
 
 
 class OracleModel:
-    """Stack + tied embedding / final norm endpoints, greedy generation with a KV cache."""
+    """Stack + tied embedding / final norm endpoints, greedy generation with a KV cache.
+    head: (fmt, shape, group, data, scales) of a quantized tied head, or None for the fp16 one;
+    a quantized head is the projection linear above (W8 per-row exact q*s, 4-bit fp16(q*s))."""
 
-    def __init__(self, layers, embedding, norm):
+    def __init__(self, layers, embedding, norm, head=None):
         self.layers = layers
         self.embedding = embedding.detach().float().half()
         self.norm_w = norm.detach().float().half()
+        self.head = head
 
     def embed(self, ids):
         return F.embedding(ids, self.embedding)
@@ -169,7 +172,15 @@ class OracleModel:
     def logits(self, hidden):
         f = hidden.float()
         inv = torch.rsqrt(f.square().mean(-1, keepdim=True) + 1e-5)
-        return F.linear((f * inv).half() * self.norm_w, self.embedding)
+        normalized = (f * inv).half() * self.norm_w
+        if self.head is None:
+            return F.linear(normalized, self.embedding)
+        fmt, shape, group, data, scales = self.head
+        if fmt == 'int8' and group == shape[1]:
+            w = torch.from_numpy(lo.exact_weight(fmt, shape, group, data, scales))
+            return (normalized.double() @ w.T).half()
+        w = torch.from_numpy(lo.dequantize(fmt, shape, group, data, scales).astype(np.float32))
+        return F.linear(normalized.float(), w).half()
 
     def prefill(self, ids):
         x = self.embed(ids)
@@ -179,14 +190,15 @@ class OracleModel:
             caches.append((k, v))
         return x, caches
 
-    def generate(self, ids, steps):
-        """Greedy: returns (tokens [steps], logits fp16 [steps, vocab]) for the steps after the prompt."""
+    def generate(self, ids, steps, forced=None):
+        """Greedy: returns (tokens [steps], logits fp16 [steps, vocab]) for the steps after the prompt.
+        forced: a token list to feed instead of the argmax (teacher forcing; logits as greedy)."""
         x, caches = self.prefill(ids)
         pos = ids.shape[1]
         logits = self.logits(x[:, -1:])[:, 0]
         tokens, all_logits = [], []
         for step in range(steps):
-            tok = int(logits[0].float().argmax())
+            tok = int(logits[0].float().argmax()) if forced is None else int(forced[step])
             tokens.append(tok)
             all_logits.append(logits[0].clone())
             if step == steps - 1:

@@ -385,3 +385,49 @@ def test_noalloc_entry_refuses_workspace_and_oversized_calls():
     assert lib.lb_linear_noalloc(ctypes.byref(big), None) == lowbit_hip.INVALID_ARGUMENT
     assert 'scratch' in lib.lb_last_error().decode()
     assert lib.lb_linear_noalloc(None, None) == lowbit_hip.INVALID_ARGUMENT
+
+
+def test_failed_state_refuses_every_enqueueing_entry():
+    """After a reported device failure the library refuses work (reference backend.cpp:58-60,
+    280-292).  Forced from the host in a child process: the state lasts until the process ends."""
+    import subprocess
+    import sys
+    code = r'''
+import ctypes, sys
+sys.path[:0] = sys.argv[1:]
+import lowbit_hip
+lib = lowbit_hip.library()
+assert lib.lb_failed() == 0 and not lowbit_hip.failed()
+a = lowbit_hip.LinearArgs(); a.struct_size = ctypes.sizeof(a)
+a.format, a.M, a.N, a.K, a.group_size = 1, 1, 64, 128, 32
+a.codes, a.scales, a.x, a.y, a.ldx, a.ldy = 0x10000, 0x20000, 0x30000, 0x40000, 128, 64
+lowbit_hip.mark_failed('forced by the test')
+assert lib.lb_failed() == 1 and lowbit_hip.failed()
+calls = [('lb_linear', lambda: lib.lb_linear(ctypes.byref(a), None)),
+         ('lb_linear_noalloc', lambda: lib.lb_linear_noalloc(ctypes.byref(a), None)),
+         ('lb_unpack_codes', lambda: lib.lb_unpack_codes(1, 64, 128, 0x10000, 0x50000, None)),
+         ('lb_dequantize', lambda: lib.lb_dequantize(1, 64, 128, 32, 0x10000, 0x20000, 0x50000, None)),
+         ('lb_fused_linear', lambda: lib.lb_fused_linear(ctypes.byref(lowbit_hip.FusedLinearArgs()), None)),
+         ('lb_decode_attention', lambda: lib.lb_decode_attention(ctypes.byref(lowbit_hip.DecodeAttentionArgs()), None)),
+         ('lb_argmax_next', lambda: lib.lb_argmax_next(0x1, 16, 0x2, 8, 0x3, 0x4, 0x5, 0x6, 4, None))]
+for name, call in calls:
+    assert call() == lowbit_hip.DEVICE_FAILED, name
+    message = lib.lb_last_error().decode()
+    assert 'restart the process' in message and 'forced by the test' in message, message
+size = ctypes.c_size_t(0)
+assert lib.lb_workspace_bytes(ctypes.byref(a), ctypes.byref(size)) == 0   # host-only queries still answer
+try:
+    import torch
+    lowbit_hip.check_operands  # the Python wrappers raise RuntimeError from the status
+    lowbit_hip._check(lowbit_hip.DEVICE_FAILED, 'lb_linear')
+except RuntimeError as error:
+    assert 'LB_DEVICE_FAILED' in str(error)
+else:
+    raise AssertionError('no RuntimeError')
+print('ok')
+'''
+    root = Path(__file__).resolve().parents[1]
+    out = subprocess.run([sys.executable, '-c', code, str(root), str(root / 'torch-intel-npu_amd')],
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.strip().endswith('ok'), out.stdout + out.stderr
+    assert not lowbit_hip.failed()   # this process is untouched

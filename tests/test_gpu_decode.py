@@ -253,17 +253,21 @@ def test_decode_attention_masks_slots_past_the_position(device, pos, cap, poison
     assert rel_l2(got, want) <= 1e-3
 
 
-def test_decode_attention_full_cache_is_a_no_op(device):
+def test_decode_attention_past_the_capacity_leaves_the_cache_and_gives_nan(device):
+    """A position outside the cache (full, or negative) reads and writes no slot, and the output is
+    NaN everywhere: a caller past the capacity sees it instead of stale values."""
+    announce('decode attention past capacity')
     cap = 16
     keys, values, q, k, v, cos, sin = attention_case(0, cap, 3)
     dk, dv = keys.to(device), values.to(device)
-    out = torch.full((576,), 7.0, dtype=torch.float16, device=device)
-    position = torch.tensor([cap], dtype=torch.int64, device=device)
-    lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
-                         out, heads=9, kv_heads=3).run()
-    torch.cuda.synchronize()
-    assert torch.equal(dk.cpu(), keys) and torch.equal(dv.cpu(), values)
-    assert bool((out.cpu() == 7.0).all())
+    for pos in (cap, cap + 5, -1):
+        out = torch.full((576,), 7.0, dtype=torch.float16, device=device)
+        position = torch.tensor([pos], dtype=torch.int64, device=device)
+        lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk,
+                             dv, out, heads=9, kv_heads=3).run()
+        torch.cuda.synchronize()
+        assert torch.equal(dk.cpu(), keys) and torch.equal(dv.cpu(), values)
+        assert bool(torch.isnan(out.cpu()).all()), pos
 
 
 def test_argmax_next_order_position_and_embedding(device):

@@ -10,8 +10,9 @@ size, plus the oracle on row slices.
 - Row equivariance: reversing the weight rows (codes and scales) reverses y bit for bit; a row's
   arithmetic does not depend on which tile, wave or workgroup computes it.
 - Oracle: the restated reference (rel-L2 <= 1e-3 and its rounding-budget gate) on row slices.
-Shapes: config 5 (Llama-3-8B head 128256x4096 INT4 g128 at M = 1 and 8; 1024x14336x4096 prefill),
-config 3 (NF4 g64 2560x960 at M = 2048), config 2 (lm_head 49152x576 g64 at M = 4 and 16) and
+Shapes: every config-5 cell (Llama-3-8B projections 4096x4096, 1024x4096, 14336x4096, 4096x14336
+and the 128256x4096 head, INT4 g128, at M = 1, 8, 32, 256, 1024), every config-3 cell (NF4 g64
+2560x960 and 960x2560 at M = 128, 512, 2048), config 2's lm_head 49152x576 g64 at M = 4 and 16,
 the W8 GEMV at M = 1 on the Llama head (per-row int8) and a grouped int8 32768x2048.
 """
 import numpy as np
@@ -24,9 +25,11 @@ from test_gpu_linear import check
 
 pytestmark = pytest.mark.gpu
 
-FULL = [('int4', 1, 128256, 4096, 128), ('int4', 8, 128256, 4096, 128), ('int4', 1024, 14336, 4096, 128),
-        ('nf4', 2048, 2560, 960, 64), ('int4', 4, 49152, 576, 64), ('int4', 16, 49152, 576, 64),
-        ('int8', 1, 128256, 4096, 4096), ('int8', 1, 32768, 2048, 64)]
+CONFIG5 = [('int4', m, n, k, 128) for m in (1, 8, 32, 256, 1024)
+           for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096))]
+CONFIG3 = [('nf4', m, n, k, 64) for m in (128, 512, 2048) for n, k in ((2560, 960), (960, 2560))]
+FULL = CONFIG5 + CONFIG3 + [('int4', 4, 49152, 576, 64), ('int4', 16, 49152, 576, 64),
+                            ('int8', 1, 128256, 4096, 4096), ('int8', 1, 32768, 2048, 64)]
 
 
 def packed_random(rng, fmt, n, k, group):
@@ -75,9 +78,9 @@ def test_full_size_properties_and_slices(device, spec):
     assert torch.equal(y_rev, y.flip(1)), 'reversed rows do not give the reversed output'
     # oracle on row slices
     got = y.cpu().numpy()
-    rows = 1024 if m <= 16 else 256
+    rows = min(1024 if m <= 16 else 256, n // 2)
     g = k // group
-    for lo in (0, n // 2 + 16, n - rows):
+    for lo in (0, n // 2 - rows // 2 + 16, n - rows):
         d = data[lo * row_bytes:(lo + rows) * row_bytes]
         s = scales[lo * g:(lo + rows) * g].tobytes()
         p = dict(fmt=fmt, m=m, n=rows, k=k, group=group, x=x, data=d, scales=s, bias=None, down=None, up=None)

@@ -231,3 +231,50 @@ def test_config4_graph_decoder_matches_oracle(device):
     rest = decoder.generate(steps - 1)
     assert [ref_tokens[0]] + rest == ref_tokens
     assert rel_l2(decoder.logits.view(-1), ref_logits[steps - 1]) <= 1e-2
+
+
+@pytest.mark.parametrize('fmt,group', [('int8', None), ('int4', 64)])
+def test_quantized_tied_head(device, fmt, group):
+    """The tied lm_head as a W8 per-row / INT4 g64 GEMV of the config-2 lm_head shape (49152x576):
+    device logits against the oracle at the kernel bar, then 16 graph-replayed decode steps with
+    that head, checked step by step against the oracle fed the same tokens (teacher forcing):
+    logits rel-L2 <= 1e-2, and every chosen token is the oracle's argmax up to twice the largest
+    logit error (a near-tie may go either way without the check failing)."""
+    announce('quantized head', fmt)
+    from torch_npu_smollm import GraphDecoder
+    from torch_npu_smollm_io import FrozenSmolIO
+    stack, io, _, _ = smollm_random.build(seed=VARIED_SEED, layers=4, rank=32, theta=10000.0, capacity=128,
+                                          **VARIED_SCALES)
+    qio = FrozenSmolIO(smollm_random.config(), io.embedding, io.norm, head_format=fmt, head_group_size=group)
+    q = qio.head
+    assert q.shape == (49152, 576) and q.format == fmt
+    layers = [so.OracleLayer(layer._weights, packed_of(layer), corr_of(layer), theta=10000.0, capacity=128)
+              for layer in stack.layers]
+    oracle = so.OracleModel(layers, io.embedding, io.norm, head=(q.format, q.shape, q.group_size, q.data, q.scales))
+    g = torch.Generator().manual_seed(3)
+    hidden = torch.randn(1, 3, 576, generator=g).half()
+    qio = qio.to(device)
+    got = qio.logits(hidden.to(device)).cpu()
+    assert rel_l2(got, oracle.logits(hidden)) <= 1e-3
+    ids = smollm_random.prompt(seed=VARIED_SEED, length=64)
+    steps = 16
+    h, caches = stack.prefill(qio.embed_tokens(ids.to(device)))
+    logits0 = qio.logits(h[:, -1:])[0, 0]
+    first = int(logits0.float().argmax())
+    decoder = GraphDecoder(stack, qio)
+    decoder.load(caches, first)
+    history, rest = [logits0.cpu()], []
+    for _ in range(steps - 1):
+        rest += decoder.generate(1)
+        history.append(decoder.logits.view(-1).cpu().clone())
+    tokens = [first] + rest
+    _, ref_logits = oracle.generate(ids, steps, forced=tokens)
+    logits = torch.stack(history)
+    errs = [rel_l2(logits[i], ref_logits[i]) for i in range(steps)]
+    abs_err = float((logits.float() - ref_logits.float()).abs().max())
+    best = ref_logits.float().max(-1).values
+    chosen = ref_logits.float()[torch.arange(steps), torch.tensor(tokens)]
+    print('[quantized head]', fmt, json.dumps(dict(max_rel_l2=max(errs), max_abs_err=abs_err,
+                                                    distinct=len(set(tokens)))), flush=True)
+    assert max(errs) <= 1e-2
+    assert bool((chosen >= best - 2 * abs_err).all())

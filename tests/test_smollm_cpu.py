@@ -292,3 +292,26 @@ def test_oracle_attention_matches_transformers_llama():
         bad_att, bad_logits = _oracle_run(layer_type, specs, emb, norm, ids, t)
         assert _rel(bad_att[0], want_att[0]) > 0.1, (layer_type.__name__, t)
         assert _rel(bad_logits, want_logits) > 0.1, (layer_type.__name__, t)
+
+
+def test_quantized_head_cpu_logits():
+    """The quantized tied head on the CPU is the projection linear of the reference
+    (torch_npu_smollm.py:150-157) on the normalized rows, as the oracle states it."""
+    g = torch.Generator().manual_seed(106)
+    cfg = dict(model_type='llama', hidden_size=576, tie_word_embeddings=True, rms_norm_eps=1e-5, vocab_size=96)
+    emb = (torch.randn(96, 576, generator=g) * .03).half()
+    norm = (1 + torch.randn(576, generator=g) * .1).half()
+    x = (torch.randn(2, 3, 576, generator=g)).half()
+    plain = FrozenSmolIO(cfg, emb, norm)
+    for fmt, group in (('int8', None), ('int4', 64), ('nf4', 32)):
+        io = FrozenSmolIO(cfg, emb, norm, head_format=fmt, head_group_size=group)
+        q = io.head
+        assert q.format == fmt and q.shape == (96, 576) and q == quantize_weight(emb, format=fmt, group_size=group)
+        model = so.OracleModel([], emb, norm, head=(q.format, q.shape, q.group_size, q.data, q.scales))
+        got = io.logits(x)
+        torch.testing.assert_close(got, model.logits(x), rtol=0, atol=0)
+        err = float((got.float() - plain.logits(x).float()).norm() / plain.logits(x).float().norm())
+        assert 0 < err < (0.02 if fmt == 'int8' else 0.3), (fmt, err)
+    for bad in (dict(head_format='int2'), dict(head_format='int8', head_group_size=64)):
+        with pytest.raises(ValueError):
+            FrozenSmolIO(cfg, emb, norm, **bad)

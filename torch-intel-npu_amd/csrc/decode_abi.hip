@@ -295,11 +295,6 @@ void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s)
   ranked ? launch_fused_r<FMT, SCALED, true>(p, tiles, s) : launch_fused_r<FMT, SCALED, false>(p, tiles, s);
 }
 
-lb_status launch_status(const char *what) {
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(LB_DEVICE_FAILED, "%s: %s", what, hipGetErrorString(e));
-  return ok();
-}
 
 }  // namespace
 
@@ -413,6 +408,7 @@ void launch_fused(const FusedParams &p, int format, bool scaled, bool ranked, in
 extern "C" {
 
 lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_fused_linear"); bad != LB_OK) return bad;
   const lb_status st = check_fused(a);
   if (st != LB_OK) return st;
   FusedParams p{};
@@ -453,6 +449,7 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
 }
 
 lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_decode_attention"); bad != LB_OK) return bad;
   if (!a) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: args is NULL");
   if (a->struct_size < sizeof(lb_decode_attention_args))
     return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: struct_size %u < %zu", a->struct_size,
@@ -505,6 +502,7 @@ lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
 
 lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embedding, int64_t hidden, void *h_next,
                          int64_t *tokens, int64_t *token, int64_t *position, int64_t limit, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_argmax_next"); bad != LB_OK) return bad;
   if (!logits || !embedding || !h_next || !tokens || !token || !position)
     return fail(LB_INVALID_ARGUMENT, "lb_argmax_next: NULL pointer");
   if (vocab < 1 || vocab > INT32_MAX / 2 || hidden < 8 || hidden % 8 != 0 || hidden > 65536 || limit < 0 ||

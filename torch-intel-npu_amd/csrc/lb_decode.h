@@ -479,7 +479,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
   const int group = p.heads / p.kv_heads;
   const int kvh = h / group;
   const int pos = (int)p.position[0];
-  if (pos < 0 || pos >= p.capacity) return;  // host guarantees; never index outside the cache
+  if (pos < 0 || pos >= p.capacity) {
+    // No slot for the new row: nothing is read from or written to the cache, and the
+    // workgroup's output dims are NaN, so a caller past the capacity sees it in the result.
+    if (t < kSliceDims) p.out[h * kHeadDim + d0 + t] = (f16)__builtin_nanf("");
+    return;
+  }
 
   // The new rows first: wave 0 reads the query row of head h, wave 1 the key row and wave 2
   // the value row of its KV head (element d and its rotate-half partner d ^ 32), waves 0 and 1

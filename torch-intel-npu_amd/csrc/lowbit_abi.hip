@@ -720,11 +720,6 @@ void launch_compact(const lb_linear_args *a, const Plan &pl, const LinearParams 
                      (const f16 *)pieces, groups);
 }
 
-lb_status launch_status(const char *what) {
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(LB_DEVICE_FAILED, "%s: %s", what, hipGetErrorString(e));
-  return ok();
-}
 
 }  // namespace
 
@@ -785,6 +780,10 @@ const char *lb_status_name(lb_status status) {
 
 const char *lb_last_error(void) { return last_error().c_str(); }
 
+int lb_failed(void) { return failed_state().failed.load(std::memory_order_acquire) ? 1 : 0; }
+
+void lb_mark_failed(const char *reason) { mark_failed(reason ? reason : "reported by the caller"); }
+
 lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes) {
   if (!bytes) return fail(LB_INVALID_ARGUMENT, "lb_workspace_bytes: bytes is NULL");
   Plan plan;
@@ -795,6 +794,7 @@ lb_status lb_workspace_bytes(const lb_linear_args *args, size_t *bytes) {
 }
 
 lb_status lb_linear(const lb_linear_args *a, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_linear"); bad != LB_OK) return bad;
   Plan plan;
   lb_status st = validate(a, true, &plan);
   if (st != LB_OK) return st;
@@ -896,6 +896,7 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
 }
 
 lb_status lb_linear_noalloc(const lb_linear_args *a, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_linear_noalloc"); bad != LB_OK) return bad;
   if (!a) return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: args is NULL");
   if (a->struct_size >= sizeof(lb_linear_args) && (a->workspace || a->workspace_bytes))
     return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: workspace must be NULL / 0 (the library holds the scratch)");
@@ -917,6 +918,7 @@ lb_status lb_linear_noalloc(const lb_linear_args *a, void *stream) {
 }
 
 lb_status lb_unpack_codes(uint32_t format, int64_t N, int64_t K, const void *codes, int8_t *out, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_unpack_codes"); bad != LB_OK) return bad;
   if (format > LB_FORMAT_NF4) return fail(LB_INVALID_ARGUMENT, "lb_unpack_codes: format must be int8/int4/nf4");
   if (N <= 0 || K <= 0 || !codes || !out) return fail(LB_INVALID_ARGUMENT, "lb_unpack_codes: bad arguments");
   const size_t count = (size_t)N * (size_t)K;
@@ -930,6 +932,7 @@ lb_status lb_unpack_codes(uint32_t format, int64_t N, int64_t K, const void *cod
 
 lb_status lb_dequantize(uint32_t format, int64_t N, int64_t K, int64_t group_size, const void *codes,
                         const void *scales, void *w_out, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_dequantize"); bad != LB_OK) return bad;
   if (format > LB_FORMAT_NF4) return fail(LB_INVALID_ARGUMENT, "lb_dequantize: format must be int8/int4/nf4");
   if (N <= 0 || K <= 0 || K > INT32_MAX || !codes || !scales || !w_out || group_size < 1 || group_size > K ||
       K % group_size != 0)

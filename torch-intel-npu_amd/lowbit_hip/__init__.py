@@ -21,8 +21,8 @@ OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM = 0x1, 0x2, 0x4, 0x20
 FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
-EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_workspace_bytes', 'lb_linear',
-           'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
+EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
+           'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
@@ -89,6 +89,10 @@ def library():
         lib.lb_status_name.restype = ctypes.c_char_p
         lib.lb_status_name.argtypes = [ctypes.c_int]
         lib.lb_last_error.restype = ctypes.c_char_p
+        lib.lb_failed.restype = ctypes.c_int
+        lib.lb_failed.argtypes = []
+        lib.lb_mark_failed.restype = None
+        lib.lb_mark_failed.argtypes = [ctypes.c_char_p]
         lib.lb_workspace_bytes.restype = ctypes.c_int
         lib.lb_workspace_bytes.argtypes = [ctypes.POINTER(LinearArgs), ctypes.POINTER(ctypes.c_size_t)]
         lib.lb_linear.restype = ctypes.c_int
@@ -124,6 +128,26 @@ def _check(status, what):
         message = library().lb_last_error().decode()
         error = ValueError if status == INVALID_ARGUMENT else RuntimeError
         raise error(f'{what} failed with {status_name(status)}: {message}')
+
+
+def failed():
+    """True once the library refuses work after a device failure (restart the process)."""
+    return bool(library().lb_failed())
+
+
+def mark_failed(reason):
+    """Put the library in its failed state: every later call raises RuntimeError (LB_DEVICE_FAILED)."""
+    library().lb_mark_failed(str(reason).encode()[:200])
+
+
+def synchronize(device=None):
+    """torch.cuda.synchronize; a device error found there marks the library failed, then re-raises
+    (the library itself never waits on the device, so this is where an asynchronous fault shows)."""
+    try:
+        torch.cuda.synchronize(device)
+    except RuntimeError as error:
+        mark_failed(f'synchronisation failed: {error}')
+        raise
 
 
 def _stream(device):

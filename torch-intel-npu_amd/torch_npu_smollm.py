@@ -643,9 +643,13 @@ class GraphDecoder:
             seq += self._fused_group(lin, [('mlp.down_proj.weight', self.h, dict(residual=self.h))], gate,
                                      prologue='silu_mul', x2=up)
             self.calls.append(seq)
-        self.head = lb.PreparedFused(self.h, [dict(codes=io.embedding, scales=None, N=io.vocab_size, y=self.logits)],
-                                     format='fp16', K=HIDDEN, group_size=HIDDEN, prologue='rmsnorm', gamma=io.norm,
-                                     eps=1e-5)
+        if io.head is None:
+            head, head_format, head_group = dict(codes=io.embedding, scales=None), 'fp16', HIDDEN
+        else:
+            codes, scales = io.head_tensors(self.device)
+            head, head_format, head_group = dict(codes=codes, scales=scales), io.head.format, io.head.group_size
+        self.head = lb.PreparedFused(self.h, [dict(head, N=io.vocab_size, y=self.logits)], format=head_format,
+                                     K=HIDDEN, group_size=head_group, prologue='rmsnorm', gamma=io.norm, eps=1e-5)
         self.argmax = lb.PreparedArgmax(self.logits, io.embedding, self.h, self.tokens, self.token, self.pos,
                                         limit=self.capacity)
 
@@ -673,8 +677,13 @@ class GraphDecoder:
                                                 N=e['N'], K=e['K'], group_size=e['group'], out=getattr(self, dst),
                                                 down=e.get('down'), up=e.get('up'), rank=e.get('rank', 0))
             self.calls.append(calls)
-        self.head = lb.PreparedLinear(self.normed, io.embedding, None, format='fp16', N=io.vocab_size, K=HIDDEN,
-                                      group_size=HIDDEN, out=self.logits)
+        if io.head is None:
+            self.head = lb.PreparedLinear(self.normed, io.embedding, None, format='fp16', N=io.vocab_size, K=HIDDEN,
+                                          group_size=HIDDEN, out=self.logits)
+        else:
+            codes, scales = io.head_tensors(self.device)
+            self.head = lb.PreparedLinear(self.normed, codes, scales, format=io.head.format, N=io.vocab_size,
+                                          K=HIDDEN, group_size=io.head.group_size, out=self.logits)
 
     @staticmethod
     def _norm_into(out, x, gamma):
@@ -773,4 +782,5 @@ class GraphDecoder:
             raise ValueError(f'{steps} steps from position {start} exceed the KV capacity {self.capacity}')
         for _ in range(steps // self.graph_tokens):
             self.graph.replay()
+        lowbit_hip.synchronize(self.device)  # a device fault of the replays marks the library failed here
         return self.tokens[start:start + steps].tolist()

@@ -30,6 +30,7 @@ extern "C" {
 #define LB_FUSED_MAX_PROBLEMS 3
 #define LB_FUSED_MAX_RANK 32
 #define LB_FUSED_MAX_K 1536
+#define LB_FUSED_WORKSPACE_BYTES 512
 
 /* lb_fused_linear_args.prologue: what is applied to the activation row before the product */
 #define LB_PROLOGUE_NONE 0u     /* x as given */
@@ -62,6 +63,15 @@ typedef struct lb_fused_linear_args {
   float eps;                /* RMSNORM epsilon */
   uint32_t reserved;
   lb_fused_problem problems[LB_FUSED_MAX_PROBLEMS];
+  /* Optional (NULL: every workgroup computes the correction activations z itself).  With a
+   * workspace of LB_FUSED_WORKSPACE_BYTES (256-byte aligned, zero before its first use) a call
+   * with corrections computes each z = fp16(x'.V^T) once, in workgroups dispatched ahead of the
+   * others, which read it after a bounded wait.  A workspace belongs to one call configuration
+   * (the same problems and ranks on every call; zero it again before using it for another) and
+   * calls sharing it must be ordered (one stream).  Fields absent from a struct whose struct_size
+   * ends before them count as NULL / 0. */
+  void *workspace;
+  size_t workspace_bytes;
 } lb_fused_linear_args;
 
 /*

@@ -129,11 +129,15 @@ def device_problems(case, problems, device, in_place):
     return out
 
 
+@pytest.mark.parametrize('shared_z', [True, False], ids=['shared-z', 'own-z'])
 @pytest.mark.parametrize('index', range(len(CASES)))
-def test_fused_linear_matches_oracle(device, index):
+def test_fused_linear_matches_oracle(device, index, shared_z):
+    """Both correction modes: z in dedicated workgroups (workspace) or in every workgroup."""
     case = CASES[index]
-    announce('fused linear', case)
-    fmt, group, K, prologue = case[:4]
+    fmt, group, K, prologue, sizes, rank = case[:6]
+    if not shared_z and not rank:
+        pytest.skip('no correction: the two modes are one launch')
+    announce('fused linear', case, 'shared z' if shared_z else 'own z')
     x, x2, gamma, problems = make_case(case, 100 + index)
     want = expected(case, x, x2, gamma, problems)
     for in_place in (False, True):
@@ -141,7 +145,7 @@ def test_fused_linear_matches_oracle(device, index):
         call = lb.PreparedFused(x.to(device), dev, format=fmt, K=K,
                                 group_size=K if group is None or fmt == 'fp16' else group, prologue=prologue,
                                 x2=None if x2 is None else x2.to(device),
-                                gamma=None if gamma is None else gamma.to(device), eps=1e-5)
+                                gamma=None if gamma is None else gamma.to(device), eps=1e-5, shared_z=shared_z)
         call.run()
         torch.cuda.synchronize()
         got = [d['y'].cpu() for d in dev]
@@ -149,11 +153,37 @@ def test_fused_linear_matches_oracle(device, index):
             assert torch.isfinite(a).all(), (i, in_place)
             err = rel_l2(a, b)
             assert err <= 1e-3, (i, in_place, err)
-        if not in_place:  # a second call on the same buffers gives the same bits
-            call.run()
+        tiles = sum((n + 15) // 16 for n in sizes)
+        if shared_z and rank:
+            assert call.counters() == [tiles, 0]   # every tile workgroup counted once, no timed-out wait
+        if not in_place:  # further calls on the same buffers give the same bits
+            for _ in range(3):
+                call.run()
             torch.cuda.synchronize()
             for d, a in zip(dev, got):
                 assert torch.equal(d['y'].cpu(), a)
+            if shared_z and rank:
+                assert call.counters() == [4 * tiles, 0]
+
+
+def test_shared_z_equals_own_z_bit_for_bit(device):
+    """The shared z is the same fp16 value each workgroup would compute (same prologue
+    arithmetic), so both modes give identical outputs on the decode shapes."""
+    announce('shared z vs own z')
+    for index in range(4):
+        case = CASES[index]
+        fmt, group, K, prologue = case[:4]
+        x, x2, gamma, problems = make_case(case, 300 + index)
+        outs = []
+        for shared_z in (True, False):
+            dev = device_problems(case, problems, device, False)
+            lb.PreparedFused(x.to(device), dev, format=fmt, K=K, group_size=K, prologue=prologue,
+                             x2=None if x2 is None else x2.to(device), gamma=None if gamma is None else gamma.to(device),
+                             eps=1e-5, shared_z=shared_z).run()
+            torch.cuda.synchronize()
+            outs.append([d['y'].cpu() for d in dev])
+        for a, b in zip(*outs):
+            assert torch.equal(a, b), case
 
 
 def test_fused_linear_agrees_with_lb_linear(device):

@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 
 #include "../../include/lowbit_decode_hip.h"
 #include "abi_util.h"
@@ -28,11 +29,17 @@ size_t code_bytes(uint32_t format, int64_t N, int64_t K) {
   return format == LB_FORMAT_FP16 ? (size_t)count * 2 : format == LB_FORMAT_INT8 ? (size_t)count : (size_t)(count + 1) / 2;
 }
 
+// Size of the argument struct before the workspace fields (callers built against it pass no workspace).
+constexpr size_t kFusedArgsV1 = offsetof(lb_fused_linear_args, workspace);
+
+void *fused_workspace(const lb_fused_linear_args *a) {
+  return a->struct_size >= sizeof(lb_fused_linear_args) ? a->workspace : nullptr;
+}
+
 lb_status check_fused(const lb_fused_linear_args *a) {
   if (!a) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: args is NULL");
-  if (a->struct_size < sizeof(lb_fused_linear_args))
-    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: struct_size %u < %zu", a->struct_size,
-                sizeof(lb_fused_linear_args));
+  if (a->struct_size < kFusedArgsV1)
+    return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: struct_size %u < %zu", a->struct_size, kFusedArgsV1);
   if (a->format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: unknown format %u", a->format);
   if (a->K <= 0 || a->K % 32 != 0 || a->K > LB_FUSED_MAX_K)
     return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: K=%lld must be a positive multiple of 32 <= %d",
@@ -54,7 +61,7 @@ lb_status check_fused(const lb_fused_linear_args *a) {
     return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: RMSNORM needs a 16-byte aligned gamma and a finite eps >= 0");
 
   const size_t kb = (size_t)a->K * 2;
-  Range in[4 + 6 * LB_FUSED_MAX_PROBLEMS];
+  Range in[4 + 6 * LB_FUSED_MAX_PROBLEMS + 1];
   int nin = 0;
   in[nin++] = range_of(a->x, kb, "x");
   in[nin++] = range_of(a->prologue == LB_PROLOGUE_SILU_MUL ? a->x2 : nullptr, a->prologue == LB_PROLOGUE_SILU_MUL ? kb : 0, "x2");
@@ -87,6 +94,15 @@ lb_status check_fused(const lb_fused_linear_args *a) {
                          "residual");
   }
   if (tiles > INT32_MAX) return fail(LB_UNSUPPORTED, "lb_fused_linear: too many rows");
+  void *ws = fused_workspace(a);
+  if (ws || (a->struct_size >= sizeof(lb_fused_linear_args) && a->workspace_bytes)) {
+    if (!ws || !aligned(ws, 256) || a->workspace_bytes < LB_FUSED_WORKSPACE_BYTES)
+      return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: workspace must be 256-byte aligned with %d bytes",
+                  LB_FUSED_WORKSPACE_BYTES);
+    in[nin++] = range_of(ws, LB_FUSED_WORKSPACE_BYTES, "workspace");
+    for (int r = 0; r + 1 < nin; ++r)
+      if (overlaps(in[nin - 1], in[r])) return fail(LB_INVALID_ARGUMENT, "lb_fused_linear: workspace overlaps %s", in[r].name);
+  }
   for (uint32_t i = 0; i < a->count; ++i) {
     const Range y = range_of(a->problems[i].y, (size_t)a->problems[i].N * 2, "y");
     for (int r = 0; r < nin; ++r)
@@ -100,6 +116,13 @@ lb_status check_fused(const lb_fused_linear_args *a) {
 
 template <int FMT, bool SCALED, int KMAX, bool RANKED>
 void launch_fused_k(const FusedParams &p, int tiles, hipStream_t s) {
+  if constexpr (RANKED) {
+    if (p.zblocks > 0) {  // z workgroups first: dispatched ahead of every tile workgroup that waits for them
+      hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, KMAX, true, true>), dim3(p.zblocks + tiles), dim3(256), 0,
+                         s, p);
+      return;
+    }
+  }
   hipLaunchKernelGGL((fused_gemv_kernel<FMT, SCALED, KMAX, RANKED>), dim3(tiles), dim3(256), 0, s, p);
 }
 
@@ -444,6 +467,16 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
   }
   bool ranked = false;
   for (uint32_t i = 0; i < a->count; ++i) ranked = ranked || a->problems[i].rank > 0;
+  void *ws = fused_workspace(a);
+  if (ranked && ws) {
+    int zb = 0;
+    for (int i = 0; i < LB_FUSED_MAX_PROBLEMS; ++i) {
+      if (i < (int)a->count) zb += (int)((a->problems[i].rank + kFusedZRanks - 1) / kFusedZRanks);
+      p.prob[i].zend = zb;
+    }
+    p.zblocks = zb;
+    p.zslot = static_cast<uint64_t *>(ws);
+  }
   launch_fused(p, (int)a->format, !dense && !p.per_row, ranked, tiles, static_cast<hipStream_t>(stream));
   return launch_status("lb_fused_linear");
 }

@@ -20,7 +20,24 @@ struct FusedProblem {
   const f16 *up;          // U [N, up_ld] or null
   int N, rank, up_ld;
   int tiles_end;          // exclusive prefix sum of 16-row tiles over the problems
+  int zend;               // exclusive prefix sum of z workgroups over the problems (shared z)
 };
+
+// Shared correction activations: a launch with zblocks > 0 starts with that many z workgroups,
+// each computing fp16(x'.V^T) for kFusedZRanks ranks of one problem.  Every three z values travel
+// in one 64-bit word, zslot[problem][rank / 3], whose low 16 bits are the launch's tag; the tile
+// workgroups read their problem's words with 64-bit atomic loads until every tag is current, then
+// count themselves on `passed` (64-bit, monotonic).  A launch's tag is (passed / tiles + 1) mod
+// 2^16, read by each workgroup at its start: only tile workgroups raise `passed`, each once per
+// launch after the wait, so at any workgroup's start it holds launch * tiles plus fewer than
+// `tiles`, and no word needs clearing between launches (the previous launch's tag is one behind).
+// The wait is bounded: a timeout is recorded in a separate word.
+constexpr int kFusedZRanks = 6;                                        // ranks per z workgroup
+constexpr int kFusedZWordsPerProblem = (kFusedMaxRank + 2) / 3;        // 11 words hold 32 ranks
+constexpr int kFusedZPassedOffset = 384;                               // byte offset of `passed` (u64)
+constexpr int kFusedZTimeoutOffset = 392;                              // byte offset of the timeout word
+constexpr int kFusedZSpinLimit = 1 << 18;
+constexpr unsigned kWaitVmcnt0 = 0x0F70;                               // s_waitcnt vmcnt(0), others free
 
 struct FusedParams {
   int force_stream;       // host-side dispatch only: take stream_gemv_kernel whatever the size
@@ -30,6 +47,8 @@ struct FusedParams {
   float eps;
   int K, G, group_shift, per_row, prologue;
   FusedProblem prob[kFusedMaxProblems];
+  uint64_t *zslot;        // shared z words [kFusedMaxProblems][12], then `passed` and the timeout word
+  int zblocks;            // z workgroups ahead of the tile workgroups (0: each tile computes z)
 };
 
 // Longest K a format's single-tile kernel takes (32 weight loads per lane); beyond

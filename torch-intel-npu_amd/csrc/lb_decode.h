@@ -51,6 +51,168 @@ __device__ __forceinline__ f16 rope_element(float x, float r, float c, float s) 
 // long-K variants (one-row lb_linear calls) need group >= 64.
 template <int KMAX> struct FusedGroupMin { static constexpr int value = KMAX <= 1536 ? 32 : 64; };
 
+// The prologue's scale factor: inv = 1 / sqrt(mean(x^2) + eps) for RMSNorm (1 otherwise), summed in
+// the same order by every workgroup of a launch (thread, wave, then the four waves), so all of them
+// stage the same row.  Contains a workgroup barrier when the prologue is RMSNorm.
+template <int XB>
+__device__ __forceinline__ float prologue_inv(const FusedParams &p, const h8 (&xv)[XB], float *wsum, int lane, int wave) {
+  if (p.prologue != PRO_RMSNORM) return 1.0f;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < XB; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
+  s = wave_sum(s);
+  if (lane == 0) wsum[wave] = s;
+  __syncthreads();
+  const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  return 1.0f / sqrtf(total / (float)p.K + p.eps);
+}
+
+// Eight staged elements of the prologue: RMSNorm fp16(fp16(x * inv) * gamma), SiLU-multiply
+// fp16(fp16(silu(x)) * x2), or x itself.
+__device__ __forceinline__ h8 prologue_apply(const FusedParams &p, const h8 &x, const h8 &a, float inv) {
+  h8 v;
+  if (p.prologue == PRO_RMSNORM) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)x[e] * inv) * (float)a[e]);
+  } else if (p.prologue == PRO_SILU_MUL) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)x[e]) * (float)a[e]);
+  } else {
+    v = x;
+  }
+  return v;
+}
+
+// `passed` of a shared-z call, read at the workgroup's start with a system-scope load (performed at
+// the memory side, past the per-XCD L2s); shared_z_tag turns it into the launch's tag,
+// (passed / tiles + 1) mod 2^16.
+__device__ __forceinline__ uint64_t shared_z_passed(const FusedParams &p) {
+  return __hip_atomic_load(p.zslot + kFusedZPassedOffset / 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ uint32_t shared_z_tag(const FusedParams &p, uint64_t passed) {
+  const uint32_t tiles = (uint32_t)p.prob[kFusedMaxProblems - 1].tiles_end;
+  return (uint32_t)((passed / tiles + 1) & 0xFFFF);
+}
+
+// One z workgroup of a shared-z launch (blockIdx.x < p.zblocks): ranks [r0, r0 + 6) of one problem,
+// z = fp16(x'.V^T) with x' the staged prologue row, published as two tagged 64-bit words with
+// system-scope atomic stores.  32 threads per rank row each take every 32nd 16-byte block of it;
+// all loads are issued first.
+template <int KMAX>
+__device__ __forceinline__ void fused_z_block(const FusedParams &p, f16 *xs, float *wsum, f16 *zsh) {
+  constexpr int TPR = 32;                             // threads per rank row (8 groups, 6 used)
+  constexpr int ZI = (KMAX / 8 + TPR - 1) / TPR;      // 16-byte V loads per thread
+  constexpr int XB = (KMAX / 8 + 255) / 256;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert(kFusedZRanks <= 256 / TPR, "one thread group per rank");
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int K = p.K, blocks = K >> 3;
+  const int b = blockIdx.x;
+  const int zp = b < p.prob[0].zend ? 0 : (b < p.prob[1].zend ? 1 : 2);
+  FusedProblem Z = p.prob[0];
+  int zfirst = 0;
+  if (zp == 1) { Z = p.prob[1]; zfirst = p.prob[0].zend; }
+  if (zp == 2) { Z = p.prob[2]; zfirst = p.prob[1].zend; }
+  const int zi = b - zfirst;                          // z workgroup of the problem: words 2 zi, 2 zi + 1
+  const int r0 = zi * kFusedZRanks;
+  const int rr = t / TPR, li = t % TPR;
+  const bool live = rr < kFusedZRanks && r0 + rr < Z.rank;
+  const uint64_t passed = shared_z_passed(p);
+  const size_t kb = (size_t)K * 2;
+  const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
+  const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.x, kb);
+  h8 av[XB], xv[XB];
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int blk = t + 256 * i;
+    av[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(abuf, blk < blocks ? blk * 16 : kOutOfRange, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int blk = t + 256 * i;
+    xv[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xbuf, blk < blocks ? blk * 16 : kOutOfRange, 0, 0));
+  }
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(Z.down, (size_t)Z.rank * K * 2);
+  u4 vz[ZI];
+#pragma unroll
+  for (int i = 0; i < ZI; ++i) {
+    const int blk = li + TPR * i;
+    const int off = live && blk < blocks ? ((r0 + rr) * K + blk * 8) * 2 : kOutOfRange;
+    vz[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const float inv = prologue_inv(p, xv, wsum, lane, wave);
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int blk = t + 256 * i;
+    if (blk < blocks) *reinterpret_cast<h8 *>(xs + blk * 8) = prologue_apply(p, xv[i], av[i], inv);
+  }
+  __syncthreads();
+  float acc = 0.0f, acc2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ZI; ++i) {
+    const int blk = li + TPR * i;
+    if (blk < blocks) {
+      asm volatile("" : "+v"(vz[i]));
+      const h8 vv = __builtin_bit_cast(h8, vz[i]);
+      const h8 xx = *reinterpret_cast<const h8 *>(xs + blk * 8);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        acc += (float)xx[e] * (float)vv[e];
+        acc2 += (float)xx[e + 1] * (float)vv[e + 1];
+      }
+    }
+  }
+  acc += acc2;
+#pragma unroll
+  for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (li == 0 && rr < kFusedZRanks) zsh[rr] = live ? (f16)acc : (f16)0.0f;
+  __syncthreads();
+  if (t < 2) {
+    const uint64_t word = (uint64_t)shared_z_tag(p, passed) | ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t]) << 16) |
+                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 1]) << 32) |
+                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 2]) << 48);
+    __hip_atomic_store(p.zslot + zp * 12 + 2 * zi + t, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+// Tile workgroups of a shared-z launch, wave 0: read the problem's z words (lane w < words holds
+// word w) with system-scope 64-bit atomic loads until every tag is the launch's (bounded), unpack
+// them to zs[rank] (fp16 values as floats, visible to the whole wave on return), then count the
+// workgroup on `passed`.
+__device__ __forceinline__ void wait_shared_z(const FusedParams &p, int pi, int rank, uint64_t passed, int lane,
+                                              float *zs) {
+  const uint32_t tag = shared_z_tag(p, passed);
+  const int words = (rank + 2) / 3;
+  const uint64_t *slot = p.zslot + pi * 12;
+  uint64_t word = 0;
+  bool ready = false;
+  for (int it = 0; it < kFusedZSpinLimit; ++it) {
+    if (lane < words) word = __hip_atomic_load(slot + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    ready = __builtin_amdgcn_ballot_w64(lane < words && (uint32_t)(word & 0xFFFF) != tag) == 0;
+    if (ready) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (lane < words) {
+#pragma unroll
+    for (int e = 0; e < 3; ++e)
+      if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = (float)__builtin_bit_cast(f16, (uint16_t)(word >> (16 * (e + 1))));
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the LDS writes above precede the wave's reads
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) {
+    if (!ready)
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(p.zslot) + kFusedZTimeoutOffset / 4, 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_fetch_add(p.zslot + kFusedZPassedOffset / 8, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // One workgroup = 4 waves = one 16-row tile of one problem; the waves split K (wave w takes
 // k-steps w, w + 4, ...) and are reduced through LDS.  K <= KMAX, so every lane issues all
 // of its weight loads (D of them) up front and the activation row is staged once.  Every row
@@ -61,7 +223,7 @@ template <int KMAX> struct FusedGroupMin { static constexpr int value = KMAX <= 
 // (one load per wave), the prologue row, the activation, the scales, V (RANKED only) and the
 // weights.  Lanes without data read out of range (zeros).  There are no branches around loads:
 // a load under a branch makes the compiler wait for it at the branch's end.
-template <int FMT, bool SCALED, int KMAX, bool RANKED>
+template <int FMT, bool SCALED, int KMAX, bool RANKED, bool SHARED_Z = false>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
@@ -73,7 +235,9 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   constexpr int T8 = CPL / 8;
   constexpr int XLD = KMAX + KSTEP + 8;           // staged row, zero from K to K + KSTEP
   constexpr int XB = (KMAX / 8 + 255) / 256;      // 16-byte activation loads per thread
-  constexpr int VB = RANKED ? KMAX / 64 : 0;      // 16-byte V loads per thread (8 threads per rank row)
+  constexpr bool OWN_Z = RANKED && !SHARED_Z;     // every workgroup computes z itself
+  static_assert(!SHARED_Z || RANKED, "shared z is for ranked launches");
+  constexpr int VB = OWN_Z ? KMAX / 64 : 0;       // 16-byte V loads per thread (8 threads per rank row)
   constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;  // groups per row at most
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0; // staged scales per thread
   constexpr int kOutOfRange = (int)0x80000000u;
@@ -87,6 +251,12 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   __shared__ float wsum[4];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
+  if constexpr (SHARED_Z) {
+    if ((int)blockIdx.x < p.zblocks) {
+      fused_z_block<KMAX>(p, xs, wsum, es);
+      return;
+    }
+  }
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -94,7 +264,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   const int K = p.K;
 
   // Problem and tile of this workgroup (wave-uniform selects; no dynamic kernarg indexing).
-  const int bid = blockIdx.x;
+  const int bid = (int)blockIdx.x - (SHARED_Z ? p.zblocks : 0);
   const int pi = bid < p.prob[0].tiles_end ? 0 : (bid < p.prob[1].tiles_end ? 1 : 2);
   FusedProblem P = p.prob[0];
   int first = 0;
@@ -104,6 +274,8 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   const int rows = min(16, P.N - n0);
   const int row_bytes = K * BITS / 8;
   const int rank = RANKED ? P.rank : 0;
+  uint64_t zpassed = 0;
+  if constexpr (SHARED_Z) zpassed = shared_z_passed(p);  // issued with the loads below, used at the epilogue
 
   // Epilogue operands: wave 0 fetches the residual, wave 1 the bias, wave 2 the per-row
   // scale of the tile's 16 rows (lanes 0..15); absent operands have an empty buffer.
@@ -146,7 +318,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   }
   const int vr = t >> 3, vpart = t & 7;
   u4 vreg[VB > 0 ? VB : 1];
-  if constexpr (RANKED) {
+  if constexpr (OWN_Z) {
     const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(P.down, (size_t)rank * K * 2);
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
@@ -171,39 +343,15 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   if constexpr (RANKED) {
     if (lane < 16) *reinterpret_cast<u4 *>(us + (4 * wave + (lane >> 2)) * kFusedMaxRank + (lane & 3) * 8) = ureg;
   }
-  float inv = 1.0f;
-  if (p.prologue == PRO_RMSNORM) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < XB; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
-    s = wave_sum(s);
-    if (lane == 0) wsum[wave] = s;
-    __syncthreads();
-    const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    inv = 1.0f / sqrtf(total / (float)K + p.eps);
-  }
+  const float inv = prologue_inv(p, xv, wsum, lane, wave);
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
     const int b = t + 256 * i;
-    if (b < blocks) {
-      h8 v;
-      if (p.prologue == PRO_RMSNORM) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[i][e] * inv) * (float)av[i][e]);
-      } else if (p.prologue == PRO_SILU_MUL) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[i][e]) * (float)av[i][e]);
-      } else {
-        v = xv[i];
-      }
-      *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(v);
-    }
+    if (b < blocks) *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(prologue_apply(p, xv[i], av[i], inv));
   }
-  // Zeros past K: MFMA lanes read up to KSTEP beyond it, the z product (RANKED) up to KMAX.
-  const int zend = RANKED ? XLD : min(XLD, K + KSTEP + 8);
-  for (int b = blocks + t; b * 8 < zend; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  // Zeros past K: MFMA lanes read up to KSTEP beyond it, the own z product up to KMAX.
+  const int zero_end = OWN_Z ? XLD : min(XLD, K + KSTEP + 8);
+  for (int b = blocks + t; b * 8 < zero_end; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
   if constexpr (SCALED) {
 #pragma unroll
     for (int i = 0; i < SC; ++i)
@@ -213,7 +361,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   __syncthreads();
 
   // ---- correction activations z = fp16(x . V^T), 8 threads per rank row ----
-  if constexpr (RANKED) {
+  if constexpr (OWN_Z) {
     float acc = 0.0f, acc2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
@@ -256,6 +404,10 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   // Lane (j, g) holds D rows 4g..4g+3 of column j; all rows are equal, row 0 (g == 0) is used.
   if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
   __syncthreads();
+  if constexpr (SHARED_Z) {
+    if (wave != 0) return;
+    wait_shared_z(p, pi, rank, zpassed, lane, zs);
+  }
   const bool writer = wave == 0 && g == 0 && j < rows;
   if (!writer) return;
   float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
@@ -357,35 +509,11 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
 
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
   if (wave < 3 && lane < ROWS) es[wave * ROWS + lane] = ev;
-  float inv = 1.0f;
-  if (p.prologue == PRO_RMSNORM) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < XB; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
-    s = wave_sum(s);
-    if (lane == 0) wsum[wave] = s;
-    __syncthreads();
-    const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    inv = 1.0f / sqrtf(total / (float)K + p.eps);
-  }
+  const float inv = prologue_inv(p, xv, wsum, lane, wave);
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
     const int b = t + 256 * i;
-    if (b < blocks) {
-      h8 v;
-      if (p.prologue == PRO_RMSNORM) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)xv[i][e] * inv) * (float)av[i][e]);
-      } else if (p.prologue == PRO_SILU_MUL) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)xv[i][e]) * (float)av[i][e]);
-      } else {
-        v = xv[i];
-      }
-      *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(v);
-    }
+    if (b < blocks) *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(prologue_apply(p, xv[i], av[i], inv));
   }
   for (int b = blocks + t; b * 8 < min(XLD, K + KSTEP + 8); b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
   if constexpr (SCALED) {

@@ -27,6 +27,7 @@ NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
+FUSED_WORKSPACE_BYTES = 512  # LB_FUSED_WORKSPACE_BYTES: tagged z words [3][12] u64, launch count u64, timeout u32
 
 
 class LinearArgs(ctypes.Structure):
@@ -60,7 +61,8 @@ class FusedLinearArgs(ctypes.Structure):
                 ('prologue', ctypes.c_uint32), ('count', ctypes.c_uint32),
                 ('x', ctypes.c_void_p), ('x2', ctypes.c_void_p), ('gamma', ctypes.c_void_p),
                 ('eps', ctypes.c_float), ('reserved', ctypes.c_uint32),
-                ('problems', FusedProblem * 3)]
+                ('problems', FusedProblem * 3),
+                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
 
 
 class DecodeAttentionArgs(ctypes.Structure):
@@ -398,9 +400,13 @@ class PreparedFused(_Prepared):
     problems: sequence of dicts with keys codes, scales (None for fp16), N, y (fp16 row of N),
     and optionally bias, residual (may be y itself), down [rank,K], up [N,rank] (rank = down rows).
     prologue: 'none', 'rmsnorm' (gamma, eps) or 'silu_mul' (x = gate row, x2 = up row).
+    shared_z (default): with corrections, each z = fp16(x'.V^T) is computed once per call by
+    dedicated workgroups into a zeroed FUSED_WORKSPACE_BYTES workspace owned by this call;
+    False: every workgroup computes z itself (no workspace).
     """
 
-    def __init__(self, x, problems, *, format, K, group_size, prologue='none', x2=None, gamma=None, eps=1e-5):
+    def __init__(self, x, problems, *, format, K, group_size, prologue='none', x2=None, gamma=None, eps=1e-5,
+                 shared_z=True):
         if prologue not in PROLOGUES:
             raise ValueError(f'unknown prologue {prologue!r}')
         if not 1 <= len(problems) <= MAX_PROBLEMS:
@@ -434,8 +440,19 @@ class PreparedFused(_Prepared):
                 q.down, q.up, q.up_ld = _ptr(down.contiguous()), _ptr(up), up.stride(0)
                 keep += [down, up]
             keep += [pr['codes'], pr.get('scales'), pr['y'], pr.get('bias'), pr.get('residual')]
+        self.workspace = None
+        if shared_z and any(pr.get('down') is not None for pr in problems):
+            self.workspace = torch.zeros(FUSED_WORKSPACE_BYTES, dtype=torch.uint8, device=x.device)
+            a.workspace, a.workspace_bytes = _ptr(self.workspace), FUSED_WORKSPACE_BYTES
+            keep.append(self.workspace)
         self._bind('lb_fused_linear', 'lb_fused_linear', a, x.device, keep)
         self.outputs = [pr['y'] for pr in problems]
+
+    def counters(self):
+        """(tile workgroups counted over all calls so far, timeout word) of the workspace."""
+        if self.workspace is None:
+            return None
+        return [int(self.workspace[384:392].view(torch.int64)), int(self.workspace[392:396].view(torch.int32))]
 
 
 def fused_linear(x, problems, **options):

@@ -100,7 +100,21 @@ typedef struct lb_decode_attention_args {
   void *out;                /* fp16 [heads, 64] */
   float scale;              /* score scale, applied after the fp16 rounding of q.k (0.125 for head_dim 64) */
   uint32_t reserved2;
+  /* Optional (NULL: every output workgroup computes the whole score row itself).  With a workspace
+   * of LB_ATTN_WORKSPACE_BYTES(heads, capacity) (256-byte aligned, zero before its first use) and
+   * heads / kv_heads <= 3, the scores are computed once, by workgroups of 48 cached positions
+   * dispatched ahead of the output workgroups, which read them after a bounded wait.  A workspace
+   * belongs to one call configuration (same heads and capacity; zero it again before another);
+   * calls sharing it must be ordered (one stream).  Fields absent from a struct whose struct_size
+   * ends before them count as NULL / 0. */
+  void *workspace;
+  size_t workspace_bytes;
 } lb_decode_attention_args;
+
+/* Workspace of the split attention: tagged score words [heads][ceil(capacity / 48) * 16] (u64),
+ * then a launch count (u64) and a timeout word. */
+#define LB_ATTN_WORKSPACE_BYTES(heads, capacity) \
+  ((size_t)(heads) * (size_t)(((capacity) + 47) / 48) * 128u + 16u)
 
 /*
  * RoPE of q and k at row p, append (k, v) at slot p, causal GQA attention over slots 0..p with

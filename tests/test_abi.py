@@ -37,7 +37,7 @@ def test_struct_layout_matches_header():
     assert ctypes.sizeof(lowbit_hip.LinearArgs) == 8 + 8 * 4 + 8 * 2 + 8 * 2 + 8 * 2 + 8 + 8 * 3 + 8 + 8 + 8 + 8 + 8
     assert ctypes.sizeof(lowbit_hip.FusedProblem) == 10 * 8
     assert ctypes.sizeof(lowbit_hip.FusedLinearArgs) == 8 + 8 + 8 + 8 + 3 * 8 + 8 + 3 * 80 + 16
-    assert ctypes.sizeof(lowbit_hip.DecodeAttentionArgs) == 8 + 4 * 8 + 9 * 8 + 8
+    assert ctypes.sizeof(lowbit_hip.DecodeAttentionArgs) == 8 + 4 * 8 + 9 * 8 + 8 + 16
 
 
 def args(**over):

@@ -230,9 +230,10 @@ def attention_case(pos, cap, seed):
     return keys, values, q, k, v, cos, sin
 
 
-@pytest.mark.parametrize('pos', [0, 1, 37, 255, 383])
-def test_decode_attention_matches_oracle(device, pos):
-    announce('decode attention', pos)
+@pytest.mark.parametrize('split', [True, False], ids=['split', 'whole'])
+@pytest.mark.parametrize('pos', [0, 1, 2, 3, 37, 47, 48, 255, 383])
+def test_decode_attention_matches_oracle(device, pos, split):
+    announce('decode attention', pos, split)
     cap = 384
     keys, values, q, k, v, cos, sin = attention_case(pos, cap, pos)
     c, s = cos[pos:pos + 1][None, None], sin[pos:pos + 1][None, None]
@@ -244,10 +245,20 @@ def test_decode_attention_matches_oracle(device, pos):
     dk, dv = keys.to(device), values.to(device)
     out = torch.full((576,), float('nan'), dtype=torch.float16, device=device)
     position = torch.tensor([pos], dtype=torch.int64, device=device)
-    lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
-                         out, heads=9, kv_heads=3).run()
+    call = lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position,
+                                dk, dv, out, heads=9, kv_heads=3, split=split)
+    call.run()
     torch.cuda.synchronize()
     assert rel_l2(out.cpu(), want) <= 1e-3
+    if split:
+        assert call.counters() == [36, 0]      # every output workgroup counted once, no timed-out wait
+        first = out.cpu().clone()
+        dk[:, :, pos] = keys[:, :, pos].to(device)   # undo the append, run twice more on the same workspace
+        dv[:, :, pos] = values[:, :, pos].to(device)
+        call.run()
+        call.run()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), first) and call.counters() == [108, 0]
     assert torch.equal(dk[:, :, pos].cpu(), kr[:, :, 0])
     assert torch.equal(dv[:, :, pos].cpu(), v.view(3, 64)[None])
     others = [i for i in range(cap) if i != pos]
@@ -255,8 +266,10 @@ def test_decode_attention_matches_oracle(device, pos):
     assert torch.equal(dv[:, :, others].cpu(), values[:, :, others])
 
 
-@pytest.mark.parametrize('pos,cap,poison', [(100, 384, True), (383, 384, False), (700, 1024, True), (1023, 1024, False)])
-def test_decode_attention_masks_slots_past_the_position(device, pos, cap, poison):
+@pytest.mark.parametrize('split', [True, False], ids=['split', 'whole'])
+@pytest.mark.parametrize('pos,cap,poison', [(100, 384, True), (383, 384, False), (700, 1024, True), (1023, 1024, False),
+                                            (4095, 4096, True), (10, 16, True)])
+def test_decode_attention_masks_slots_past_the_position(device, pos, cap, poison, split):
     """Slots past the position may hold anything (here NaN / Inf when `poison`): the kernel loads the
     first 512 slots before it reads the position, and must select them away; capacities above 512
     take further load rounds."""
@@ -276,7 +289,7 @@ def test_decode_attention_masks_slots_past_the_position(device, pos, cap, poison
     out = torch.full((576,), float('nan'), dtype=torch.float16, device=device)
     position = torch.tensor([pos], dtype=torch.int64, device=device)
     lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk, dv,
-                         out, heads=9, kv_heads=3).run()
+                         out, heads=9, kv_heads=3, split=split).run()
     torch.cuda.synchronize()
     got = out.cpu()
     assert bool(torch.isfinite(got).all())
@@ -290,14 +303,15 @@ def test_decode_attention_past_the_capacity_leaves_the_cache_and_gives_nan(devic
     cap = 16
     keys, values, q, k, v, cos, sin = attention_case(0, cap, 3)
     dk, dv = keys.to(device), values.to(device)
-    for pos in (cap, cap + 5, -1):
-        out = torch.full((576,), 7.0, dtype=torch.float16, device=device)
-        position = torch.tensor([pos], dtype=torch.int64, device=device)
-        lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position, dk,
-                             dv, out, heads=9, kv_heads=3).run()
-        torch.cuda.synchronize()
-        assert torch.equal(dk.cpu(), keys) and torch.equal(dv.cpu(), values)
-        assert bool(torch.isnan(out.cpu()).all()), pos
+    for split in (True, False):
+        for pos in (cap, cap + 5, -1):
+            out = torch.full((576,), 7.0, dtype=torch.float16, device=device)
+            position = torch.tensor([pos], dtype=torch.int64, device=device)
+            lb.PreparedAttention(q.to(device), k.to(device), v.to(device), cos.to(device), sin.to(device), position,
+                                 dk, dv, out, heads=9, kv_heads=3, split=split).run()
+            torch.cuda.synchronize()
+            assert torch.equal(dk.cpu(), keys) and torch.equal(dv.cpu(), values)
+            assert bool(torch.isnan(out.cpu()).all()), (pos, split)
 
 
 def test_argmax_next_order_position_and_embedding(device):

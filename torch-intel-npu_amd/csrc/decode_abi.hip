@@ -31,6 +31,7 @@ size_t code_bytes(uint32_t format, int64_t N, int64_t K) {
 
 // Size of the argument struct before the workspace fields (callers built against it pass no workspace).
 constexpr size_t kFusedArgsV1 = offsetof(lb_fused_linear_args, workspace);
+constexpr size_t kAttnArgsV1 = offsetof(lb_decode_attention_args, workspace);
 
 void *fused_workspace(const lb_fused_linear_args *a) {
   return a->struct_size >= sizeof(lb_fused_linear_args) ? a->workspace : nullptr;
@@ -484,9 +485,8 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
 lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
   if (const lb_status bad = refuse_if_failed("lb_decode_attention"); bad != LB_OK) return bad;
   if (!a) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: args is NULL");
-  if (a->struct_size < sizeof(lb_decode_attention_args))
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: struct_size %u < %zu", a->struct_size,
-                sizeof(lb_decode_attention_args));
+  if (a->struct_size < kAttnArgsV1)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: struct_size %u < %zu", a->struct_size, kAttnArgsV1);
   if (a->head_dim != kHeadDim) return fail(LB_UNSUPPORTED, "lb_decode_attention: head_dim must be %d", kHeadDim);
   if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0 || a->heads > 1024)
     return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: heads must be a multiple of kv_heads (<= 1024)");
@@ -513,6 +513,17 @@ lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
   }
   if (overlaps(out, keys) || overlaps(out, values))
     return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: out overlaps the cache");
+  void *ws = a->struct_size >= sizeof(lb_decode_attention_args) ? a->workspace : nullptr;
+  const size_t ws_need = LB_ATTN_WORKSPACE_BYTES(a->heads, a->capacity);
+  if (ws || (a->struct_size >= sizeof(lb_decode_attention_args) && a->workspace_bytes)) {
+    if (!ws || !aligned(ws, 256) || a->workspace_bytes < ws_need)
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: workspace must be 256-byte aligned with %zu bytes", ws_need);
+    const Range wr = range_of(ws, ws_need, "workspace");
+    if (overlaps(wr, out) || overlaps(wr, keys) || overlaps(wr, values))
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: workspace overlaps an output");
+    for (const Range &r : in)
+      if (overlaps(wr, r)) return fail(LB_INVALID_ARGUMENT, "lb_decode_attention: workspace overlaps %s", r.name);
+  }
   AttnParams p{};
   p.q = static_cast<const f16 *>(a->q);
   p.k = static_cast<const f16 *>(a->k);
@@ -527,6 +538,14 @@ lb_status lb_decode_attention(const lb_decode_attention_args *a, void *stream) {
   p.kv_heads = (int)a->kv_heads;
   p.capacity = (int)a->capacity;
   p.scale = a->scale;
+  if (ws && a->heads / a->kv_heads <= kAttnMaxGroup) {
+    p.words = static_cast<uint64_t *>(ws);
+    p.chunks = (int)((a->capacity + kAttnChunk - 1) / kAttnChunk);
+    p.score_wgs = (int)a->kv_heads * p.chunks;
+    hipLaunchKernelGGL(split_attention_kernel, dim3((unsigned)(p.score_wgs + a->heads * kAttnDimSlices)), dim3(256),
+                       (size_t)a->capacity * sizeof(float), static_cast<hipStream_t>(stream), p);
+    return launch_status("lb_decode_attention");
+  }
   hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)a->heads, kAttnDimSlices), dim3(256),
                      (size_t)a->capacity * sizeof(float),
                      static_cast<hipStream_t>(stream), p);

@@ -571,6 +571,11 @@ struct AttnParams {
   f16 *out;                  // [heads, 64]
   int heads, kv_heads, capacity;
   float scale;
+  // Split form (split_attention_kernel): tagged score words [heads][chunks * 16], then `passed`
+  // (u64) and a timeout word; score workgroups first.
+  uint64_t *words;
+  int chunks;                // position chunks of kAttnChunk per KV head
+  int score_wgs;             // kv_heads * chunks
 };
 
 constexpr int kHeadDim = 64;
@@ -748,6 +753,239 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnParams p) {
     const float r = ((pv[t] + pv[kSliceDims + t]) + pv[2 * kSliceDims + t]) + pv[3 * kSliceDims + t];
     p.out[h * kHeadDim + d0 + t] = (f16)r;
   }
+}
+
+// Split decode attention: the scores and the output in separate workgroups of one launch.
+//
+// Score workgroups (the first kv_heads * chunks of the grid, so they are dispatched before any
+// workgroup that waits for them): KV head kvh, positions [48 c, 48 c + 48) up to the new token's.
+// Each applies RoPE to the query rows of the KV group and to the new key, writes the new key and
+// value into the cache if its chunk holds the new slot, computes the scores fp16(fp16(q.k) * scale)
+// for every query head of the group and publishes them three to a 64-bit word whose low 16 bits
+// are the launch's tag (system-scope atomic stores, performed at the memory side).
+//
+// Output workgroups: query head h, kSliceDims output dims.  Each reads its head's score words with
+// system-scope 64-bit atomic loads until every tag is the launch's (bounded), then follows the
+// reference staging on the whole row (global max, fp32 sum of exp, probabilities fp16(e / total)),
+// and forms fp16(P.V) over its dims from the cached values and the new value row.  The launch tag
+// is (passed / output workgroups + 1) mod 2^16, with `passed` raised once per output workgroup
+// after its wait, as in the shared-z decode GEMVs.  No workgroup reads a cache slot another writes.
+constexpr int kAttnChunk = 48;                          // positions per score workgroup
+constexpr int kAttnChunkWords = kAttnChunk / 3;         // score words per head and chunk
+constexpr int kAttnMaxGroup = 3;                        // query heads per KV head in the split form
+constexpr int kAttnSpinLimit = 1 << 18;
+
+__device__ __forceinline__ uint32_t attn_tag(const AttnParams &p, uint64_t passed) {
+  const uint32_t outs = (uint32_t)(p.heads * kAttnDimSlices);
+  return (uint32_t)((passed / outs + 1) & 0xFFFF);
+}
+
+__device__ __forceinline__ uint64_t *attn_passed(const AttnParams &p) {
+  return p.words + (size_t)p.heads * p.chunks * kAttnChunkWords;
+}
+
+__device__ __forceinline__ void attention_scores_block(const AttnParams &p, int b) {
+  __shared__ __align__(16) f16 qs[kAttnMaxGroup * kHeadDim];
+  __shared__ __align__(16) f16 kn[kHeadDim];
+  __shared__ float sco[kAttnMaxGroup * kAttnChunk];
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x;
+  const int group = p.heads / p.kv_heads;
+  const int kvh = b / p.chunks, c = b % p.chunks;
+  const int c0 = c * kAttnChunk;
+  const int pos = (int)p.position[0];
+  if (pos < 0 || pos >= p.capacity || c0 > pos) return;  // nothing of this chunk is needed
+  const uint64_t passed = __hip_atomic_load(attn_passed(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+
+  // New rows: thread t < 64 group reads element d (and its rotate-half partner) of query row
+  // kvh * group + t / 64, the next 64 threads the key row; threads 0..63 also the value row.
+  const int hh = t >> 6, d = t & 63;
+  const bool is_q = hh < group, is_k = hh == group;
+  const f16 *src = is_q ? p.q + (size_t)(kvh * group + hh) * kHeadDim : p.k + (size_t)kvh * kHeadDim;
+  const __amdgpu_buffer_rsrc_t rbuf = buffer_rsrc(src, is_q || is_k ? kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t cbuf = buffer_rsrc(p.cos + (size_t)pos * kHeadDim, kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t snbuf = buffer_rsrc(p.sin + (size_t)pos * kHeadDim, kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t vnbuf = buffer_rsrc(p.v + (size_t)kvh * kHeadDim, t < kHeadDim ? kHeadDim * 2 : 0);
+  const f16 x0 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rbuf, d * 2, 0, 0));
+  const f16 x1 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rbuf, (d ^ 32) * 2, 0, 0));
+  const f16 cv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(cbuf, d * 2, 0, 0));
+  const f16 sv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(snbuf, d * 2, 0, 0));
+  const f16 vnew = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(vnbuf, d * 2, 0, 0));
+  // Cached key rows of the chunk (slots below pos): 8 threads per row, 32 rows per pass.
+  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
+  const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(p.keys + head_base, (size_t)pos * kHeadDim * 2);
+  const int kr = t >> 3, kb = t & 7;
+  constexpr int kPasses = (kAttnChunk + 31) / 32;
+  u4 kreg[kPasses];
+#pragma unroll
+  for (int i = 0; i < kPasses; ++i) {
+    const int r = kr + 32 * i, s = c0 + r;
+    kreg[i] = __builtin_bit_cast(
+        u4, __builtin_amdgcn_raw_buffer_load_b128(kbuf, r < kAttnChunk && s < pos ? (s * kHeadDim + 8 * kb) * 2 : kOutOfRange, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (is_q || is_k) {
+    const float rot = d < 32 ? -(float)x1 : (float)x1;
+    const f16 r = rope_element((float)x0, rot, (float)cv, (float)sv);
+    if (is_q) qs[hh * kHeadDim + d] = r; else kn[d] = r;
+    if (is_k && pos < c0 + kAttnChunk) p.keys[head_base + (size_t)pos * kHeadDim + d] = r;
+  }
+  if (t < kHeadDim && pos < c0 + kAttnChunk) p.values[head_base + (size_t)pos * kHeadDim + t] = vnew;
+  __syncthreads();
+
+  // Scores: thread (row kr + 32 i, block kb) forms 8-element partial dot products for every query
+  // head of the group, summed over the row's 8 threads.
+#pragma unroll
+  for (int i = 0; i < kPasses; ++i) {
+    const int r = kr + 32 * i, s = c0 + r;
+    asm volatile("" : "+v"(kreg[i]));
+    const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * kb) : __builtin_bit_cast(h8, kreg[i]);
+    for (int q = 0; q < group; ++q) {
+      const h8 qq = *reinterpret_cast<const h8 *>(qs + q * kHeadDim + 8 * kb);
+      float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        acc0 += (float)qq[e] * (float)kk[e];
+        acc1 += (float)qq[e + 1] * (float)kk[e + 1];
+      }
+      float acc = acc0 + acc1;
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 4, 64);
+      if (kb == 0 && r < kAttnChunk) sco[q * kAttnChunk + r] = (float)(f16)((float)(f16)acc * p.scale);
+    }
+  }
+  __syncthreads();
+  if (t < group * kAttnChunkWords) {
+    const int q = t / kAttnChunkWords, w = t % kAttnChunkWords;
+    uint64_t word = attn_tag(p, passed);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      const float v = c0 + 3 * w + e <= pos ? sco[q * kAttnChunk + 3 * w + e] : 0.0f;
+      word |= (uint64_t)__builtin_bit_cast(uint16_t, (f16)v) << (16 * (e + 1));
+    }
+    uint64_t *dst = p.words + (size_t)(kvh * group + q) * p.chunks * kAttnChunkWords + c * kAttnChunkWords + w;
+    __hip_atomic_store(dst, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+__device__ __forceinline__ void attention_output_block(const AttnParams &p, int idx, float *sc) {
+  __shared__ __align__(16) f16 vn[kSliceDims];
+  __shared__ float wred[4];
+  __shared__ float pv[4 * kSliceDims];
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int h = idx / kAttnDimSlices;
+  const int d0 = (idx % kAttnDimSlices) * kSliceDims;
+  const int group = p.heads / p.kv_heads;
+  const int kvh = h / group;
+  const int pos = (int)p.position[0];
+  uint64_t *passed_word = attn_passed(p);
+  const uint64_t passed = __hip_atomic_load(passed_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (pos < 0 || pos >= p.capacity) {
+    if (t < kSliceDims) p.out[h * kHeadDim + d0 + t] = (f16)__builtin_nanf("");
+    if (t == 0) __hip_atomic_fetch_add(passed_word, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return;
+  }
+  // Cached value rows of this workgroup's dims (slots below pos) and the new value row.
+  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(p.values + head_base, (size_t)pos * kHeadDim * 2);
+  const int blk = t % kSliceBlocks, part = t / kSliceBlocks;
+  u4 vreg[kValueSlots];
+  auto load_values = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      vreg[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, s < pos ? (s * kHeadDim + d0 + 8 * blk) * 2 : kOutOfRange, 0, 0));
+    }
+  };
+  load_values(0);
+  const __amdgpu_buffer_rsrc_t vnbuf = buffer_rsrc(p.v + (size_t)kvh * kHeadDim + d0, t < kSliceDims ? kSliceDims * 2 : 0);
+  const f16 vnew = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(vnbuf, t * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  if (t < kSliceDims) vn[t] = vnew;
+
+  // The head's scores: word w holds slots 3 w .. 3 w + 2 (chunk w / 16 of its head).
+  const uint32_t tag = attn_tag(p, passed);
+  const int words = pos / 3 + 1;
+  const uint64_t *hw = p.words + (size_t)h * p.chunks * kAttnChunkWords;
+  bool late = false;
+  for (int w = t; w < words; w += 256) {
+    uint64_t word = 0;
+    int it = 0;
+    for (; it < kAttnSpinLimit; ++it) {
+      word = __hip_atomic_load(hw + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      if ((uint32_t)(word & 0xFFFF) == tag) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    late = late || it == kAttnSpinLimit;
+#pragma unroll
+    for (int e = 0; e < 3; ++e)
+      if (3 * w + e <= pos) sc[3 * w + e] = (float)__builtin_bit_cast(f16, (uint16_t)(word >> (16 * (e + 1))));
+  }
+  if (late)
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(passed_word + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __syncthreads();
+  if (t == 0) __hip_atomic_fetch_add(passed_word, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+
+  // Reference staging over slots 0..pos: global max, fp32 sum of exp, probabilities fp16(e / total).
+  float lmax = -INFINITY;
+  for (int s = t; s <= pos; s += 256) lmax = fmaxf(lmax, sc[s]);
+  lmax = wave_max(lmax);
+  if (lane == 0) wred[wave] = lmax;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float lsum = 0.0f;
+  for (int s = t; s <= pos; s += 256) {
+    const float e = expf(sc[s] - m);
+    sc[s] = e;
+    lsum += e;
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();  // every wave has read wred
+  if (lane == 0) wred[wave] = lsum;
+  __syncthreads();
+  const float total = ((wred[0] + wred[1]) + wred[2]) + wred[3];
+  for (int s = t; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
+  __syncthreads();
+
+  // out = fp16(P . V) over this workgroup's dims, as in decode_attention_kernel.
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base <= pos; base += kAttnParts * kValueSlots) {
+    if (base > 0) load_values(base);
+#pragma unroll
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      if (base + kAttnParts * i > pos) break;  // wave-uniform
+      asm volatile("" : "+v"(vreg[i]));
+      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
+      const float pr = s <= pos ? sc[min(s, pos)] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
+    }
+  }
+#pragma unroll
+  for (int off = kSliceBlocks; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off, 64);
+  if (lane < kSliceBlocks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[wave * kSliceDims + lane * 8 + e] = o[e];
+  }
+  __syncthreads();
+  if (t < kSliceDims) {
+    const float r = ((pv[t] + pv[kSliceDims + t]) + pv[2 * kSliceDims + t]) + pv[3 * kSliceDims + t];
+    p.out[h * kHeadDim + d0 + t] = (f16)r;
+  }
+}
+
+__global__ __launch_bounds__(256) void split_attention_kernel(AttnParams p) {
+  extern __shared__ float sc[];  // [capacity] scores, then probabilities (output workgroups)
+  if ((int)blockIdx.x < p.score_wgs) attention_scores_block(p, (int)blockIdx.x);
+  else attention_output_block(p, (int)blockIdx.x - p.score_wgs, sc);
 }
 
 // Greedy next token: first index of the largest logit (torch.argmax order), written to

@@ -27,6 +27,11 @@ NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
+def attention_workspace_bytes(heads, capacity):
+    """LB_ATTN_WORKSPACE_BYTES: tagged score words [heads][ceil(capacity / 48) * 16], launch count, timeout."""
+    return heads * ((capacity + 47) // 48) * 128 + 16
+
+
 FUSED_WORKSPACE_BYTES = 512  # LB_FUSED_WORKSPACE_BYTES: tagged z words [3][12] u64, launch count u64, timeout u32
 
 
@@ -73,7 +78,8 @@ class DecodeAttentionArgs(ctypes.Structure):
                 ('q', ctypes.c_void_p), ('k', ctypes.c_void_p), ('v', ctypes.c_void_p),
                 ('cos', ctypes.c_void_p), ('sin', ctypes.c_void_p), ('position', ctypes.c_void_p),
                 ('keys', ctypes.c_void_p), ('values', ctypes.c_void_p), ('out', ctypes.c_void_p),
-                ('scale', ctypes.c_float), ('reserved2', ctypes.c_uint32)]
+                ('scale', ctypes.c_float), ('reserved2', ctypes.c_uint32),
+                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
 
 
 _lib = None
@@ -463,9 +469,13 @@ def fused_linear(x, problems, **options):
 
 
 class PreparedAttention(_Prepared):
-    """lb_decode_attention for one token: q [heads*64], k, v [kv_heads*64], position int64 [1]."""
+    """lb_decode_attention for one token: q [heads*64], k, v [kv_heads*64], position int64 [1].
+    split (heads / kv_heads <= 3): scores computed once per 48 positions by dedicated workgroups,
+    through a zeroed workspace owned by this call; False (default): every output workgroup computes
+    the whole score row (no workspace), the faster form at the SmolLM cache sizes."""
 
-    def __init__(self, q, k, v, cos, sin, position, keys, values, out, *, heads, kv_heads, scale=0.125):
+    def __init__(self, q, k, v, cos, sin, position, keys, values, out, *, heads, kv_heads, scale=0.125,
+                 split=False):
         capacity = keys.shape[-2]
         a = DecodeAttentionArgs()
         a.struct_size = ctypes.sizeof(DecodeAttentionArgs)
@@ -479,9 +489,22 @@ class PreparedAttention(_Prepared):
         a.q, a.k, a.v, a.cos, a.sin = _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin)
         a.position, a.keys, a.values, a.out = _ptr(position), _ptr(keys), _ptr(values), _ptr(out)
         a.scale = scale
-        self._bind('lb_decode_attention', 'lb_decode_attention', a, q.device,
-                   [q, k, v, cos, sin, position, keys, values, out])
+        keep = [q, k, v, cos, sin, position, keys, values, out]
+        self.workspace = None
+        if split and heads // kv_heads <= 3:
+            size = attention_workspace_bytes(heads, capacity)
+            self.workspace = torch.zeros(size, dtype=torch.uint8, device=q.device)
+            a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+            keep.append(self.workspace)
+        self._bind('lb_decode_attention', 'lb_decode_attention', a, q.device, keep)
         self.out = out
+
+    def counters(self):
+        """(output workgroups counted over all calls so far, timeout word) of the split workspace."""
+        if self.workspace is None:
+            return None
+        tail = self.workspace[-16:]
+        return [int(tail[:8].view(torch.int64)), int(tail[8:12].view(torch.int32))]
 
 
 class PreparedArgmax:

@@ -559,14 +559,15 @@ class GraphDecoder:
     then RMSNorm -> tied fp16 lm_head (lb_fused_linear) and the greedy token with the next
     embedding (lb_argmax_next).  Projections of different formats (fp16-protected ones)
     get separate launches.  fused=False runs the same step as staged PyTorch-ROCm glue
-    around one lb_linear per projection.
+    around one lb_linear per projection.  shared_z (default) gives every fused launch with
+    corrections its own workspace, so each correction's z is computed once per launch.
     """
 
-    def __init__(self, stack, io, *, fused=True):
+    def __init__(self, stack, io, *, fused=True, shared_z=True):
         self.device = io.embedding.device
         if self.device.type != 'cuda':
             raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
-        self.stack, self.io, self.fused = stack, io, fused
+        self.stack, self.io, self.fused, self.shared_z = stack, io, fused, shared_z
         dev = self.device
         cap = stack.layers[0].capacity
         self.capacity = cap
@@ -609,7 +610,7 @@ class GraphDecoder:
                 first = lin[run[0][0]]
                 calls.append(lb.PreparedFused(x, [self._problem(lin[name], y, **extra) for name, y, extra in run],
                                               format=first['format'], K=first['K'], group_size=first['group'],
-                                              **options))
+                                              shared_z=self.shared_z, **options))
                 run.clear()
 
         for member in members:

@@ -125,6 +125,47 @@ typedef struct lb_decode_attention_args {
 lb_status lb_decode_attention(const lb_decode_attention_args *args, void *stream);
 
 /*
+ * One decoder layer for one token in one launch: RMSNorm -> q | k | v (+ corrections) -> RoPE, KV
+ * append, GQA attention -> o (+ correction) + residual -> RMSNorm -> gate | up (+ corrections) ->
+ * SiLU(gate) * up -> down (+ correction) + residual, with the staging of lb_fused_linear and
+ * lb_decode_attention.  The counterpart of the reference's one-graph-per-layer decode
+ * (torch_npu_smollm.py:195-340, FrozenSmolLayer.graph), replacing the five launches of those
+ * entry points with one: each stage runs in workgroups of its own that hand their outputs to the
+ * later stages through the workspace (bounded waits), and every workgroup fetches its weights at
+ * launch.  Limits: hidden = heads * 64 <= 640, intermediate <= 1536 (multiples of 32),
+ * heads / kv_heads <= 3, capacity <= 4096, ranks <= 32, one format and group for all seven
+ * projections (group_size 0: int8 per row; otherwise a power of two >= 32 dividing both K).
+ */
+typedef struct lb_decode_layer_args {
+  uint32_t struct_size;        /* sizeof(lb_decode_layer_args) */
+  uint32_t format;             /* lb_format of all seven projections */
+  int64_t group_size;          /* see above */
+  int64_t hidden, intermediate;
+  void *h;                     /* fp16 [hidden], 16-byte aligned: the layer input, replaced by its output */
+  const void *norm1, *norm2;   /* fp16 [hidden] RMSNorm weights, 16-byte aligned */
+  float eps;
+  uint32_t reserved;
+  lb_fused_problem proj[7];    /* q, k, v, o, gate, up, down: codes, scales, N, rank, down, up, up_ld
+                                  (N: hidden, 64 kv_heads, 64 kv_heads, hidden, intermediate,
+                                  intermediate, hidden); y, bias and residual must be NULL */
+  int64_t heads, kv_heads, capacity;
+  const void *cos, *sin;       /* fp16 [capacity, 64] RoPE tables */
+  const int64_t *position;     /* device scalar p: the new token's slot (outside 0..capacity-1 the cache is
+                                  left alone and the attention output is NaN) */
+  void *keys, *values;         /* fp16 [kv_heads, capacity, 64], 16-byte aligned; slot p is written */
+  float scale;                 /* attention score scale (0.125) */
+  uint32_t reserved2;
+  void *workspace;             /* LB_DECODE_LAYER_WORKSPACE_BYTES, 256-byte aligned, zero before its first use;
+                                  one per call configuration; calls sharing it must be ordered (one stream) */
+  size_t workspace_bytes;
+} lb_decode_layer_args;
+
+#define LB_DECODE_LAYER_WORKSPACE_BYTES(hidden, intermediate, kv_heads) \
+  ((size_t)8u * (size_t)(92 + ((hidden) + 128 * (kv_heads)) / 2 + (hidden) + (intermediate)))
+
+lb_status lb_decode_layer(const lb_decode_layer_args *args, void *stream);
+
+/*
  * Greedy step: t = first index of the largest logit (NaN logits are never chosen);
  * token[0] = t; if 0 <= position[0] < limit: tokens[position[0]] = t and position[0] += 1;
  * h_next = embedding[t] (fp16 [hidden]).  Replaces the host argmax and the next step's embedding

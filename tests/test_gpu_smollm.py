@@ -192,10 +192,12 @@ def test_varied_greedy_sequence_matches_oracle(device):
     assert report['max_abs_err'] < report['min_margin'] / 2
 
 
-@pytest.mark.parametrize('fused', [True, False])
-def test_graph_decoder_matches_eager(device, fused):
-    """The captured decode step reproduces the eager decode tokens and logits (4 layers, 24 steps)."""
-    announce('graph decoder', 'fused' if fused else 'staged')
+@pytest.mark.parametrize('mode', ['layer', 'fused', 'staged'])
+def test_graph_decoder_matches_eager(device, mode):
+    """The captured decode step reproduces the eager decode tokens and logits (4 layers, 24 steps):
+    one lb_decode_layer launch per layer, the five fused launches, or the staged glue."""
+    announce('graph decoder', mode)
+    fused = mode != 'staged'
     from torch_npu_smollm import GraphDecoder
     stack, io, _, _ = smollm_random.build(seed=5, layers=4, rank=32, theta=10000.0, capacity=96)
     io = io.to(device)
@@ -204,9 +206,11 @@ def test_graph_decoder_matches_eager(device, fused):
     x = io.embed_tokens(ids.to(device))
     h, caches = stack.prefill(x)
     first = int(io.logits(h[:, -1:])[0, 0].float().argmax())
-    decoder = GraphDecoder(stack, io, fused=fused)
+    decoder = GraphDecoder(stack, io, fused=fused, layer=mode == 'layer')
+    assert decoder.layer_kernel == (mode == 'layer')
     decoder.load(caches, first)
     rest = decoder.generate(23)
+    assert decoder.timeouts() == 0
     assert [first] + rest == tokens
     assert rel_l2(decoder.logits.view(-1), logits[23]) <= 1e-2
     with pytest.raises(ValueError):

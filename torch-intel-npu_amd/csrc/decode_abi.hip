@@ -8,6 +8,7 @@
 #include "../../include/lowbit_decode_hip.h"
 #include "abi_util.h"
 #include "lb_decode.h"
+#include "lb_layer.h"
 #include "lb_stream.h"
 
 using namespace lb;
@@ -582,3 +583,155 @@ lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embeddin
 }
 
 }  // extern "C"
+
+namespace {
+
+// Validation of lb_decode_layer_args; fills the kernel parameters on success.
+lb_status check_layer(const lb_decode_layer_args *a, LayerParams *out, int *fmt, bool *scaled, bool *ranked) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: args is NULL");
+  if (a->struct_size < sizeof(lb_decode_layer_args))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: struct_size %u < %zu", a->struct_size, sizeof(lb_decode_layer_args));
+  if (a->format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: unknown format %u", a->format);
+  const int64_t H = a->hidden, I = a->intermediate;
+  if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0 || a->heads / a->kv_heads > 3 ||
+      H != a->heads * kHeadDim || H > 640 || I < 32 || I > kFusedMaxK || I % 32 != 0)
+    return fail(LB_INVALID_ARGUMENT,
+                "lb_decode_layer: needs hidden = 64 heads <= 640, heads / kv_heads <= 3, intermediate a multiple of 32 "
+                "<= %d", kFusedMaxK);
+  if (a->capacity < 1 || a->capacity > 4096)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: capacity %lld outside 1..4096", (long long)a->capacity);
+  const bool dense = a->format == LB_FORMAT_FP16;
+  const int64_t g = a->group_size;
+  const bool per_row = a->format == LB_FORMAT_INT8 && g == 0;
+  if (!dense && !per_row && !(pow2(g) && g >= 32 && H % g == 0 && I % g == 0))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: group_size %lld must be 0 (int8 per row) or a power of two "
+                "(>= 32) dividing hidden and intermediate", (long long)g);
+  if (!a->h || !aligned(a->h, 16) || !a->norm1 || !aligned(a->norm1, 16) || !a->norm2 || !aligned(a->norm2, 16) ||
+      !std::isfinite(a->eps) || a->eps < 0)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: h, norm1, norm2 must be 16-byte aligned; eps finite >= 0");
+  if (!a->cos || !a->sin || !aligned(a->cos, 2) || !aligned(a->sin, 2) || !a->position || !aligned(a->position, 8) ||
+      !a->keys || !a->values || !aligned(a->keys, 16) || !aligned(a->values, 16) || !std::isfinite(a->scale))
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: attention buffers NULL or misaligned, or scale not finite");
+  const size_t need = LB_DECODE_LAYER_WORKSPACE_BYTES(H, I, a->kv_heads);
+  if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: workspace must be 256-byte aligned with %zu bytes", need);
+  const int64_t kv = a->kv_heads * kHeadDim;
+  const int64_t want_n[P_COUNT] = {H, kv, kv, H, I, I, H};
+  const char *names[P_COUNT] = {"q", "k", "v", "o", "gate", "up", "down"};
+  LayerParams p{};
+  bool any_rank = false;
+  const size_t row = kHeadDim * 2, cache = (size_t)a->kv_heads * a->capacity * row;
+  Range in[8 + 4 * P_COUNT];
+  int nin = 0;
+  in[nin++] = range_of(a->norm1, (size_t)H * 2, "norm1");
+  in[nin++] = range_of(a->norm2, (size_t)H * 2, "norm2");
+  in[nin++] = range_of(a->cos, (size_t)a->capacity * row, "cos");
+  in[nin++] = range_of(a->sin, (size_t)a->capacity * row, "sin");
+  in[nin++] = range_of(a->position, sizeof(int64_t), "position");
+  for (int i = 0; i < P_COUNT; ++i) {
+    const lb_fused_problem &q = a->proj[i];
+    const int64_t K = i == P_DOWN ? I : H;
+    if (q.N != want_n[i])
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s has N=%lld, expected %lld", names[i], (long long)q.N,
+                  (long long)want_n[i]);
+    if (q.y || q.bias || q.residual)
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: y, bias and residual must be NULL", names[i]);
+    if (!q.codes || !aligned(q.codes, 16) || (!dense && (!q.scales || !aligned(q.scales, 2))))
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: codes (16-byte aligned) and scales required", names[i]);
+    if (q.rank < 0 || q.rank > LB_FUSED_MAX_RANK)
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: rank %lld outside 0..32", names[i], (long long)q.rank);
+    if (q.rank > 0 && (!q.down || !q.up || !aligned(q.down, 16) || !aligned(q.up, 16) || q.up_ld < q.rank ||
+                       q.up_ld % 8 != 0))
+      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: correction needs 16-byte aligned down/up, up_ld %% 8 == 0",
+                  names[i]);
+    any_rank = any_rank || q.rank > 0;
+    const int64_t G = dense ? 1 : per_row ? 1 : K / g;
+    in[nin++] = range_of(q.codes, code_bytes(a->format, q.N, K), "codes");
+    in[nin++] = range_of(dense ? nullptr : q.scales, dense ? 0 : (size_t)(q.N * G * 2), "scales");
+    in[nin++] = range_of(q.rank ? q.down : nullptr, q.rank ? (size_t)(q.rank * K * 2) : 0, "down");
+    in[nin++] = range_of(q.rank ? q.up : nullptr, q.rank ? (size_t)((q.N - 1) * q.up_ld + q.rank) * 2 : 0, "up");
+    LayerProblem &d = p.prob[i];
+    d.codes = static_cast<const uint8_t *>(q.codes);
+    d.scales = static_cast<const f16 *>(q.scales);
+    d.down = q.rank ? static_cast<const f16 *>(q.down) : nullptr;
+    d.up = q.rank ? static_cast<const f16 *>(q.up) : nullptr;
+    d.N = (int)q.N;
+    d.rank = (int)q.rank;
+    d.up_ld = (int)q.up_ld;
+  }
+  const Range outs[] = {range_of(a->h, (size_t)H * 2, "h"), range_of(a->keys, cache, "keys"),
+                        range_of(a->values, cache, "values"), range_of(a->workspace, need, "workspace")};
+  for (int o = 0; o < 4; ++o) {
+    for (int r = 0; r < nin; ++r)
+      if (overlaps(outs[o], in[r])) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s overlaps %s", outs[o].name, in[r].name);
+    for (int r = o + 1; r < 4; ++r)
+      if (overlaps(outs[o], outs[r])) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s overlaps %s", outs[o].name, outs[r].name);
+  }
+  p.h = static_cast<f16 *>(a->h);
+  p.norm1 = static_cast<const f16 *>(a->norm1);
+  p.norm2 = static_cast<const f16 *>(a->norm2);
+  p.eps = a->eps;
+  p.hidden = (int)H;
+  p.inter = (int)I;
+  p.per_row = per_row;
+  const int64_t g1 = dense || per_row ? H : g, g2 = dense || per_row ? I : g;
+  p.G1 = (int)(H / g1);
+  p.shift1 = shift_of(g1, H);
+  p.G2 = (int)(I / g2);
+  p.shift2 = shift_of(g2, I);
+  p.cos = static_cast<const f16 *>(a->cos);
+  p.sin = static_cast<const f16 *>(a->sin);
+  p.position = a->position;
+  p.keys = static_cast<f16 *>(a->keys);
+  p.values = static_cast<f16 *>(a->values);
+  p.heads = (int)a->heads;
+  p.kv_heads = (int)a->kv_heads;
+  p.capacity = (int)a->capacity;
+  p.scale = a->scale;
+  p.ws = static_cast<uint64_t *>(a->workspace);
+  p.w_z = 8;
+  p.w_qkv = p.w_z + P_COUNT * kLayerZWords;
+  p.w_att = p.w_qkv + (int)((H + 2 * kv) / 2);
+  p.w_h1 = p.w_att + (int)(H / 2);
+  p.w_gu = p.w_h1 + (int)(H / 2);
+  auto zc = [&](int i) { return (p.prob[i].rank + kFusedZRanks - 1) / kFusedZRanks; };
+  auto tc = [&](int i) { return (p.prob[i].N + 15) / 16; };
+  const int counts[R_COUNT] = {zc(P_Q) + zc(P_K) + zc(P_V), tc(P_Q) + tc(P_K) + tc(P_V), (int)a->heads * kAttnDimSlices,
+                               zc(P_O), tc(P_O), zc(P_GATE) + zc(P_UP), tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};
+  int acc = 0;
+  for (int r = 0; r < R_COUNT; ++r) p.end[r] = acc += counts[r];
+  *out = p;
+  *fmt = (int)a->format;
+  *scaled = !dense && !per_row;
+  *ranked = any_rank;
+  return ok();
+}
+
+template <int FMT, bool SCALED>
+void launch_layer_t(const LayerParams &p, bool ranked, size_t smem, hipStream_t s) {
+  const dim3 grid((unsigned)p.end[R_COUNT - 1]);
+  if (ranked) hipLaunchKernelGGL((decode_layer_kernel<FMT, SCALED, true>), grid, dim3(256), smem, s, p);
+  else hipLaunchKernelGGL((decode_layer_kernel<FMT, SCALED, false>), grid, dim3(256), smem, s, p);
+}
+
+}  // namespace
+
+extern "C" lb_status lb_decode_layer(const lb_decode_layer_args *a, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_decode_layer"); bad != LB_OK) return bad;
+  LayerParams p;
+  int fmt;
+  bool scaled, ranked;
+  const lb_status st = check_layer(a, &p, &fmt, &scaled, &ranked);
+  if (st != LB_OK) return st;
+  // Dynamic LDS: the largest role (a 1536-long tile: staged row, scales, U rows, reductions, NF4
+  // table) or the attention (its rows and one float per cache slot).
+  const size_t smem = std::max<size_t>(9216, 1024 + (size_t)4 * p.capacity);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (fmt) {
+    case FMT_INT8: scaled ? launch_layer_t<FMT_INT8, true>(p, ranked, smem, s) : launch_layer_t<FMT_INT8, false>(p, ranked, smem, s); break;
+    case FMT_INT4: launch_layer_t<FMT_INT4, true>(p, ranked, smem, s); break;
+    case FMT_NF4: launch_layer_t<FMT_NF4, true>(p, ranked, smem, s); break;
+    default: launch_layer_t<FMT_FP16, false>(p, ranked, smem, s); break;
+  }
+  return launch_status("lb_decode_layer");
+}

@@ -51,6 +51,34 @@ __device__ __forceinline__ f16 rope_element(float x, float r, float c, float s) 
 // long-K variants (one-row lb_linear calls) need group >= 64.
 template <int KMAX> struct FusedGroupMin { static constexpr int value = KMAX <= 1536 ? 32 : 64; };
 
+// The correction term d = sum_r z[r] * U[row][r] (fp32, r in order), eight ranks per step.  zs
+// and the staged U row must be zero from rank up to the next multiple of eight.
+__device__ __forceinline__ float correction_dot(const float *zs, const f16 *urow, int rank) {
+  float d = 0.0f;
+#pragma unroll
+  for (int r8 = 0; r8 < kFusedMaxRank / 8; ++r8) {
+    if (8 * r8 < rank) {
+      const h8 u = *reinterpret_cast<const h8 *>(urow + 8 * r8);
+      const f4 z0 = *reinterpret_cast<const f4 *>(zs + 8 * r8);
+      const f4 z1 = *reinterpret_cast<const f4 *>(zs + 8 * r8 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d += z0[e] * (float)u[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d += z1[e] * (float)u[4 + e];
+    }
+  }
+  return d;
+}
+
+// Stages a lane's 8-column piece of a U row (columns 8 uq .. 8 uq + 7), zero from column rank on.
+__device__ __forceinline__ void stage_u_piece(f16 *dst, const u4 &piece, int uq, int rank) {
+  h8 u = __builtin_bit_cast(h8, piece);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (8 * uq + e >= rank) u[e] = (f16)0.0f;
+  *reinterpret_cast<h8 *>(dst) = u;
+}
+
 // The prologue's scale factor: inv = 1 / sqrt(mean(x^2) + eps) for RMSNorm (1 otherwise), summed in
 // the same order by every workgroup of a launch (thread, wave, then the four waves), so all of them
 // stage the same row.  Contains a workgroup barrier when the prologue is RMSNorm.
@@ -198,10 +226,12 @@ __device__ __forceinline__ void wait_shared_z(const FusedParams &p, int pi, int 
     if (ready) break;
     __builtin_amdgcn_s_sleep(1);
   }
-  if (lane < words) {
+  if (lane < kFusedZWordsPerProblem) {  // every zs entry, zero from rank on
 #pragma unroll
     for (int e = 0; e < 3; ++e)
-      if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = (float)__builtin_bit_cast(f16, (uint16_t)(word >> (16 * (e + 1))));
+      if (3 * lane + e < kFusedMaxRank)
+        zs[3 * lane + e] =
+            3 * lane + e < rank ? (float)__builtin_bit_cast(f16, (uint16_t)(word >> (16 * (e + 1)))) : 0.0f;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the LDS writes above precede the wave's reads
   __builtin_amdgcn_wave_barrier();
@@ -246,7 +276,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
   __shared__ __align__(16) f16 us[RANKED ? 16 * kFusedMaxRank : 8];  // U rows of the tile
   __shared__ f16 es[3 * 16];                      // residual, bias, per-row scale of the tile
-  __shared__ float zs[kFusedMaxRank];
+  __shared__ __align__(16) float zs[kFusedMaxRank];
   __shared__ float red[(KG - 1) * 16];
   __shared__ float wsum[4];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
@@ -341,7 +371,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
   if (lane < 16 && wave < 3) es[wave * 16 + lane] = ev;
   if constexpr (RANKED) {
-    if (lane < 16) *reinterpret_cast<u4 *>(us + (4 * wave + (lane >> 2)) * kFusedMaxRank + (lane & 3) * 8) = ureg;
+    if (lane < 16) stage_u_piece(us + (4 * wave + (lane >> 2)) * kFusedMaxRank + (lane & 3) * 8, ureg, lane & 3, rank);
   }
   const float inv = prologue_inv(p, xv, wsum, lane, wave);
 #pragma unroll
@@ -417,8 +447,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   f16 h = (f16)sum;
   if (P.bias) h = (f16)((float)h + (float)es[16 + j]);
   if (RANKED && rank > 0) {
-    float d = 0.0f;
-    for (int r = 0; r < rank; ++r) d += zs[r] * (float)us[j * kFusedMaxRank + r];
+    const float d = correction_dot(zs, us + j * kFusedMaxRank, rank);
     h = (f16)((float)h + (float)(f16)d);
   }
   if (P.residual) h = (f16)((float)es[j] + (float)h);

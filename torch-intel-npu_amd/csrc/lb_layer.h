@@ -1,0 +1,682 @@
+// One SmolLM decoder layer for one token in one launch (lb_decode_layer).
+//
+// The five launches of the fused decode step (RMSNorm -> q|k|v, RoPE + attention, o + residual,
+// RMSNorm -> gate|up, SiLU * up -> down + residual) become workgroup roles of one grid, in this
+// dispatch order:
+//
+//   Z_QKV  correction activations z of q, k, v      T_QKV  q | k | v tiles (16 rows each)
+//   ATTN   RoPE, KV append, attention (head, dims)   Z_O / T_O    o projection + residual
+//   Z_GU / T_GU  gate | up                           Z_D / T_D    down projection + residual
+//
+// A role hands its output to later roles through the workspace as tagged 64-bit words (two fp16
+// values and the launch's 16-bit tag; the correction activations three to a word), written and
+// read with system-scope atomics, which are performed at the memory side past the per-XCD L2s.
+// A consumer waits (bounded) on one word of its source, chosen by its workgroup index so the
+// consumers of a stage poll different addresses, then reads the words it needs and re-reads any
+// whose tag is not yet current.  Every
+// workgroup issues its weight, scale, U-row and KV-cache loads at launch, so while it waits its
+// data arrives.  A workgroup only ever waits for workgroups of earlier roles, which the hardware
+// dispatches before it, so every wait ends.
+//
+// The launch's tag is (passed / workgroups + 1) mod 2^16: every workgroup reads `passed` at its
+// start and raises it once at its end, so at any start it holds launch * workgroups plus fewer
+// than `workgroups`, and no word is ever cleared (the previous launch's tag is one behind).
+//
+// Arithmetic and fp16 rounding points are those of the fused decode kernels (the reference's
+// CPU layer, torch_npu_smollm.py:142-193): the prologues, the MFMA products with fp32
+// accumulation, z = fp16(x'.V^T), d = fp16(z.U^T), y = fp16(fp16(main) + d), the residual adds,
+// and the attention staging of decode_attention_kernel.
+#pragma once
+#include "lb_decode.h"
+
+namespace lb {
+
+enum LayerRole { R_ZQKV, R_TQKV, R_ATTN, R_ZO, R_TO, R_ZGU, R_TGU, R_ZD, R_TD, R_COUNT };
+enum LayerProj { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, P_COUNT };
+enum LayerSource { SRC_H, SRC_ATT, SRC_H1, SRC_GU };
+
+struct LayerProblem {
+  const uint8_t *codes;   // packed codes [N, K] (fp16 weights for FMT_FP16)
+  const f16 *scales;      // [N, G]
+  const f16 *down;        // V [rank, K] or null
+  const f16 *up;          // U [N, up_ld] or null
+  int N, rank, up_ld;
+};
+
+struct LayerParams {
+  f16 *h;                   // [hidden] residual row: the layer's input, overwritten by its output
+  const f16 *norm1, *norm2; // [hidden] RMSNorm weights
+  float eps;
+  int hidden, inter;        // K of q/k/v/o/gate/up, K of down
+  int G1, shift1, G2, shift2, per_row;
+  LayerProblem prob[P_COUNT];
+  const f16 *cos, *sin;     // [capacity, 64]
+  const int64_t *position;  // device scalar: the slot of the new token
+  f16 *keys, *values;       // [kv_heads, capacity, 64]
+  int heads, kv_heads, capacity;
+  float scale;
+  uint64_t *ws;             // workspace words: [0] passed, [1] timeout, then the regions below
+  int w_z, w_qkv, w_att, w_h1, w_gu;
+  int end[R_COUNT];         // exclusive prefix sums of workgroups per role
+};
+
+constexpr int kLayerSpinLimit = 1 << 18;
+constexpr int kLayerZWords = 12;  // z words per problem (6 ranks per z workgroup, three per word)
+
+__device__ __forceinline__ uint64_t sys_load(const uint64_t *a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void sys_store(uint64_t *a, uint64_t v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w & 0xFFFF); }
+__device__ __forceinline__ f16 word_half(uint64_t w, int e) {
+  return __builtin_bit_cast(f16, (uint16_t)(w >> (16 * (e + 1))));
+}
+__device__ __forceinline__ uint64_t pair_word(uint32_t tag, f16 a, f16 b) {
+  return (uint64_t)tag | ((uint64_t)__builtin_bit_cast(uint16_t, a) << 16) |
+         ((uint64_t)__builtin_bit_cast(uint16_t, b) << 32);
+}
+
+// The launch's tag from `passed` as read at the workgroup's start.
+__device__ __forceinline__ uint32_t layer_tag(const LayerParams &p, uint64_t passed) {
+  return (uint32_t)((passed / (uint32_t)p.end[R_COUNT - 1] + 1) & 0xFFFF);
+}
+
+__device__ __forceinline__ void layer_timeout(const LayerParams &p) {
+  __hip_atomic_store(reinterpret_cast<uint32_t *>(p.ws + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// A word whose tag is current (bounded wait; a timeout is recorded and the stale word returned).
+__device__ __forceinline__ uint64_t wait_word(const LayerParams &p, const uint64_t *a, uint32_t tag) {
+  uint64_t w = sys_load(a);
+  for (int it = 0; word_tag(w) != tag; ++it) {
+    if (it == kLayerSpinLimit) {
+      layer_timeout(p);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    w = sys_load(a);
+  }
+  return w;
+}
+
+// Thread 0 waits for the sentinel word, then the whole workgroup proceeds.
+__device__ __forceinline__ void wait_sentinel(const LayerParams &p, const uint64_t *a, uint32_t tag) {
+  if (threadIdx.x == 0) (void)wait_word(p, a, tag);
+  __syncthreads();
+}
+
+// Eight consecutive values (four pair words) of a word region, each word waited for.
+__device__ __forceinline__ h8 read_block_words(const LayerParams &p, const uint64_t *a, uint32_t tag) {
+  h8 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint64_t w = wait_word(p, a + q, tag);
+    v[2 * q] = word_half(w, 0);
+    v[2 * q + 1] = word_half(w, 1);
+  }
+  return v;
+}
+
+// The source row of a role's products (K values, 8 per block, thread t holding blocks t + 256 i)
+// and the prologue's second row (gamma, or the up half for SiLU-multiply).
+template <int XB>
+__device__ __forceinline__ void layer_source_row(const LayerParams &p, int src, int K, uint32_t tag, h8 (&xv)[XB],
+                                                 h8 (&av)[XB]) {
+  const int t = threadIdx.x, blocks = K >> 3;
+  const uint64_t *base = p.ws + (src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu);
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    if (b < blocks) {
+      xv[i] = read_block_words(p, base + 4 * b, tag);
+      if (src == SRC_GU) av[i] = read_block_words(p, base + p.inter / 2 + 4 * b, tag);
+    } else {
+      xv[i] = h8{};
+      if (src == SRC_GU) av[i] = h8{};
+    }
+  }
+}
+
+// The word a consumer of a word source polls before reading the rest: one chosen by the
+// workgroup's index, so the consumers of a stage spread their polls over the stage's words
+// instead of all polling one address.
+__device__ __forceinline__ const uint64_t *source_sentinel(const LayerParams &p, int src) {
+  const int words = src == SRC_GU ? p.inter : p.hidden / 2;
+  const int base = src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu;
+  return p.ws + base + (int)((blockIdx.x * 37u) % (unsigned)words);
+}
+
+__device__ __forceinline__ float layer_inv(int prologue, int K, float eps, float sumsq_total) {
+  return prologue == PRO_RMSNORM ? 1.0f / sqrtf(sumsq_total / (float)K + eps) : 1.0f;
+}
+
+// RMS of the source row with the fused kernels' order (thread, wave, four waves).
+template <int XB>
+__device__ __forceinline__ float layer_prologue_inv(int prologue, int K, float eps, const h8 (&xv)[XB], float *wsum) {
+  if (prologue != PRO_RMSNORM) return 1.0f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < XB; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)xv[i][e] * (float)xv[i][e];
+  s = wave_sum(s);
+  if (lane == 0) wsum[wave] = s;
+  __syncthreads();
+  const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  return layer_inv(prologue, K, eps, total);
+}
+
+__device__ __forceinline__ h8 layer_prologue_apply(int prologue, const h8 &x, const h8 &a, float inv) {
+  h8 v;
+  if (prologue == PRO_RMSNORM) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)x[e] * inv) * (float)a[e]);
+  } else if (prologue == PRO_SILU_MUL) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)x[e]) * (float)a[e]);
+  } else {
+    v = x;
+  }
+  return v;
+}
+
+// The source, prologue and K of each GEMV role.
+struct RoleShape {
+  int src, prologue, K;
+  const f16 *gamma;
+};
+__device__ __forceinline__ RoleShape role_shape(const LayerParams &p, int pi) {
+  if (pi <= P_V) return {SRC_H, PRO_RMSNORM, p.hidden, p.norm1};
+  if (pi == P_O) return {SRC_ATT, PRO_NONE, p.hidden, nullptr};
+  if (pi <= P_UP) return {SRC_H1, PRO_RMSNORM, p.hidden, p.norm2};
+  return {SRC_GU, PRO_SILU_MUL, p.inter, nullptr};
+}
+
+// Loads the plain source row (the layer input h) and the prologue's gamma row, straight-line.
+template <int XB>
+__device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const RoleShape &rs, h8 (&xv)[XB],
+                                                  h8 (&av)[XB]) {
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x, blocks = rs.K >> 3;
+  const size_t kb = (size_t)rs.K * 2;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.h, rs.src == SRC_H ? kb : 0);
+  const __amdgpu_buffer_rsrc_t gbuf = buffer_rsrc(rs.gamma, rs.gamma ? kb : 0);
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    xv[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xbuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+    av[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(gbuf, b < blocks ? b * 16 : kOutOfRange, 0, 0));
+  }
+}
+
+// ---------------------------------------------------------------- z workgroups
+// Ranks [6 zi, 6 zi + 6) of problem pi: z = fp16(x'.V^T), published as two tagged words.
+template <int KMAX>
+__device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int zi, uint64_t passed, f16 *xs,
+                                             float *wsum, f16 *zsh) {
+  constexpr int TPR = 32;
+  constexpr int ZI = (KMAX / 8 + TPR - 1) / TPR;
+  constexpr int XB = (KMAX / 8 + 255) / 256;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x;
+  const RoleShape rs = role_shape(p, pi);
+  const LayerProblem &Z = p.prob[pi];
+  const int K = rs.K, blocks = K >> 3;
+  const int r0 = zi * kFusedZRanks;
+  const int rr = t / TPR, li = t % TPR;
+  const bool live = rr < kFusedZRanks && r0 + rr < Z.rank;
+  h8 xv[XB], av[XB];
+  layer_plain_loads(p, rs, xv, av);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(Z.down, (size_t)Z.rank * K * 2);
+  u4 vz[ZI];
+#pragma unroll
+  for (int i = 0; i < ZI; ++i) {
+    const int blk = li + TPR * i;
+    const int off = live && blk < blocks ? ((r0 + rr) * K + blk * 8) * 2 : kOutOfRange;
+    vz[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tag = layer_tag(p, passed);
+  if (rs.src != SRC_H) {
+    h8 gamma_rows[XB];
+#pragma unroll
+    for (int i = 0; i < XB; ++i) gamma_rows[i] = av[i];
+    wait_sentinel(p, source_sentinel(p, rs.src), tag);
+    layer_source_row(p, rs.src, K, tag, xv, av);
+    if (rs.src != SRC_GU) {
+#pragma unroll
+      for (int i = 0; i < XB; ++i) av[i] = gamma_rows[i];
+    }
+  }
+  const float inv = layer_prologue_inv(rs.prologue, K, p.eps, xv, wsum);
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int blk = t + 256 * i;
+    if (blk < blocks) *reinterpret_cast<h8 *>(xs + blk * 8) = layer_prologue_apply(rs.prologue, xv[i], av[i], inv);
+  }
+  __syncthreads();
+  float acc = 0.0f, acc2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ZI; ++i) {
+    const int blk = li + TPR * i;
+    if (blk < blocks) {
+      asm volatile("" : "+v"(vz[i]));
+      const h8 vv = __builtin_bit_cast(h8, vz[i]);
+      const h8 xx = *reinterpret_cast<const h8 *>(xs + blk * 8);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        acc += (float)xx[e] * (float)vv[e];
+        acc2 += (float)xx[e + 1] * (float)vv[e + 1];
+      }
+    }
+  }
+  acc += acc2;
+#pragma unroll
+  for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (li == 0 && rr < kFusedZRanks) zsh[rr] = live ? (f16)acc : (f16)0.0f;
+  __syncthreads();
+  if (t < 2) {
+    const uint64_t word = (uint64_t)tag | ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t]) << 16) |
+                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 1]) << 32) |
+                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 2]) << 48);
+    sys_store(p.ws + p.w_z + pi * kLayerZWords + 2 * zi + t, word);
+  }
+}
+
+// ---------------------------------------------------------------- GEMV tiles
+// Rows [n0, n0 + 16) of problem pi, with the fused decode kernel's product and epilogue.  Output:
+// q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
+// residual h1).
+template <int FMT, bool SCALED, int KMAX, bool RANKED>
+__device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, int n0, uint64_t passed, uint8_t *smem) {
+  constexpr int CPL = FormatTraits<FMT>::CPL;
+  constexpr int BITS = FormatTraits<FMT>::BITS;
+  constexpr int KSTEP = 4 * CPL;
+  constexpr int KG = 4;
+  constexpr int WSTEP = KG * KSTEP;
+  constexpr int D = (KMAX + WSTEP - 1) / WSTEP;
+  static_assert(D <= 32, "KMAX too long for this format");
+  constexpr int T8 = CPL / 8;
+  constexpr int XLD = KMAX + KSTEP + 8;
+  constexpr int XB = (KMAX / 8 + 255) / 256;
+  constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;
+  constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  f16 *xs = reinterpret_cast<f16 *>(smem);                                  // [XLD]
+  f16 *ss = xs + XLD;                                                       // [16 GMAX + 8]
+  f16 *us = ss + (SCALED ? 16 * GMAX + 8 : 8);                              // [16 * 32]
+  float *zs = reinterpret_cast<float *>(us + 16 * kFusedMaxRank);           // [32]
+  float *red = zs + kFusedMaxRank;                                          // [48]
+  float *wsum = red + (KG - 1) * 16;                                        // [4]
+  uint32_t *nf4_table = reinterpret_cast<uint32_t *>(wsum + 4);             // [256]
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const RoleShape rs = role_shape(p, pi);
+  const LayerProblem &P = p.prob[pi];
+  const int K = rs.K;
+  const int G = K == p.hidden ? p.G1 : p.G2;
+  const int group_shift = K == p.hidden ? p.shift1 : p.shift2;
+  const int rows = min(16, P.N - n0);
+  const int row_bytes = K * BITS / 8;
+  const int rank = RANKED ? P.rank : 0;
+
+  // Wave 0, lane r < rows: the row's per-row scale and (o) its residual h value.
+  const f16 rscale = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(P.scales, p.per_row && wave == 0 ? (size_t)P.N * 2 : 0),
+                                                lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
+  const f16 rres = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.h, pi == P_O && wave == 0 ? (size_t)P.N * 2 : 0),
+                                                lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
+  u4 ureg = {0u, 0u, 0u, 0u};
+  if constexpr (RANKED) {
+    const int ur = 4 * wave + (lane >> 2), uq = lane & 3;
+    const int off = lane < 16 && ur < rows && uq * 8 < rank ? ((n0 + ur) * P.up_ld + uq * 8) * 2 : kOutOfRange;
+    ureg = __builtin_bit_cast(
+        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(P.up, rank > 0 ? (size_t)P.N * P.up_ld * 2 : 0), off, 0, 0));
+  }
+  h8 xv[XB], av[XB];
+  layer_plain_loads(p, rs, xv, av);
+  f16 sreg[SC > 0 ? SC : 1];
+  if constexpr (SCALED) {
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)n0 * G, (size_t)rows * G * 2);
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
+  }
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(P.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  u4 w[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int k = (wave + KG * u) * KSTEP + g * CPL;
+    const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
+    w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tag = layer_tag(p, passed);
+
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
+  if constexpr (RANKED) {
+    if (lane < 16) stage_u_piece(us + (4 * wave + (lane >> 2)) * kFusedMaxRank + (lane & 3) * 8, ureg, lane & 3, rank);
+  }
+  if constexpr (SCALED) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i)
+      if (t + i * 256 < 16 * GMAX) ss[t + i * 256] = sreg[i];
+    if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;
+  }
+  // The source row: the layer input (loaded above) or the words of an earlier role.
+  if (rs.src != SRC_H) {
+    h8 gamma_rows[XB];
+#pragma unroll
+    for (int i = 0; i < XB; ++i) gamma_rows[i] = av[i];
+    wait_sentinel(p, source_sentinel(p, rs.src), tag);
+    layer_source_row(p, rs.src, K, tag, xv, av);
+    if (rs.src != SRC_GU) {
+#pragma unroll
+      for (int i = 0; i < XB; ++i) av[i] = gamma_rows[i];
+    }
+  }
+  const float inv = layer_prologue_inv(rs.prologue, K, p.eps, xv, wsum);
+  const int blocks = K >> 3;
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    if (b < blocks) *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(layer_prologue_apply(rs.prologue, xv[i], av[i], inv));
+  }
+  const int zero_end = min(XLD, K + KSTEP + 8);
+  for (int b = blocks + t; b * 8 < zero_end; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  __syncthreads();
+
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const f16 *a0 = xs + g * CPL;
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int kb = (wave + KG * u) * KSTEP;
+    if (kb >= K) break;
+    asm volatile("" : "+v"(w[u]));
+    h2 s2 = {(f16)1.0f, (f16)1.0f};
+    if constexpr (SCALED) {
+      const f16 sc = ss[j * G + ((kb + g * CPL) >> group_shift)];
+      s2 = h2{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < T8; ++q) {
+      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
+      const h8 b = decode8<FMT, !SCALED>(w[u], q, s2, nf4_table);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+  if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
+  __syncthreads();
+  if (wave != 0) return;
+
+  // ---- epilogue: wave 0; lane j < rows owns row n0 + j ----
+  if constexpr (RANKED) {
+    if (rank > 0) {
+      const int words = (rank + 2) / 3;
+      const uint64_t *zw = p.ws + p.w_z + pi * kLayerZWords;
+      if (lane < kFusedZWordsPerProblem) {  // every zs entry, zero from rank on
+        const uint64_t word = lane < words ? wait_word(p, zw + lane, tag) : 0;
+#pragma unroll
+        for (int e = 0; e < 3; ++e)
+          if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = 3 * lane + e < rank ? (float)word_half(word, e) : 0.0f;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  f16 residual = rres;
+  if (pi == P_DOWN && lane < rows)  // h1 is final: the gate|up words this tile read depend on it
+    residual = word_half(wait_word(p, p.ws + p.w_h1 + (n0 + lane) / 2, tag), (n0 + lane) & 1);
+  float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
+  if (p.per_row) sum *= (float)rscale;
+  f16 hv = (f16)sum;
+  if (RANKED && rank > 0) {
+    const float d = correction_dot(zs, us + j * kFusedMaxRank, rank);
+    hv = (f16)((float)hv + (float)(f16)d);
+  }
+  if (pi == P_O || pi == P_DOWN) hv = (f16)((float)residual + (float)hv);
+  const f16 next = __builtin_bit_cast(f16, (uint16_t)__shfl(__builtin_bit_cast(uint16_t, hv), lane + 1, 64));
+  if (g != 0 || j >= rows) return;
+  if (pi == P_DOWN) {
+    p.h[n0 + j] = hv;
+    return;
+  }
+  if (j & 1) return;
+  int region, off;
+  if (pi <= P_V) {
+    region = p.w_qkv;
+    off = pi == P_Q ? 0 : pi == P_K ? p.prob[P_Q].N : p.prob[P_Q].N + p.prob[P_K].N;
+  } else if (pi == P_O) {
+    region = p.w_h1;
+    off = 0;
+  } else {
+    region = p.w_gu;
+    off = pi == P_GATE ? 0 : p.inter;
+  }
+  sys_store(p.ws + region + (off + n0 + j) / 2, pair_word(tag, hv, next));
+}
+
+// ---------------------------------------------------------------- attention
+// Query head h, output dims [d0, d0 + kSliceDims): the staging of decode_attention_kernel on q, k
+// and v rows read from the q|k|v words; the output dims are published as att words.
+__device__ __forceinline__ void layer_attention_role(const LayerParams &p, int idx, uint64_t passed, uint8_t *smem) {
+  f16 *qs = reinterpret_cast<f16 *>(smem);               // [64] raw, then rotated
+  f16 *kn = qs + kHeadDim;                               // [64]
+  f16 *vn = kn + kHeadDim;                               // [64]
+  f16 *raw = vn + kHeadDim;                              // [128] raw q and k rows
+  float *wred = reinterpret_cast<float *>(raw + 2 * kHeadDim);  // [4]
+  float *pv = wred + 4;                                  // [4 * kSliceDims]
+  float *sc = pv + 4 * kSliceDims;                       // [capacity]
+  constexpr int kOutOfRange = (int)0x80000000u;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int h = idx / kAttnDimSlices;
+  const int d0 = (idx % kAttnDimSlices) * kSliceDims;
+  const int group = p.heads / p.kv_heads;
+  const int kvh = h / group;
+  const int pos = (int)p.position[0];
+  const bool valid = pos >= 0 && pos < p.capacity;
+  const int cpos = valid ? pos : 0;
+  const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
+  // Cached rows (slots below pos) and the RoPE row, issued before the wait for q, k, v.
+  const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(p.keys + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(p.values + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
+  const int blk = t % kSliceBlocks, part = t / kSliceBlocks;
+  u4 kreg[kScoreSlots][kHeadDim / 8];
+  u4 vreg[kValueSlots];
+  auto load_keys = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < kScoreSlots; ++i) {
+      const int s = base + t + 256 * i;
+#pragma unroll
+      for (int b = 0; b < kHeadDim / 8; ++b)
+        kreg[i][b] = __builtin_bit_cast(
+            u4, __builtin_amdgcn_raw_buffer_load_b128(kbuf, s < pos ? (s * kHeadDim + 8 * b) * 2 : kOutOfRange, 0, 0));
+    }
+  };
+  auto load_values = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      vreg[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, s < pos ? (s * kHeadDim + d0 + 8 * blk) * 2 : kOutOfRange, 0, 0));
+    }
+  };
+  load_keys(0);
+  load_values(0);
+  const int d = lane;
+  const __amdgpu_buffer_rsrc_t cbuf = buffer_rsrc(p.cos + (size_t)cpos * kHeadDim, wave < 2 ? kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t snbuf = buffer_rsrc(p.sin + (size_t)cpos * kHeadDim, wave < 2 ? kHeadDim * 2 : 0);
+  const f16 cv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(cbuf, d * 2, 0, 0));
+  const f16 sv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(snbuf, d * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tag = layer_tag(p, passed);
+
+  // q of head h, k and v of KV head kvh: 96 words from the q|k|v region.
+  const int nq = p.prob[P_Q].N, nk = p.prob[P_K].N;
+  const uint64_t *qkv = p.ws + p.w_qkv;
+  wait_sentinel(p, qkv + (nq + nk + (kvh + 1) * kHeadDim) / 2 - 1, tag);
+  if (t < 3 * kHeadDim / 2) {
+    const int part3 = t / (kHeadDim / 2), wi = t % (kHeadDim / 2);
+    const int first = part3 == 0 ? h * kHeadDim : part3 == 1 ? nq + kvh * kHeadDim : nq + nk + kvh * kHeadDim;
+    const uint64_t word = wait_word(p, qkv + first / 2 + wi, tag);
+    f16 *dst = part3 == 0 ? raw : part3 == 1 ? raw + kHeadDim : vn;
+    dst[2 * wi] = word_half(word, 0);
+    dst[2 * wi + 1] = word_half(word, 1);
+  }
+  __syncthreads();
+  if (wave < 2) {
+    const f16 *src = raw + wave * kHeadDim;
+    const float x0 = (float)src[d], x1 = (float)src[d ^ 32];
+    const float rot = d < 32 ? -x1 : x1;
+    const f16 r = rope_element(x0, rot, (float)cv, (float)sv);
+    if (wave == 0) qs[d] = r; else kn[d] = r;
+  }
+  __syncthreads();
+  if (!valid) {
+    if (t < kSliceDims) {
+      f16 nan = (f16)__builtin_nanf("");
+      if ((t & 1) == 0)
+        sys_store(p.ws + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, nan, nan));
+    }
+    return;
+  }
+  if (h % group == 0 && idx % kAttnDimSlices == 0 && t < 2 * kHeadDim) {
+    const int dd = t & 63;
+    f16 *dst = (t < kHeadDim ? p.keys : p.values) + head_base + (size_t)pos * kHeadDim + dd;
+    *dst = t < kHeadDim ? kn[dd] : vn[dd];
+  }
+
+  float lmax = -INFINITY;
+  for (int base = 0; base <= pos; base += 256 * kScoreSlots) {
+    if (base > 0) load_keys(base);
+#pragma unroll
+    for (int i = 0; i < kScoreSlots; ++i) {
+      const int s = base + t + 256 * i;
+      if (base + 256 * i > pos) break;
+      float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+      for (int b = 0; b < kHeadDim / 8; ++b) {
+        asm volatile("" : "+v"(kreg[i][b]));
+        const h8 qq = *reinterpret_cast<const h8 *>(qs + 8 * b);
+        const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * b) : __builtin_bit_cast(h8, kreg[i][b]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          acc0 += (float)qq[e] * (float)kk[e];
+          acc1 += (float)qq[e + 1] * (float)kk[e + 1];
+        }
+      }
+      if (s <= pos) {
+        const float v = (float)(f16)((float)(f16)(acc0 + acc1) * p.scale);
+        sc[s] = v;
+        lmax = fmaxf(lmax, v);
+      }
+    }
+  }
+  lmax = wave_max(lmax);
+  if (lane == 0) wred[wave] = lmax;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float lsum = 0.0f;
+  for (int s = t; s <= pos; s += 256) {
+    const float e = expf(sc[s] - m);
+    sc[s] = e;
+    lsum += e;
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();
+  if (lane == 0) wred[wave] = lsum;
+  __syncthreads();
+  const float total = ((wred[0] + wred[1]) + wred[2]) + wred[3];
+  for (int s = t; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
+  __syncthreads();
+
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base <= pos; base += kAttnParts * kValueSlots) {
+    if (base > 0) load_values(base);
+#pragma unroll
+    for (int i = 0; i < kValueSlots; ++i) {
+      const int s = base + part + kAttnParts * i;
+      if (base + kAttnParts * i > pos) break;
+      asm volatile("" : "+v"(vreg[i]));
+      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + d0 + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
+      const float pr = s <= pos ? sc[min(s, pos)] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
+    }
+  }
+#pragma unroll
+  for (int off = kSliceBlocks; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off, 64);
+  if (lane < kSliceBlocks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[wave * kSliceDims + lane * 8 + e] = o[e];
+  }
+  __syncthreads();
+  if (t < kSliceDims && (t & 1) == 0) {
+    const f16 a = (f16)(((pv[t] + pv[kSliceDims + t]) + pv[2 * kSliceDims + t]) + pv[3 * kSliceDims + t]);
+    const int t1 = t + 1;
+    const f16 b = (f16)(((pv[t1] + pv[kSliceDims + t1]) + pv[2 * kSliceDims + t1]) + pv[3 * kSliceDims + t1]);
+    sys_store(p.ws + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, a, b));
+  }
+}
+
+// ---------------------------------------------------------------- the kernel
+template <int FMT, bool SCALED, bool RANKED>
+__global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float wsum[4];
+  __shared__ f16 zsh[8];
+  const int b = blockIdx.x;
+  const uint64_t passed = sys_load(p.ws);  // waited for only where a role first needs the tag
+  const int role = b < p.end[R_ZQKV] ? R_ZQKV : b < p.end[R_TQKV] ? R_TQKV : b < p.end[R_ATTN] ? R_ATTN
+                   : b < p.end[R_ZO] ? R_ZO : b < p.end[R_TO] ? R_TO : b < p.end[R_ZGU] ? R_ZGU
+                   : b < p.end[R_TGU] ? R_TGU : b < p.end[R_ZD] ? R_ZD : R_TD;
+  const int i = b - (role == 0 ? 0 : p.end[role - 1]);
+  // Which problem a z or tile workgroup serves, by the per-problem counts within its role.
+  auto zsplit = [&](int p0, int count, int &pi, int &zi) {
+    pi = p0;
+    zi = i;
+    for (int q = 0; q < count - 1; ++q) {
+      const int n = (p.prob[pi].rank + kFusedZRanks - 1) / kFusedZRanks;
+      if (zi < n) break;
+      zi -= n;
+      ++pi;
+    }
+  };
+  auto tsplit = [&](int p0, int count, int &pi, int &n0) {
+    pi = p0;
+    int ti = i;
+    for (int q = 0; q < count - 1; ++q) {
+      const int n = (p.prob[pi].N + 15) / 16;
+      if (ti < n) break;
+      ti -= n;
+      ++pi;
+    }
+    n0 = ti * 16;
+  };
+  int pi = 0, k = 0;
+  switch (role) {
+    case R_ZQKV: zsplit(P_Q, 3, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
+    case R_ZO: zsplit(P_O, 1, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
+    case R_ZGU: zsplit(P_GATE, 2, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
+    case R_ZD: zsplit(P_DOWN, 1, pi, k); layer_z_role<kFusedMaxK>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
+    case R_TQKV: tsplit(P_Q, 3, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
+    case R_TO: tsplit(P_O, 1, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
+    case R_TGU: tsplit(P_GATE, 2, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
+    case R_TD: tsplit(P_DOWN, 1, pi, k); layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED>(p, pi, k, passed, smem); break;
+    default: layer_attention_role(p, i, passed, smem); break;
+  }
+  // Every workgroup counts itself once, after all of its work (thread 0 of wave 0 runs every role
+  // to its end).
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(p.ws, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+}  // namespace lb

@@ -24,7 +24,7 @@ FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
-DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next')
+DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_decode_layer')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
 def attention_workspace_bytes(heads, capacity):
@@ -82,6 +82,25 @@ class DecodeAttentionArgs(ctypes.Structure):
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
 
 
+class DecodeLayerArgs(ctypes.Structure):
+    """Mirror of lb_decode_layer_args."""
+    _fields_ = [('struct_size', ctypes.c_uint32), ('format', ctypes.c_uint32),
+                ('group_size', ctypes.c_int64), ('hidden', ctypes.c_int64), ('intermediate', ctypes.c_int64),
+                ('h', ctypes.c_void_p), ('norm1', ctypes.c_void_p), ('norm2', ctypes.c_void_p),
+                ('eps', ctypes.c_float), ('reserved', ctypes.c_uint32),
+                ('proj', FusedProblem * 7),
+                ('heads', ctypes.c_int64), ('kv_heads', ctypes.c_int64), ('capacity', ctypes.c_int64),
+                ('cos', ctypes.c_void_p), ('sin', ctypes.c_void_p), ('position', ctypes.c_void_p),
+                ('keys', ctypes.c_void_p), ('values', ctypes.c_void_p),
+                ('scale', ctypes.c_float), ('reserved2', ctypes.c_uint32),
+                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
+
+
+def layer_workspace_bytes(hidden, intermediate, kv_heads):
+    """LB_DECODE_LAYER_WORKSPACE_BYTES."""
+    return 8 * (92 + (hidden + 128 * kv_heads) // 2 + hidden + intermediate)
+
+
 _lib = None
 
 
@@ -117,6 +136,8 @@ def library():
         lib.lb_fused_linear.argtypes = [ctypes.POINTER(FusedLinearArgs), ctypes.c_void_p]
         lib.lb_decode_attention.restype = ctypes.c_int
         lib.lb_decode_attention.argtypes = [ctypes.POINTER(DecodeAttentionArgs), ctypes.c_void_p]
+        lib.lb_decode_layer.restype = ctypes.c_int
+        lib.lb_decode_layer.argtypes = [ctypes.POINTER(DecodeLayerArgs), ctypes.c_void_p]
         lib.lb_argmax_next.restype = ctypes.c_int
         lib.lb_argmax_next.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -531,3 +552,57 @@ class PreparedArgmax:
         status = self._fn(*self._call, ctypes.c_void_p(handle))
         if status != OK:
             _check(status, 'lb_argmax_next')
+
+
+class PreparedLayer(_Prepared):
+    """lb_decode_layer: one decoder layer for one token in one launch.
+
+    h: fp16 [hidden] residual row (input, replaced by the output).  projections: seven dicts
+    (q, k, v, o, gate, up, down) with codes, scales (None for fp16), N, and optionally down [rank, K]
+    and up [N, rank].  group_size 0 means int8 per row.  cos/sin [capacity, 64], position int64 [1],
+    keys/values [kv_heads, capacity, 64].  The call owns a zeroed workspace.
+    """
+
+    def __init__(self, h, projections, *, format, group_size, hidden, intermediate, norm1, norm2, eps, heads,
+                 kv_heads, cos, sin, position, keys, values, scale=0.125):
+        if len(projections) != 7:
+            raise ValueError('seven projections: q, k, v, o, gate, up, down')
+        capacity = keys.shape[-2]
+        a = DecodeLayerArgs()
+        a.struct_size = ctypes.sizeof(DecodeLayerArgs)
+        a.format = FORMATS[format]
+        a.group_size, a.hidden, a.intermediate = group_size, hidden, intermediate
+        keep = [_row(h, 'h', hidden), _row(norm1, 'norm1', hidden), _row(norm2, 'norm2', hidden)]
+        a.h, a.norm1, a.norm2, a.eps = _ptr(h), _ptr(norm1), _ptr(norm2), eps
+        for i, pr in enumerate(projections):
+            q = a.proj[i]
+            q.N = pr['N']
+            q.codes, q.scales = _ptr(pr['codes']), _ptr(pr.get('scales'))
+            keep += [pr['codes'], pr.get('scales')]
+            down, up = pr.get('down'), pr.get('up')
+            if down is not None:
+                down = down.contiguous()
+                if up.stride(-1) != 1 or up.stride(0) % 8:
+                    padded = torch.zeros((up.shape[0], (up.shape[1] + 7) // 8 * 8), dtype=up.dtype, device=up.device)
+                    padded[:, :up.shape[1]] = up
+                    up = padded
+                q.rank = down.shape[0]
+                q.down, q.up, q.up_ld = _ptr(down), _ptr(up), up.stride(0)
+                keep += [down, up]
+        for t, name, count in ((cos, 'cos', capacity * 64), (sin, 'sin', capacity * 64),
+                               (keys, 'keys', kv_heads * capacity * 64), (values, 'values', kv_heads * capacity * 64)):
+            keep.append(_row(t, name, count))
+        keep.append(_row(position, 'position', 1, torch.int64))
+        a.heads, a.kv_heads, a.capacity = heads, kv_heads, capacity
+        a.cos, a.sin, a.position, a.keys, a.values, a.scale = (_ptr(cos), _ptr(sin), _ptr(position), _ptr(keys),
+                                                               _ptr(values), scale)
+        size = layer_workspace_bytes(hidden, intermediate, kv_heads)
+        self.workspace = torch.zeros(size, dtype=torch.uint8, device=h.device)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+        keep.append(self.workspace)
+        self._bind('lb_decode_layer', 'lb_decode_layer', a, h.device, keep)
+        self.out = h
+
+    def counters(self):
+        """(workgroups counted over all calls so far, timeout word) of the workspace."""
+        return [int(self.workspace[:8].view(torch.int64)), int(self.workspace[8:12].view(torch.int32))]

@@ -558,12 +558,14 @@ class GraphDecoder:
       5. SiLU(gate) * up -> down projection (+ correction) + residual  lb_fused_linear
     then RMSNorm -> tied fp16 lm_head (lb_fused_linear) and the greedy token with the next
     embedding (lb_argmax_next).  Projections of different formats (fp16-protected ones)
-    get separate launches.  fused=False runs the same step as staged PyTorch-ROCm glue
+    get separate launches.  layer=True (default) runs those five steps of a layer as one
+    lb_decode_layer launch whenever its seven projections share one format and group (the
+    reference's one graph per layer); the fused launches remain for other layers.  fused=False runs the same step as staged PyTorch-ROCm glue
     around one lb_linear per projection.  shared_z (default) gives every fused launch with
     corrections its own workspace, so each correction's z is computed once per launch.
     """
 
-    def __init__(self, stack, io, *, fused=True, shared_z=True):
+    def __init__(self, stack, io, *, fused=True, shared_z=True, layer=True):
         self.device = io.embedding.device
         if self.device.type != 'cuda':
             raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
@@ -579,7 +581,10 @@ class GraphDecoder:
         self.keys = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
         self.values = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
         self.states = [layer._dev(dev) for layer in stack.layers]
-        if fused:
+        self.layer_kernel = fused and layer and all(self._layer_ready(st) for st in self.states)
+        if self.layer_kernel:
+            self._build_layer(z)
+        elif fused:
             self._build_fused(z)
         else:
             self._build_staged(z)
@@ -644,6 +649,11 @@ class GraphDecoder:
             seq += self._fused_group(lin, [('mlp.down_proj.weight', self.h, dict(residual=self.h))], gate,
                                      prologue='silu_mul', x2=up)
             self.calls.append(seq)
+        self._build_head(io)
+
+    def _build_head(self, io):
+        """Final RMSNorm -> tied lm_head (one fused launch) and the greedy token with the next embedding."""
+        import lowbit_hip as lb
         if io.head is None:
             head, head_format, head_group = dict(codes=io.embedding, scales=None), 'fp16', HIDDEN
         else:
@@ -653,6 +663,55 @@ class GraphDecoder:
                                      K=HIDDEN, group_size=head_group, prologue='rmsnorm', gamma=io.norm, eps=1e-5)
         self.argmax = lb.PreparedArgmax(self.logits, io.embedding, self.h, self.tokens, self.token, self.pos,
                                         limit=self.capacity)
+
+    # ---------------------------------------------------------------- one launch per layer
+    _ORDER = ('self_attn.q_proj.weight', 'self_attn.k_proj.weight', 'self_attn.v_proj.weight',
+              'self_attn.o_proj.weight', 'mlp.gate_proj.weight', 'mlp.up_proj.weight', 'mlp.down_proj.weight')
+
+    @classmethod
+    def _layer_ready(cls, state):
+        """One format for all seven projections, groups lb_decode_layer takes (int8 per row, or one
+        power-of-two group), so the layer can run as one lb_decode_layer launch."""
+        entries = [state['lin'][name] for name in cls._ORDER]
+        fmt = entries[0]['format']
+        if any(e['format'] != fmt for e in entries):
+            return False
+        if fmt == 'fp16':
+            return True
+        groups = {e['group'] if e['group'] != e['K'] else 0 for e in entries}
+        if len(groups) != 1:
+            return False
+        group = groups.pop()
+        return (group == 0 and fmt == 'int8') or (group >= 32 and group & (group - 1) == 0)
+
+    def _build_layer(self, z):
+        """Each layer as one lb_decode_layer launch, then the fused head and the argmax."""
+        import lowbit_hip as lb
+        io = self.io
+        self.h = z(HIDDEN)
+        self.calls = []
+        for state, keys, values in zip(self.states, self.keys, self.values):
+            entries = [state['lin'][name] for name in self._ORDER]
+            fmt = entries[0]['format']
+            group = 0 if fmt == 'fp16' or entries[0]['group'] == entries[0]['K'] else entries[0]['group']
+            projections = []
+            for e in entries:
+                pr = dict(codes=e['codes'], scales=e['scales'], N=e['N'])
+                if e.get('rank', 0):
+                    pr.update(down=e['down'], up=e['up'])
+                projections.append(pr)
+            self.calls.append([lb.PreparedLayer(self.h, projections, format=fmt, group_size=group, hidden=HIDDEN,
+                                                intermediate=1536, norm1=state['norm1'], norm2=state['norm2'],
+                                                eps=1e-5, heads=HEADS, kv_heads=KV_HEADS, cos=state['cos'],
+                                                sin=state['sin'], position=self.pos, keys=keys, values=values,
+                                                scale=0.125)])
+        self._build_head(io)
+
+    def timeouts(self):
+        """Timed-out waits recorded by the layer launches since construction (0 when healthy)."""
+        if not self.layer_kernel:
+            return 0
+        return sum(seq[0].counters()[1] for seq in self.calls)
 
     # ---------------------------------------------------------------- staged launches
     def _build_staged(self, z):

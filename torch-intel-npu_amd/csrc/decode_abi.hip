@@ -696,8 +696,8 @@ lb_status check_layer(const lb_decode_layer_args *a, LayerParams *out, int *fmt,
   p.w_gu = p.w_h1 + (int)(H / 2);
   auto zc = [&](int i) { return (p.prob[i].rank + kFusedZRanks - 1) / kFusedZRanks; };
   auto tc = [&](int i) { return (p.prob[i].N + 15) / 16; };
-  const int counts[R_COUNT] = {zc(P_Q) + zc(P_K) + zc(P_V), tc(P_Q) + tc(P_K) + tc(P_V), (int)a->heads * kAttnDimSlices,
-                               zc(P_O), tc(P_O), zc(P_GATE) + zc(P_UP), tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};
+  const int counts[R_COUNT] = {tc(P_Q) + tc(P_K) + tc(P_V), (int)a->heads * kAttnDimSlices, tc(P_O),
+                               tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};
   int acc = 0;
   for (int r = 0; r < R_COUNT; ++r) p.end[r] = acc += counts[r];
   *out = p;
@@ -725,7 +725,7 @@ extern "C" lb_status lb_decode_layer(const lb_decode_layer_args *a, void *stream
   if (st != LB_OK) return st;
   // Dynamic LDS: the largest role (a 1536-long tile: staged row, scales, U rows, reductions, NF4
   // table) or the attention (its rows and one float per cache slot).
-  const size_t smem = std::max<size_t>(9216, 1024 + (size_t)4 * p.capacity);
+  const size_t smem = std::max<size_t>(9216, 2048 + (size_t)4 * p.capacity);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (fmt) {
     case FMT_INT8: scaled ? launch_layer_t<FMT_INT8, true>(p, ranked, smem, s) : launch_layer_t<FMT_INT8, false>(p, ranked, smem, s); break;

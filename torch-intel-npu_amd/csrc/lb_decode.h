@@ -22,16 +22,51 @@
 
 namespace lb {
 
+// Cross-lane moves on the VALU's data-parallel primitives (DPP), a few cycles each instead of an
+// LDS permute round trip.  Lane layouts (rows of 16 lanes): quad_perm [1,0,3,2] and [2,3,0,1]
+// swap neighbours at distance 1 and 2, row_half_mirror maps lane i of each 8 to 7 - i,
+// row_mirror lane i of each 16 to 15 - i, row_shl:1 gives lane i the value of lane i + 1 (0 at
+// the row's end), row_ror:n the value of lane i - n (mod 16).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+constexpr int kDppRowShl1 = 0x101, kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_move(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, dpp_move<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// Sum over each aligned group of 8 / 16 lanes, the same bits in every lane of the group (each
+// step adds two equal-shaped partial sums, in either order the same value).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_move<kDppXor1>(v);
+  v += dpp_move<kDppXor2>(v);
+  return v + dpp_move<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  return v + dpp_move<kDppMirror>(v);
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Whole-wave sum / max (every lane active), wave-uniform: the four row results combined in a
+// fixed order.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v = sum16(v);
+  return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, dpp_move<kDppXor1>(v));
+  v = fmaxf(v, dpp_move<kDppXor2>(v));
+  v = fmaxf(v, dpp_move<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_move<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
@@ -615,8 +650,39 @@ constexpr int kAttnDimSlices = LB_ATTN_SLICES;          // workgroups per query 
 constexpr int kSliceDims = kHeadDim / kAttnDimSlices;   // output dims per workgroup
 constexpr int kSliceBlocks = kSliceDims / 8;            // 16-byte V blocks per slot and workgroup
 constexpr int kAttnParts = 256 / kSliceBlocks;          // position partitions of the P.V product
+constexpr int kPvPartials = 16;  // P.V partial sums per output dim: one per row of 16 lanes of each wave
+
+// P.V: lane l of a wave holds o[8], the partial products of V block l % kSliceBlocks over its
+// positions.  The lanes of one block within each row of 16 are summed on DPP (distance 2 within
+// quads, then rotations by 4 and 8), and each row's sums go to pv[(4 wave + row) * kSliceDims + d].
+__device__ __forceinline__ void pv_row_partials(float (&o)[8], float *pv, int lane, int wave);
+// The output dim d: the 16 row partials added in a fixed order.
+__device__ __forceinline__ float pv_total(const float *pv, int d);
+
 constexpr int kScoreSlots = 2;   // K rows per thread per round: 512 slots per round
 constexpr int kValueSlots = (384 + kAttnParts - 1) / kAttnParts;  // V blocks per thread per round (>= 384 slots)
+
+__device__ __forceinline__ void pv_row_partials(float (&o)[8], float *pv, int lane, int wave) {
+  static_assert(kSliceBlocks == 2, "the DPP steps pair lanes of equal parity");
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o[e] += dpp_move<kDppXor2>(o[e]);
+    o[e] += dpp_move<kDppRowRor4>(o[e]);
+    o[e] += dpp_move<kDppRowRor8>(o[e]);
+  }
+  const int r = lane & 15;
+  if (r < kSliceBlocks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[(wave * 4 + (lane >> 4)) * kSliceDims + r * 8 + e] = o[e];
+  }
+}
+
+__device__ __forceinline__ float pv_total(const float *pv, int d) {
+  float r = pv[d];
+#pragma unroll
+  for (int q = 1; q < kPvPartials; ++q) r += pv[q * kSliceDims + d];
+  return r;
+}
 static_assert(kSliceBlocks >= 1 && kHeadDim % kAttnDimSlices == 0, "attention slices");
 
 // kAttnDimSlices workgroups per query head, each owning kSliceDims of the output dims.  Every

@@ -4,9 +4,13 @@
 // RMSNorm -> gate|up, SiLU * up -> down + residual) become workgroup roles of one grid, in this
 // dispatch order:
 //
-//   Z_QKV  correction activations z of q, k, v      T_QKV  q | k | v tiles (16 rows each)
-//   ATTN   RoPE, KV append, attention (head, dims)   Z_O / T_O    o projection + residual
-//   Z_GU / T_GU  gate | up                           Z_D / T_D    down projection + residual
+//   T_QKV  q | k | v tiles (16 rows each)            ATTN   RoPE, KV append, attention (head, dims)
+//   T_O    o projection + residual                   T_GU   gate | up
+//   Z_D    correction activations z of down          T_D    down projection + residual
+//
+// A tile over K <= 640 computes its problem's correction activations z = fp16(x'.V^T) itself from
+// V rows fetched at launch (8 threads per rank); the down projection (K up to 1536) takes z from
+// the Z_D workgroups instead, whose V slices stay small.
 //
 // A role hands its output to later roles through the workspace as tagged 64-bit words (two fp16
 // values and the launch's 16-bit tag; the correction activations three to a word), written and
@@ -31,7 +35,7 @@
 
 namespace lb {
 
-enum LayerRole { R_ZQKV, R_TQKV, R_ATTN, R_ZO, R_TO, R_ZGU, R_TGU, R_ZD, R_TD, R_COUNT };
+enum LayerRole { R_TQKV, R_ATTN, R_TO, R_TGU, R_ZD, R_TD, R_COUNT };
 enum LayerProj { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, P_COUNT };
 enum LayerSource { SRC_H, SRC_ATT, SRC_H1, SRC_GU };
 
@@ -88,15 +92,20 @@ __device__ __forceinline__ void layer_timeout(const LayerParams &p) {
 }
 
 // A word whose tag is current (bounded wait; a timeout is recorded and the stale word returned).
+// The retry loop is kept rolled and out of line (unlikely branch), so the straight-line code a
+// workgroup executes stays short.
 __device__ __forceinline__ uint64_t wait_word(const LayerParams &p, const uint64_t *a, uint32_t tag) {
   uint64_t w = sys_load(a);
-  for (int it = 0; word_tag(w) != tag; ++it) {
-    if (it == kLayerSpinLimit) {
-      layer_timeout(p);
-      break;
+  if (__builtin_expect(word_tag(w) != tag, 0)) {
+#pragma nounroll
+    for (int it = 0; word_tag(w) != tag; ++it) {
+      if (it == kLayerSpinLimit) {
+        layer_timeout(p);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      w = sys_load(a);
     }
-    __builtin_amdgcn_s_sleep(2);
-    w = sys_load(a);
   }
   return w;
 }
@@ -107,31 +116,76 @@ __device__ __forceinline__ void wait_sentinel(const LayerParams &p, const uint64
   __syncthreads();
 }
 
-// Eight consecutive values (four pair words) of a word region, each word waited for.
-__device__ __forceinline__ h8 read_block_words(const LayerParams &p, const uint64_t *a, uint32_t tag) {
+// Cache policy of a buffer load that reads at the memory side past the per-XCD L2s (sc0 sc1, the
+// coherence of the system-scope atomics above).
+constexpr int kSysCoherent = 17;
+
+// The workspace as a buffer (its last region, gate|up, ends the words the kernel touches).
+// Built from readfirstlane copies, so the descriptor stays in scalar registers after the
+// divergent wait that precedes its use.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(const LayerParams &p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p.ws);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint32_t words = __builtin_amdgcn_readfirstlane((uint32_t)(p.w_gu + p.inter));
+  return buffer_rsrc(reinterpret_cast<const uint64_t *>(((uint64_t)hi << 32) | lo), (size_t)words * 8);
+}
+
+// Words [word, word + 4) (word even) with two 16-byte loads issued back to back; an offset of
+// kOutOfRange reads zeros.
+__device__ __forceinline__ void load_words4(__amdgpu_buffer_rsrc_t wb, int byte_off, uint64_t (&w)[4]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const u4 v = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, byte_off < 0 ? byte_off : byte_off + 16 * h, 0, kSysCoherent));
+    w[2 * h] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    w[2 * h + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+  }
+}
+
+// Re-reads (bounded wait) each of the four words whose tag is not current.
+__device__ __forceinline__ void settle_words4(const LayerParams &p, const uint64_t *a, uint32_t tag, uint64_t (&w)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (__builtin_expect(word_tag(w[q]) != tag, 0)) w[q] = wait_word(p, a + q, tag);
+}
+
+__device__ __forceinline__ h8 words4_to_h8(const uint64_t (&w)[4]) {
   h8 v;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const uint64_t w = wait_word(p, a + q, tag);
-    v[2 * q] = word_half(w, 0);
-    v[2 * q + 1] = word_half(w, 1);
+    v[2 * q] = word_half(w[q], 0);
+    v[2 * q + 1] = word_half(w[q], 1);
   }
   return v;
 }
 
 // The source row of a role's products (K values, 8 per block, thread t holding blocks t + 256 i)
-// and the prologue's second row (gamma, or the up half for SiLU-multiply).
+// and the prologue's second row (gamma, or the up half for SiLU-multiply).  Every word of the
+// thread is requested at once; only words still stale are then waited for one by one.
 template <int XB>
 __device__ __forceinline__ void layer_source_row(const LayerParams &p, int src, int K, uint32_t tag, h8 (&xv)[XB],
                                                  h8 (&av)[XB]) {
+  constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, blocks = K >> 3;
-  const uint64_t *base = p.ws + (src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu);
+  const int base = src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu;
+  const int second = base + p.inter / 2;
+  const __amdgpu_buffer_rsrc_t wb = workspace_rsrc(p);
+  uint64_t wx[XB][4], wa[XB][4];
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = t + 256 * i;
+    load_words4(wb, b < blocks ? (base + 4 * b) * 8 : kOutOfRange, wx[i]);
+    if (src == SRC_GU) load_words4(wb, b < blocks ? (second + 4 * b) * 8 : kOutOfRange, wa[i]);
+  }
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
     const int b = t + 256 * i;
     if (b < blocks) {
-      xv[i] = read_block_words(p, base + 4 * b, tag);
-      if (src == SRC_GU) av[i] = read_block_words(p, base + p.inter / 2 + 4 * b, tag);
+      settle_words4(p, p.ws + base + 4 * b, tag, wx[i]);
+      xv[i] = words4_to_h8(wx[i]);
+      if (src == SRC_GU) {
+        settle_words4(p, p.ws + second + 4 * b, tag, wa[i]);
+        av[i] = words4_to_h8(wa[i]);
+      }
     } else {
       xv[i] = h8{};
       if (src == SRC_GU) av[i] = h8{};
@@ -273,9 +327,9 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int z
       }
     }
   }
-  acc += acc2;
-#pragma unroll
-  for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  static_assert(TPR == 32, "two ranks per wave");
+  acc = sum16(acc + acc2);
+  acc = (t & 63) < 32 ? lane_value(acc, 0) + lane_value(acc, 16) : lane_value(acc, 32) + lane_value(acc, 48);
   if (li == 0 && rr < kFusedZRanks) zsh[rr] = live ? (f16)acc : (f16)0.0f;
   __syncthreads();
   if (t < 2) {
@@ -290,7 +344,7 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int z
 // Rows [n0, n0 + 16) of problem pi, with the fused decode kernel's product and epilogue.  Output:
 // q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
 // residual h1).
-template <int FMT, bool SCALED, int KMAX, bool RANKED>
+template <int FMT, bool SCALED, int KMAX, bool RANKED, bool OWN_Z>
 __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, int n0, uint64_t passed, uint8_t *smem) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
@@ -304,6 +358,8 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   constexpr int XB = (KMAX / 8 + 255) / 256;
   constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
+  constexpr int VB = OWN_Z ? (KMAX / 8 + 7) / 8 : 0;  // V blocks per thread (8 threads per rank row)
+  static_assert(!OWN_Z || (RANKED && VB * 64 <= KMAX + 4 * CPL + 8), "own z: staged row too short");
   constexpr int kOutOfRange = (int)0x80000000u;
   f16 *xs = reinterpret_cast<f16 *>(smem);                                  // [XLD]
   f16 *ss = xs + XLD;                                                       // [16 GMAX + 8]
@@ -341,6 +397,18 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   }
   h8 xv[XB], av[XB];
   layer_plain_loads(p, rs, xv, av);
+  // Own z: thread t holds blocks t % 8 + 8 i of V row t / 8 (zeros past the rank and K).
+  const int vr = t >> 3, vpart = t & 7;
+  u4 vreg[VB > 0 ? VB : 1];
+  if constexpr (OWN_Z) {
+    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(P.down, rank > 0 ? (size_t)rank * K * 2 : 0);
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int k = (vpart + 8 * i) * 8;
+      const int off = vr < rank && k < K ? (vr * K + k) * 2 : kOutOfRange;
+      vreg[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
+    }
+  }
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
     const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)n0 * G, (size_t)rows * G * 2);
@@ -388,27 +456,60 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
     const int b = t + 256 * i;
     if (b < blocks) *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(layer_prologue_apply(rs.prologue, xv[i], av[i], inv));
   }
-  const int zero_end = min(XLD, K + KSTEP + 8);
+  // Zeros past K: MFMA lanes read up to KSTEP beyond it, the own z product up to VB * 64.
+  const int zero_end = OWN_Z ? XLD : min(XLD, K + KSTEP + 8);
   for (int b = blocks + t; b * 8 < zero_end; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
   __syncthreads();
 
+  // Own z = fp16(x'.V^T) into zs (zero from the rank on), read by the epilogue after the barrier
+  // that follows the product.  x' and V are both in the format's slot order within a block.
+  if constexpr (OWN_Z) {
+    if (rank > 0) {
+      h8 xx[VB];
+#pragma unroll
+      for (int i = 0; i < VB; ++i) xx[i] = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
+      float za = 0.0f, zb = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        asm volatile("" : "+v"(vreg[i]));
+        const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          za += (float)xx[i][e] * (float)vv[e];
+          zb += (float)xx[i][e + 1] * (float)vv[e + 1];
+        }
+      }
+      za = sum8(za + zb);
+      if (vpart == 0) zs[vr] = vr < rank ? (float)(f16)za : 0.0f;
+    }
+  }
+
   f4 acc = {0.f, 0.f, 0.f, 0.f};
+  // Every A fragment (and group scale) is read from LDS before the first product, so the reads
+  // overlap instead of each waiting behind the previous MFMA.
   const f16 *a0 = xs + g * CPL;
+  h8 afr[D][T8];
+  f16 gsc[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int kb = (wave + KG * u) * KSTEP;
+#pragma unroll
+    for (int q = 0; q < T8; ++q) afr[u][q] = kb < K ? *reinterpret_cast<const h8 *>(a0 + kb + 8 * q) : h8{};
+    gsc[u] = (f16)1.0f;
+    if constexpr (SCALED) {
+      if (kb < K) gsc[u] = ss[j * G + ((kb + g * CPL) >> group_shift)];
+    }
+  }
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
     if (kb >= K) break;
     asm volatile("" : "+v"(w[u]));
-    h2 s2 = {(f16)1.0f, (f16)1.0f};
-    if constexpr (SCALED) {
-      const f16 sc = ss[j * G + ((kb + g * CPL) >> group_shift)];
-      s2 = h2{sc, sc};
-    }
+    const h2 s2 = {gsc[u], gsc[u]};
 #pragma unroll
     for (int q = 0; q < T8; ++q) {
-      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
       const h8 b = decode8<FMT, !SCALED>(w[u], q, s2, nf4_table);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[u][q], b, acc, 0, 0, 0);
     }
   }
   if (wave > 0 && g == 0) red[(wave - 1) * 16 + j] = acc[0];
@@ -416,7 +517,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   if (wave != 0) return;
 
   // ---- epilogue: wave 0; lane j < rows owns row n0 + j ----
-  if constexpr (RANKED) {
+  if constexpr (RANKED && !OWN_Z) {
     if (rank > 0) {
       const int words = (rank + 2) / 3;
       const uint64_t *zw = p.ws + p.w_z + pi * kLayerZWords;
@@ -441,7 +542,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
     hv = (f16)((float)hv + (float)(f16)d);
   }
   if (pi == P_O || pi == P_DOWN) hv = (f16)((float)residual + (float)hv);
-  const f16 next = __builtin_bit_cast(f16, (uint16_t)__shfl(__builtin_bit_cast(uint16_t, hv), lane + 1, 64));
+  const f16 next = __builtin_bit_cast(f16, (uint16_t)dpp_move<kDppRowShl1>((int)__builtin_bit_cast(uint16_t, hv)));
   if (g != 0 || j >= rows) return;
   if (pi == P_DOWN) {
     p.h[n0 + j] = hv;
@@ -471,8 +572,8 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
   f16 *vn = kn + kHeadDim;                               // [64]
   f16 *raw = vn + kHeadDim;                              // [128] raw q and k rows
   float *wred = reinterpret_cast<float *>(raw + 2 * kHeadDim);  // [4]
-  float *pv = wred + 4;                                  // [4 * kSliceDims]
-  float *sc = pv + 4 * kSliceDims;                       // [capacity]
+  float *pv = wred + 4;                                  // [kPvPartials * kSliceDims]
+  float *sc = pv + kPvPartials * kSliceDims;             // [capacity]
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -553,6 +654,9 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
     *dst = t < kHeadDim ? kn[dd] : vn[dd];
   }
 
+  h8 qreg[kHeadDim / 8];
+#pragma unroll
+  for (int b = 0; b < kHeadDim / 8; ++b) qreg[b] = *reinterpret_cast<const h8 *>(qs + 8 * b);
   float lmax = -INFINITY;
   for (int base = 0; base <= pos; base += 256 * kScoreSlots) {
     if (base > 0) load_keys(base);
@@ -564,7 +668,7 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
 #pragma unroll
       for (int b = 0; b < kHeadDim / 8; ++b) {
         asm volatile("" : "+v"(kreg[i][b]));
-        const h8 qq = *reinterpret_cast<const h8 *>(qs + 8 * b);
+        const h8 qq = qreg[b];
         const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * b) : __builtin_bit_cast(h8, kreg[i][b]);
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
@@ -611,19 +715,10 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
       for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];
     }
   }
-#pragma unroll
-  for (int off = kSliceBlocks; off < 64; off <<= 1)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off, 64);
-  if (lane < kSliceBlocks) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) pv[wave * kSliceDims + lane * 8 + e] = o[e];
-  }
+  pv_row_partials(o, pv, lane, wave);
   __syncthreads();
   if (t < kSliceDims && (t & 1) == 0) {
-    const f16 a = (f16)(((pv[t] + pv[kSliceDims + t]) + pv[2 * kSliceDims + t]) + pv[3 * kSliceDims + t]);
-    const int t1 = t + 1;
-    const f16 b = (f16)(((pv[t1] + pv[kSliceDims + t1]) + pv[2 * kSliceDims + t1]) + pv[3 * kSliceDims + t1]);
+    const f16 a = (f16)pv_total(pv, t), b = (f16)pv_total(pv, t + 1);
     sys_store(p.ws + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, a, b));
   }
 }
@@ -636,8 +731,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p) {
   __shared__ f16 zsh[8];
   const int b = blockIdx.x;
   const uint64_t passed = sys_load(p.ws);  // waited for only where a role first needs the tag
-  const int role = b < p.end[R_ZQKV] ? R_ZQKV : b < p.end[R_TQKV] ? R_TQKV : b < p.end[R_ATTN] ? R_ATTN
-                   : b < p.end[R_ZO] ? R_ZO : b < p.end[R_TO] ? R_TO : b < p.end[R_ZGU] ? R_ZGU
+  const int role = b < p.end[R_TQKV] ? R_TQKV : b < p.end[R_ATTN] ? R_ATTN : b < p.end[R_TO] ? R_TO
                    : b < p.end[R_TGU] ? R_TGU : b < p.end[R_ZD] ? R_ZD : R_TD;
   const int i = b - (role == 0 ? 0 : p.end[role - 1]);
   // Which problem a z or tile workgroup serves, by the per-problem counts within its role.
@@ -664,14 +758,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p) {
   };
   int pi = 0, k = 0;
   switch (role) {
-    case R_ZQKV: zsplit(P_Q, 3, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
-    case R_ZO: zsplit(P_O, 1, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
-    case R_ZGU: zsplit(P_GATE, 2, pi, k); layer_z_role<640>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
     case R_ZD: zsplit(P_DOWN, 1, pi, k); layer_z_role<kFusedMaxK>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
-    case R_TQKV: tsplit(P_Q, 3, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
-    case R_TO: tsplit(P_O, 1, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
-    case R_TGU: tsplit(P_GATE, 2, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED>(p, pi, k, passed, smem); break;
-    case R_TD: tsplit(P_DOWN, 1, pi, k); layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED>(p, pi, k, passed, smem); break;
+    case R_TQKV: tsplit(P_Q, 3, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
+    case R_TO: tsplit(P_O, 1, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
+    case R_TGU: tsplit(P_GATE, 2, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
+    case R_TD: tsplit(P_DOWN, 1, pi, k); layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED, false>(p, pi, k, passed, smem); break;
     default: layer_attention_role(p, i, passed, smem); break;
   }
   // Every workgroup counts itself once, after all of its work (thread 0 of wave 0 runs every role

@@ -160,10 +160,65 @@ typedef struct lb_decode_layer_args {
   size_t workspace_bytes;
 } lb_decode_layer_args;
 
+/* Words of one layer's region of a decode-layer workspace (tagged hand-over words of every stage),
+ * and the workspace of one layer: an 8-word header (launch count, timeout word) and one region. */
+#define LB_DECODE_LAYER_WORDS(hidden, intermediate, kv_heads)                                              \
+  (((size_t)84u + ((size_t)(hidden) + 128u * (size_t)(kv_heads)) / 2u + 3u * (size_t)(hidden) / 2u + \
+    (size_t)(intermediate) + 31u) / 32u * 32u)
 #define LB_DECODE_LAYER_WORKSPACE_BYTES(hidden, intermediate, kv_heads) \
-  ((size_t)8u * (size_t)(92 + ((hidden) + 128 * (kv_heads)) / 2 + (hidden) + (intermediate)))
+  ((size_t)8u * (8u + LB_DECODE_LAYER_WORDS(hidden, intermediate, kv_heads)))
 
 lb_status lb_decode_layer(const lb_decode_layer_args *args, void *stream);
+
+/*
+ * A whole decoder stack for one token in one launch: the layers of lb_decode_layer one after the
+ * other, with the same arithmetic (the output equals `layers` lb_decode_layer calls bit for bit).
+ * The counterpart of the reference's per-token chain of layer graphs, submitted in fenced groups
+ * (torch_npu_smollm.py:644-654, torch_intel_npu.py:560-570).  Every workgroup keeps its stage
+ * through all layers and fetches the next layer's weights while earlier stages run; the grid must
+ * be resident on the device all at once (lb_decode_stack returns LB_UNSUPPORTED where it is not).
+ * All layers share shapes, format, group size and per-projection ranks.
+ *
+ * lb_decode_stack_prepare validates the arguments and writes the layer table (device addresses of
+ * every layer's tensors) into `table`, synchronously on `stream`; it is a set-up call, made once
+ * before lb_decode_stack calls (which may be captured into a HIP graph) with the same layers.
+ * lb_decode_stack refuses a table that lb_decode_stack_prepare did not write for these layers.
+ */
+#define LB_DECODE_STACK_MAX_LAYERS 64
+#define LB_DECODE_STACK_TABLE_BYTES(layers) ((size_t)(layers) * 256u)
+#define LB_DECODE_STACK_WORKSPACE_BYTES(hidden, intermediate, kv_heads, layers) \
+  ((size_t)8u * (8u + (size_t)(layers) * LB_DECODE_LAYER_WORDS(hidden, intermediate, kv_heads)))
+
+typedef struct lb_decode_stack_layer {
+  const void *norm1, *norm2;   /* fp16 [hidden], 16-byte aligned */
+  lb_fused_problem proj[7];    /* as lb_decode_layer_args.proj; rank and up_ld equal in every layer */
+  void *keys, *values;         /* fp16 [kv_heads, capacity, 64], 16-byte aligned; slot p is written */
+} lb_decode_stack_layer;
+
+typedef struct lb_decode_stack_args {
+  uint32_t struct_size;        /* sizeof(lb_decode_stack_args) */
+  uint32_t format;             /* lb_format of every projection */
+  int64_t group_size;          /* as lb_decode_layer_args.group_size */
+  int64_t hidden, intermediate;
+  int64_t layers;              /* 1..LB_DECODE_STACK_MAX_LAYERS */
+  const lb_decode_stack_layer *layer;  /* host array [layers] */
+  void *h;                     /* fp16 [hidden]: the first layer's input, replaced by the last layer's output */
+  float eps;
+  uint32_t reserved;
+  int64_t heads, kv_heads, capacity;
+  const void *cos, *sin;       /* fp16 [capacity, 64] RoPE tables */
+  const int64_t *position;     /* device scalar p, as lb_decode_layer_args.position */
+  float scale;
+  uint32_t reserved2;
+  void *table;                 /* device, LB_DECODE_STACK_TABLE_BYTES(layers), 256-byte aligned */
+  size_t table_bytes;
+  void *workspace;             /* LB_DECODE_STACK_WORKSPACE_BYTES, 256-byte aligned, zero before its first use;
+                                  one per call configuration; calls sharing it must be ordered (one stream) */
+  size_t workspace_bytes;
+} lb_decode_stack_args;
+
+lb_status lb_decode_stack_prepare(const lb_decode_stack_args *args, void *stream);
+lb_status lb_decode_stack(const lb_decode_stack_args *args, void *stream);
 
 /*
  * Greedy step: t = first index of the largest logit (NaN logits are never chosen);

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LB_ABI_VERSION 3
+#define LB_ABI_VERSION 4
 
 typedef enum lb_status {
   LB_OK = 0,

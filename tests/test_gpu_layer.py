@@ -132,3 +132,89 @@ def test_decode_layer_rejects_bad_arguments(device):
     call.args.workspace_bytes = 64
     with pytest.raises(ValueError, match='workspace'):
         call.run()
+
+
+def stack_entry(layer, device, keys, values):
+    """One lb_decode_stack_layer dict (the tensors of `layer` on `device`)."""
+    state = layer._dev(device)
+    projections = []
+    for n in GraphDecoder._ORDER:
+        e = state['lin'][n]
+        pr = dict(codes=e['codes'], scales=e['scales'], N=e['N'])
+        if e.get('rank', 0):
+            pr.update(down=e['down'], up=e['up'])
+        projections.append(pr)
+    return dict(norm1=state['norm1'], norm2=state['norm2'], keys=keys, values=values, projections=projections)
+
+
+STACK_CASES = [('w8a16', 32, 3, 200), ('w8a16', 32, 2, 0), ('w4a16', 0, 3, 77), ('fp16', 0, 2, 383)]
+
+
+@pytest.mark.parametrize('mode,rank,layers,pos', STACK_CASES, ids=['-'.join(map(str, c)) for c in STACK_CASES])
+def test_decode_stack_matches_layer_calls(device, mode, rank, layers, pos):
+    """lb_decode_stack over L layers gives the bits of L lb_decode_layer calls (same arithmetic), and
+    the oracle's chained decode steps within the decoder bar."""
+    announce('decode stack', mode, rank, layers, pos)
+    made = [make_layer(mode, rank, 100 + 7 * l + pos) for l in range(layers)]
+    x = made[0][2]
+    position = torch.tensor([pos], dtype=torch.int64, device=device)
+    # oracle chain
+    want = x
+    wks, wvs = [], []
+    for layer, oracle, _, keys, values in made:
+        want, wk, wv = oracle.decode(want, keys[:, :, :pos], values[:, :, :pos], pos)
+        wks.append(wk[0, :, pos])
+        wvs.append(wv[0, :, pos])
+    # per-layer launches
+    h1 = x.view(576).to(device).clone()
+    caches1 = [(k[0].to(device).contiguous(), v[0].to(device).contiguous()) for _, _, _, k, v in made]
+    for (layer, *_), (dk, dv) in zip(made, caches1):
+        prepared(layer, device, h1, dk, dv, position).run()
+    # one stacked launch
+    h2 = x.view(576).to(device).clone()
+    caches2 = [(k[0].to(device).contiguous(), v[0].to(device).contiguous()) for _, _, _, k, v in made]
+    state = made[0][0]._dev(device)
+    fmt, group, _ = GraphDecoder._layer_key(state)
+    stack = lb.PreparedStack(h2, [stack_entry(m[0], device, dk, dv) for m, (dk, dv) in zip(made, caches2)],
+                             format=fmt, group_size=group, hidden=576, intermediate=1536, eps=1e-5, heads=9,
+                             kv_heads=3, cos=state['cos'], sin=state['sin'], position=position)
+    stack.run()
+    torch.cuda.synchronize()
+    got = h2.cpu()
+    err = rel_l2(got, want.view(576))
+    print(f'[decode stack] {mode} rank {rank} layers {layers} pos {pos}: rel-L2 {err:.2e}', flush=True)
+    assert torch.equal(got, h1.cpu())
+    for (ak, av), (bk, bv) in zip(caches1, caches2):
+        assert torch.equal(ak.cpu(), bk.cpu()) and torch.equal(av.cpu(), bv.cpu())
+    assert bool(torch.isfinite(got).all()) and err <= 1e-2
+    for l, (dk, dv) in enumerate(caches2):
+        assert rel_l2(dk[:, pos].cpu(), wks[l]) <= 1e-2 and rel_l2(dv[:, pos].cpu(), wvs[l]) <= 1e-2
+    total, timeout = stack.counters()
+    assert timeout == 0 and total > 0
+    # again from the same input: the same bits, every workgroup counted once per call
+    for _ in range(2):
+        h2.copy_(x.view(576).to(device))
+        stack.run()
+    torch.cuda.synchronize()
+    assert torch.equal(h2.cpu(), got)
+    assert stack.counters() == [3 * total, 0]
+
+
+def test_decode_stack_refuses_unprepared_table(device):
+    made = [make_layer('w8a16', 32, 11 + l) for l in range(2)]
+    position = torch.tensor([5], dtype=torch.int64, device=device)
+    h = made[0][2].view(576).to(device).clone()
+    caches = [(k[0].to(device).contiguous(), v[0].to(device).contiguous()) for _, _, _, k, v in made]
+    state = made[0][0]._dev(device)
+    stack = lb.PreparedStack(h, [stack_entry(m[0], device, dk, dv) for m, (dk, dv) in zip(made, caches)],
+                             format='int8', group_size=0, hidden=576, intermediate=1536, eps=1e-5, heads=9,
+                             kv_heads=3, cos=state['cos'], sin=state['sin'], position=position)
+    # layers that differ from the ones the table was prepared for
+    n0, n1 = stack._rows[0].norm1, stack._rows[1].norm1
+    stack._rows[0].norm1, stack._rows[1].norm1 = n1, n0
+    with pytest.raises(ValueError, match='not prepared'):
+        stack.run()
+    stack._rows[0].norm1, stack._rows[1].norm1 = n0, n1
+    stack.run()
+    torch.cuda.synchronize()
+    assert stack.counters()[1] == 0

@@ -192,10 +192,11 @@ def test_varied_greedy_sequence_matches_oracle(device):
     assert report['max_abs_err'] < report['min_margin'] / 2
 
 
-@pytest.mark.parametrize('mode', ['layer', 'fused', 'staged'])
+@pytest.mark.parametrize('mode', ['stack', 'layer', 'fused', 'staged'])
 def test_graph_decoder_matches_eager(device, mode):
     """The captured decode step reproduces the eager decode tokens and logits (4 layers, 24 steps):
-    one lb_decode_layer launch per layer, the five fused launches, or the staged glue."""
+    one lb_decode_stack launch for all layers, one lb_decode_layer launch per layer, the five fused
+    launches, or the staged glue."""
     announce('graph decoder', mode)
     fused = mode != 'staged'
     from torch_npu_smollm import GraphDecoder
@@ -206,8 +207,8 @@ def test_graph_decoder_matches_eager(device, mode):
     x = io.embed_tokens(ids.to(device))
     h, caches = stack.prefill(x)
     first = int(io.logits(h[:, -1:])[0, 0].float().argmax())
-    decoder = GraphDecoder(stack, io, fused=fused, layer=mode == 'layer')
-    assert decoder.layer_kernel == (mode == 'layer')
+    decoder = GraphDecoder(stack, io, fused=fused, layer=mode in ('layer', 'stack'), stack_kernel=mode == 'stack')
+    assert decoder.layer_kernel == (mode in ('layer', 'stack')) and decoder.stack_kernel == (mode == 'stack')
     decoder.load(caches, first)
     rest = decoder.generate(23)
     assert decoder.timeouts() == 0

@@ -4,6 +4,9 @@
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
+#include <cstring>
+#include <map>
+#include <vector>
 
 #include "../../include/lowbit_decode_hip.h"
 #include "abi_util.h"
@@ -586,152 +589,325 @@ lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embeddin
 
 namespace {
 
-// Validation of lb_decode_layer_args; fills the kernel parameters on success.
-lb_status check_layer(const lb_decode_layer_args *a, LayerParams *out, int *fmt, bool *scaled, bool *ranked) {
-  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: args is NULL");
-  if (a->struct_size < sizeof(lb_decode_layer_args))
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: struct_size %u < %zu", a->struct_size, sizeof(lb_decode_layer_args));
-  if (a->format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: unknown format %u", a->format);
-  const int64_t H = a->hidden, I = a->intermediate;
-  if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0 || a->heads / a->kv_heads > 3 ||
-      H != a->heads * kHeadDim || H > 640 || I < 32 || I > kFusedMaxK || I % 32 != 0)
+static_assert(sizeof(LayerWeights) == 256, "LB_DECODE_STACK_TABLE_BYTES assumes 256 bytes per layer");
+
+// Everything of a decode-layer launch but the per-layer tensors: shapes, format, attention,
+// workspace layout and the role grid.  `layers` regions of LB_DECODE_LAYER_WORDS words follow the
+// workspace header.
+struct LayerShape {
+  uint32_t format;
+  int64_t group_size, hidden, intermediate, heads, kv_heads, capacity, layers;
+  void *h;
+  float eps, scale;
+  const void *cos, *sin;
+  const int64_t *position;
+  void *workspace;
+  size_t workspace_bytes;
+};
+
+lb_status check_shape(const char *who, const LayerShape &a, LayerParams *p, Range *in, int &nin) {
+  if (a.format > LB_FORMAT_FP16) return fail(LB_INVALID_ARGUMENT, "%s: unknown format %u", who, a.format);
+  const int64_t H = a.hidden, I = a.intermediate;
+  if (a.heads < 1 || a.kv_heads < 1 || a.heads % a.kv_heads != 0 || a.heads / a.kv_heads > 3 ||
+      H != a.heads * kHeadDim || H > 640 || I < 32 || I > kFusedMaxK || I % 32 != 0)
     return fail(LB_INVALID_ARGUMENT,
-                "lb_decode_layer: needs hidden = 64 heads <= 640, heads / kv_heads <= 3, intermediate a multiple of 32 "
-                "<= %d", kFusedMaxK);
-  if (a->capacity < 1 || a->capacity > 4096)
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: capacity %lld outside 1..4096", (long long)a->capacity);
-  const bool dense = a->format == LB_FORMAT_FP16;
-  const int64_t g = a->group_size;
-  const bool per_row = a->format == LB_FORMAT_INT8 && g == 0;
+                "%s: needs hidden = 64 heads <= 640, heads / kv_heads <= 3, intermediate a multiple of 32 <= %d", who,
+                kFusedMaxK);
+  if (a.capacity < 1 || a.capacity > 4096)
+    return fail(LB_INVALID_ARGUMENT, "%s: capacity %lld outside 1..4096", who, (long long)a.capacity);
+  if (a.layers < 1 || a.layers > LB_DECODE_STACK_MAX_LAYERS)
+    return fail(LB_INVALID_ARGUMENT, "%s: layers %lld outside 1..%d", who, (long long)a.layers, LB_DECODE_STACK_MAX_LAYERS);
+  const bool dense = a.format == LB_FORMAT_FP16;
+  const int64_t g = a.group_size;
+  const bool per_row = a.format == LB_FORMAT_INT8 && g == 0;
   if (!dense && !per_row && !(pow2(g) && g >= 32 && H % g == 0 && I % g == 0))
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: group_size %lld must be 0 (int8 per row) or a power of two "
-                "(>= 32) dividing hidden and intermediate", (long long)g);
-  if (!a->h || !aligned(a->h, 16) || !a->norm1 || !aligned(a->norm1, 16) || !a->norm2 || !aligned(a->norm2, 16) ||
-      !std::isfinite(a->eps) || a->eps < 0)
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: h, norm1, norm2 must be 16-byte aligned; eps finite >= 0");
-  if (!a->cos || !a->sin || !aligned(a->cos, 2) || !aligned(a->sin, 2) || !a->position || !aligned(a->position, 8) ||
-      !a->keys || !a->values || !aligned(a->keys, 16) || !aligned(a->values, 16) || !std::isfinite(a->scale))
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: attention buffers NULL or misaligned, or scale not finite");
-  const size_t need = LB_DECODE_LAYER_WORKSPACE_BYTES(H, I, a->kv_heads);
-  if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
-    return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: workspace must be 256-byte aligned with %zu bytes", need);
-  const int64_t kv = a->kv_heads * kHeadDim;
-  const int64_t want_n[P_COUNT] = {H, kv, kv, H, I, I, H};
-  const char *names[P_COUNT] = {"q", "k", "v", "o", "gate", "up", "down"};
-  LayerParams p{};
-  bool any_rank = false;
-  const size_t row = kHeadDim * 2, cache = (size_t)a->kv_heads * a->capacity * row;
-  Range in[8 + 4 * P_COUNT];
-  int nin = 0;
-  in[nin++] = range_of(a->norm1, (size_t)H * 2, "norm1");
-  in[nin++] = range_of(a->norm2, (size_t)H * 2, "norm2");
-  in[nin++] = range_of(a->cos, (size_t)a->capacity * row, "cos");
-  in[nin++] = range_of(a->sin, (size_t)a->capacity * row, "sin");
-  in[nin++] = range_of(a->position, sizeof(int64_t), "position");
-  for (int i = 0; i < P_COUNT; ++i) {
-    const lb_fused_problem &q = a->proj[i];
-    const int64_t K = i == P_DOWN ? I : H;
-    if (q.N != want_n[i])
-      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s has N=%lld, expected %lld", names[i], (long long)q.N,
-                  (long long)want_n[i]);
-    if (q.y || q.bias || q.residual)
-      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: y, bias and residual must be NULL", names[i]);
-    if (!q.codes || !aligned(q.codes, 16) || (!dense && (!q.scales || !aligned(q.scales, 2))))
-      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: codes (16-byte aligned) and scales required", names[i]);
-    if (q.rank < 0 || q.rank > LB_FUSED_MAX_RANK)
-      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: rank %lld outside 0..32", names[i], (long long)q.rank);
-    if (q.rank > 0 && (!q.down || !q.up || !aligned(q.down, 16) || !aligned(q.up, 16) || q.up_ld < q.rank ||
-                       q.up_ld % 8 != 0))
-      return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s: correction needs 16-byte aligned down/up, up_ld %% 8 == 0",
-                  names[i]);
-    any_rank = any_rank || q.rank > 0;
-    const int64_t G = dense ? 1 : per_row ? 1 : K / g;
-    in[nin++] = range_of(q.codes, code_bytes(a->format, q.N, K), "codes");
-    in[nin++] = range_of(dense ? nullptr : q.scales, dense ? 0 : (size_t)(q.N * G * 2), "scales");
-    in[nin++] = range_of(q.rank ? q.down : nullptr, q.rank ? (size_t)(q.rank * K * 2) : 0, "down");
-    in[nin++] = range_of(q.rank ? q.up : nullptr, q.rank ? (size_t)((q.N - 1) * q.up_ld + q.rank) * 2 : 0, "up");
-    LayerProblem &d = p.prob[i];
-    d.codes = static_cast<const uint8_t *>(q.codes);
-    d.scales = static_cast<const f16 *>(q.scales);
-    d.down = q.rank ? static_cast<const f16 *>(q.down) : nullptr;
-    d.up = q.rank ? static_cast<const f16 *>(q.up) : nullptr;
-    d.N = (int)q.N;
-    d.rank = (int)q.rank;
-    d.up_ld = (int)q.up_ld;
-  }
-  const Range outs[] = {range_of(a->h, (size_t)H * 2, "h"), range_of(a->keys, cache, "keys"),
-                        range_of(a->values, cache, "values"), range_of(a->workspace, need, "workspace")};
-  for (int o = 0; o < 4; ++o) {
-    for (int r = 0; r < nin; ++r)
-      if (overlaps(outs[o], in[r])) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s overlaps %s", outs[o].name, in[r].name);
-    for (int r = o + 1; r < 4; ++r)
-      if (overlaps(outs[o], outs[r])) return fail(LB_INVALID_ARGUMENT, "lb_decode_layer: %s overlaps %s", outs[o].name, outs[r].name);
-  }
-  p.h = static_cast<f16 *>(a->h);
-  p.norm1 = static_cast<const f16 *>(a->norm1);
-  p.norm2 = static_cast<const f16 *>(a->norm2);
-  p.eps = a->eps;
-  p.hidden = (int)H;
-  p.inter = (int)I;
-  p.per_row = per_row;
+    return fail(LB_INVALID_ARGUMENT, "%s: group_size %lld must be 0 (int8 per row) or a power of two "
+                "(>= 32) dividing hidden and intermediate", who, (long long)g);
+  if (!a.h || !aligned(a.h, 16) || !std::isfinite(a.eps) || a.eps < 0)
+    return fail(LB_INVALID_ARGUMENT, "%s: h must be 16-byte aligned; eps finite >= 0", who);
+  if (!a.cos || !a.sin || !aligned(a.cos, 2) || !aligned(a.sin, 2) || !a.position || !aligned(a.position, 8) ||
+      !std::isfinite(a.scale))
+    return fail(LB_INVALID_ARGUMENT, "%s: RoPE tables or position NULL or misaligned, or scale not finite", who);
+  const size_t need = LB_DECODE_STACK_WORKSPACE_BYTES(H, I, a.kv_heads, a.layers);
+  if (!a.workspace || !aligned(a.workspace, 256) || a.workspace_bytes < need)
+    return fail(LB_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned with %zu bytes", who, need);
+  const size_t row = kHeadDim * 2;
+  in[nin++] = range_of(a.cos, (size_t)a.capacity * row, "cos");
+  in[nin++] = range_of(a.sin, (size_t)a.capacity * row, "sin");
+  in[nin++] = range_of(a.position, sizeof(int64_t), "position");
+  LayerParams q{};
+  q.h = static_cast<f16 *>(a.h);
+  q.eps = a.eps;
+  q.hidden = (int)H;
+  q.inter = (int)I;
+  q.per_row = per_row;
   const int64_t g1 = dense || per_row ? H : g, g2 = dense || per_row ? I : g;
-  p.G1 = (int)(H / g1);
-  p.shift1 = shift_of(g1, H);
-  p.G2 = (int)(I / g2);
-  p.shift2 = shift_of(g2, I);
-  p.cos = static_cast<const f16 *>(a->cos);
-  p.sin = static_cast<const f16 *>(a->sin);
-  p.position = a->position;
-  p.keys = static_cast<f16 *>(a->keys);
-  p.values = static_cast<f16 *>(a->values);
-  p.heads = (int)a->heads;
-  p.kv_heads = (int)a->kv_heads;
-  p.capacity = (int)a->capacity;
-  p.scale = a->scale;
-  p.ws = static_cast<uint64_t *>(a->workspace);
-  p.w_z = 8;
-  p.w_qkv = p.w_z + P_COUNT * kLayerZWords;
-  p.w_att = p.w_qkv + (int)((H + 2 * kv) / 2);
-  p.w_h1 = p.w_att + (int)(H / 2);
-  p.w_gu = p.w_h1 + (int)(H / 2);
-  auto zc = [&](int i) { return (p.prob[i].rank + kFusedZRanks - 1) / kFusedZRanks; };
-  auto tc = [&](int i) { return (p.prob[i].N + 15) / 16; };
-  const int counts[R_COUNT] = {tc(P_Q) + tc(P_K) + tc(P_V), (int)a->heads * kAttnDimSlices, tc(P_O),
-                               tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};
-  int acc = 0;
-  for (int r = 0; r < R_COUNT; ++r) p.end[r] = acc += counts[r];
-  *out = p;
-  *fmt = (int)a->format;
-  *scaled = !dense && !per_row;
-  *ranked = any_rank;
+  q.G1 = (int)(H / g1);
+  q.shift1 = shift_of(g1, H);
+  q.G2 = (int)(I / g2);
+  q.shift2 = shift_of(g2, I);
+  q.cos = static_cast<const f16 *>(a.cos);
+  q.sin = static_cast<const f16 *>(a.sin);
+  q.position = a.position;
+  q.heads = (int)a.heads;
+  q.kv_heads = (int)a.kv_heads;
+  q.capacity = (int)a.capacity;
+  q.scale = a.scale;
+  q.ws = static_cast<uint64_t *>(a.workspace);
+  q.layers = (int)a.layers;
+  q.layer_words = (int)LB_DECODE_LAYER_WORDS(H, I, a.kv_heads);
+  const int64_t kv = a.kv_heads * kHeadDim;
+  q.w_z = 0;
+  q.w_qkv = q.w_z + P_COUNT * kLayerZWords;
+  q.w_att = q.w_qkv + (int)((H + 2 * kv) / 2);
+  q.w_h1 = q.w_att + (int)(H / 2);
+  q.w_gu = q.w_h1 + (int)(H / 2);
+  q.w_h = q.w_gu + (int)I;
+  const int64_t want_n[P_COUNT] = {H, kv, kv, H, I, I, H};
+  for (int i = 0; i < P_COUNT; ++i) q.N[i] = (int)want_n[i];
+  *p = q;
   return ok();
 }
 
-template <int FMT, bool SCALED>
-void launch_layer_t(const LayerParams &p, bool ranked, size_t smem, hipStream_t s) {
-  const dim3 grid((unsigned)p.end[R_COUNT - 1]);
-  if (ranked) hipLaunchKernelGGL((decode_layer_kernel<FMT, SCALED, true>), grid, dim3(256), smem, s, p);
-  else hipLaunchKernelGGL((decode_layer_kernel<FMT, SCALED, false>), grid, dim3(256), smem, s, p);
+// One layer's tensors: shapes against the launch, ranks and U strides equal to those of the first
+// layer (the role grid is shared), into `w`; their byte ranges are appended to `in` / `out`.
+lb_status check_weights(const char *who, int layer, uint32_t format, const lb_fused_problem *proj, const void *norm1,
+                        const void *norm2, void *keys, void *values, LayerParams *p, LayerWeights *w, Range *in,
+                        int &nin, Range *out, int &nout) {
+  static const char *names[P_COUNT] = {"q", "k", "v", "o", "gate", "up", "down"};
+  const bool dense = format == LB_FORMAT_FP16;
+  if (!norm1 || !aligned(norm1, 16) || !norm2 || !aligned(norm2, 16) || !keys || !values || !aligned(keys, 16) ||
+      !aligned(values, 16))
+    return fail(LB_INVALID_ARGUMENT, "%s: layer %d: norm1, norm2, keys, values must be 16-byte aligned", who, layer);
+  const size_t cache = (size_t)p->kv_heads * p->capacity * kHeadDim * 2;
+  in[nin++] = range_of(norm1, (size_t)p->hidden * 2, "norm1");
+  in[nin++] = range_of(norm2, (size_t)p->hidden * 2, "norm2");
+  out[nout++] = range_of(keys, cache, "keys");
+  out[nout++] = range_of(values, cache, "values");
+  LayerWeights d{};
+  for (int i = 0; i < P_COUNT; ++i) {
+    const lb_fused_problem &q = proj[i];
+    const int64_t K = i == P_DOWN ? p->inter : p->hidden;
+    if (q.N != p->N[i])
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s has N=%lld, expected %d", who, layer, names[i], (long long)q.N,
+                  p->N[i]);
+    if (q.y || q.bias || q.residual)
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s: y, bias and residual must be NULL", who, layer, names[i]);
+    if (!q.codes || !aligned(q.codes, 16) || (!dense && (!q.scales || !aligned(q.scales, 2))))
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s: codes (16-byte aligned) and scales required", who, layer,
+                  names[i]);
+    if (q.rank < 0 || q.rank > LB_FUSED_MAX_RANK)
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s: rank %lld outside 0..32", who, layer, names[i], (long long)q.rank);
+    if (q.rank > 0 && (!q.down || !q.up || !aligned(q.down, 16) || !aligned(q.up, 16) || q.up_ld < q.rank ||
+                       q.up_ld % 8 != 0))
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s: correction needs 16-byte aligned down/up, up_ld %% 8 == 0", who,
+                  layer, names[i]);
+    const int up_ld = q.rank ? (int)q.up_ld : 0;
+    if (layer == 0) {
+      p->rank[i] = (int)q.rank;
+      p->up_ld[i] = up_ld;
+    } else if (p->rank[i] != (int)q.rank || p->up_ld[i] != up_ld) {
+      return fail(LB_INVALID_ARGUMENT, "%s: layer %d: %s: rank and up_ld must equal those of layer 0", who, layer,
+                  names[i]);
+    }
+    const int64_t G = dense ? 1 : p->per_row ? 1 : (i == P_DOWN ? p->G2 : p->G1);
+    in[nin++] = range_of(q.codes, code_bytes(format, q.N, K), "codes");
+    in[nin++] = range_of(dense ? nullptr : q.scales, dense ? 0 : (size_t)(q.N * G * 2), "scales");
+    in[nin++] = range_of(q.rank ? q.down : nullptr, q.rank ? (size_t)(q.rank * K * 2) : 0, "down");
+    in[nin++] = range_of(q.rank ? q.up : nullptr, q.rank ? (size_t)((q.N - 1) * q.up_ld + q.rank) * 2 : 0, "up");
+    d.codes[i] = static_cast<const uint8_t *>(q.codes);
+    d.scales[i] = static_cast<const f16 *>(q.scales);
+    d.down[i] = q.rank ? static_cast<const f16 *>(q.down) : nullptr;
+    d.up[i] = q.rank ? static_cast<const f16 *>(q.up) : nullptr;
+  }
+  d.norm1 = static_cast<const f16 *>(norm1);
+  d.norm2 = static_cast<const f16 *>(norm2);
+  d.keys = static_cast<f16 *>(keys);
+  d.values = static_cast<f16 *>(values);
+  *w = d;
+  return ok();
+}
+
+lb_status check_overlaps(const char *who, const Range *in, int nin, const Range *out, int nout) {
+  for (int o = 0; o < nout; ++o) {
+    for (int r = 0; r < nin; ++r)
+      if (overlaps(out[o], in[r])) return fail(LB_INVALID_ARGUMENT, "%s: %s overlaps %s", who, out[o].name, in[r].name);
+    for (int r = o + 1; r < nout; ++r)
+      if (overlaps(out[o], out[r])) return fail(LB_INVALID_ARGUMENT, "%s: %s overlaps %s", who, out[o].name, out[r].name);
+  }
+  return ok();
+}
+
+// The role grid (T_QKV, ATTN, T_O, T_GU, Z_D, T_D) and the launch's template choice.
+void finish_params(LayerParams *p, uint32_t format, int64_t group_size, int *fmt, bool *scaled, bool *ranked) {
+  auto zc = [&](int i) { return (p->rank[i] + kFusedZRanks - 1) / kFusedZRanks; };
+  auto tc = [&](int i) { return (p->N[i] + 15) / 16; };
+  const int counts[R_COUNT] = {tc(P_Q) + tc(P_K) + tc(P_V), p->heads * kAttnDimSlices, tc(P_O),
+                               tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};
+  int acc = 0;
+  for (int r = 0; r < R_COUNT; ++r) p->end[r] = acc += counts[r];
+  bool any = false;
+  for (int i = 0; i < P_COUNT; ++i) any = any || p->rank[i] > 0;
+  *fmt = (int)format;
+  *scaled = format != LB_FORMAT_FP16 && !(format == LB_FORMAT_INT8 && group_size == 0);
+  *ranked = any;
+}
+
+// Dynamic LDS: the largest role (a 1536-long tile: staged row, scales, U rows, reductions, NF4
+// table) or the attention (its rows, the P.V partials and one float per cache slot).
+size_t layer_smem(const LayerParams &p) { return std::max<size_t>(9216, 2048 + (size_t)4 * p.capacity); }
+
+template <int FMT, bool SCALED, bool RANKED, bool STACK>
+const void *layer_kernel_fn() {
+  return reinterpret_cast<const void *>(&decode_layer_kernel<FMT, SCALED, RANKED, STACK>);
+}
+
+template <bool STACK>
+const void *layer_kernel(int fmt, bool scaled, bool ranked) {
+  switch (fmt) {
+    case FMT_INT8:
+      if (scaled) return ranked ? layer_kernel_fn<FMT_INT8, true, true, STACK>() : layer_kernel_fn<FMT_INT8, true, false, STACK>();
+      return ranked ? layer_kernel_fn<FMT_INT8, false, true, STACK>() : layer_kernel_fn<FMT_INT8, false, false, STACK>();
+    case FMT_INT4: return ranked ? layer_kernel_fn<FMT_INT4, true, true, STACK>() : layer_kernel_fn<FMT_INT4, true, false, STACK>();
+    case FMT_NF4: return ranked ? layer_kernel_fn<FMT_NF4, true, true, STACK>() : layer_kernel_fn<FMT_NF4, true, false, STACK>();
+    default: return ranked ? layer_kernel_fn<FMT_FP16, false, true, STACK>() : layer_kernel_fn<FMT_FP16, false, false, STACK>();
+  }
+}
+
+lb_status launch_layers(const char *who, const void *fn, const LayerParams &p, const LayerWeights *table, hipStream_t s) {
+  LayerParams args = p;
+  const LayerWeights *tab = table;
+  void *kargs[] = {&args, &tab};
+  const hipError_t e = hipLaunchKernel(fn, dim3((unsigned)p.end[R_COUNT - 1]), dim3(256), kargs, layer_smem(p), s);
+  if (e != hipSuccess) {
+    char reason[256];
+    snprintf(reason, sizeof reason, "%s: launch failed: %s", who, hipGetErrorString(e));
+    mark_failed(reason);
+    return fail(LB_DEVICE_FAILED, "%s", reason);
+  }
+  return launch_status(who);
+}
+
+// Tables written by lb_decode_stack_prepare: the bytes, so a later call can verify that its
+// arguments describe the same layers, and whether the device holds the stacked grid at once.
+struct PreparedTable {
+  std::vector<LayerWeights> rows;
+  bool resident;
+};
+std::mutex &table_mutex() {
+  static std::mutex m;
+  return m;
+}
+std::map<const void *, PreparedTable> &table_registry() {
+  static std::map<const void *, PreparedTable> r;
+  return r;
+}
+
+lb_status check_stack(const char *who, const lb_decode_stack_args *a, LayerParams *p, std::vector<LayerWeights> *rows,
+                      int *fmt, bool *scaled, bool *ranked) {
+  if (!a) return fail(LB_INVALID_ARGUMENT, "%s: args is NULL", who);
+  if (a->struct_size < sizeof(lb_decode_stack_args))
+    return fail(LB_INVALID_ARGUMENT, "%s: struct_size %u < %zu", who, a->struct_size, sizeof(lb_decode_stack_args));
+  const LayerShape shape{a->format, a->group_size, a->hidden, a->intermediate, a->heads, a->kv_heads, a->capacity,
+                         a->layers, a->h, a->eps, a->scale, a->cos, a->sin, a->position, a->workspace,
+                         a->workspace_bytes};
+  const int L = a->layers >= 1 && a->layers <= LB_DECODE_STACK_MAX_LAYERS ? (int)a->layers : 1;
+  std::vector<Range> in((size_t)L * (2 + 4 * P_COUNT) + 8), out((size_t)L * 2 + 8);
+  int nin = 0, nout = 0;
+  if (const lb_status st = check_shape(who, shape, p, in.data(), nin); st != LB_OK) return st;
+  if (!a->layer) return fail(LB_INVALID_ARGUMENT, "%s: layer array is NULL", who);
+  if (!a->table || !aligned(a->table, 256) || a->table_bytes < LB_DECODE_STACK_TABLE_BYTES(a->layers))
+    return fail(LB_INVALID_ARGUMENT, "%s: table must be 256-byte aligned with %zu bytes", who,
+                (size_t)LB_DECODE_STACK_TABLE_BYTES(a->layers));
+  rows->assign((size_t)L, LayerWeights{});
+  for (int l = 0; l < L; ++l) {
+    const lb_decode_stack_layer &y = a->layer[l];
+    if (const lb_status st = check_weights(who, l, a->format, y.proj, y.norm1, y.norm2, y.keys, y.values, p,
+                                           &(*rows)[(size_t)l], in.data(), nin, out.data(), nout);
+        st != LB_OK)
+      return st;
+  }
+  out[nout++] = range_of(a->h, (size_t)a->hidden * 2, "h");
+  out[nout++] = range_of(a->workspace, LB_DECODE_STACK_WORKSPACE_BYTES(a->hidden, a->intermediate, a->kv_heads, a->layers),
+                         "workspace");
+  out[nout++] = range_of(a->table, LB_DECODE_STACK_TABLE_BYTES(a->layers), "table");
+  if (const lb_status st = check_overlaps(who, in.data(), nin, out.data(), nout); st != LB_OK) return st;
+  finish_params(p, a->format, a->group_size, fmt, scaled, ranked);
+  return ok();
 }
 
 }  // namespace
 
 extern "C" lb_status lb_decode_layer(const lb_decode_layer_args *a, void *stream) {
-  if (const lb_status bad = refuse_if_failed("lb_decode_layer"); bad != LB_OK) return bad;
+  const char *who = "lb_decode_layer";
+  if (const lb_status bad = refuse_if_failed(who); bad != LB_OK) return bad;
+  if (!a) return fail(LB_INVALID_ARGUMENT, "%s: args is NULL", who);
+  if (a->struct_size < sizeof(lb_decode_layer_args))
+    return fail(LB_INVALID_ARGUMENT, "%s: struct_size %u < %zu", who, a->struct_size, sizeof(lb_decode_layer_args));
+  const LayerShape shape{a->format, a->group_size, a->hidden, a->intermediate, a->heads, a->kv_heads, a->capacity,
+                         1, a->h, a->eps, a->scale, a->cos, a->sin, a->position, a->workspace, a->workspace_bytes};
+  Range in[8 + 2 + 4 * P_COUNT], out[8];
+  int nin = 0, nout = 0;
   LayerParams p;
+  if (const lb_status st = check_shape(who, shape, &p, in, nin); st != LB_OK) return st;
+  if (const lb_status st = check_weights(who, 0, a->format, a->proj, a->norm1, a->norm2, a->keys, a->values, &p, &p.w,
+                                         in, nin, out, nout);
+      st != LB_OK)
+    return st;
+  out[nout++] = range_of(a->h, (size_t)a->hidden * 2, "h");
+  out[nout++] = range_of(a->workspace, LB_DECODE_LAYER_WORKSPACE_BYTES(a->hidden, a->intermediate, a->kv_heads),
+                         "workspace");
+  if (const lb_status st = check_overlaps(who, in, nin, out, nout); st != LB_OK) return st;
   int fmt;
   bool scaled, ranked;
-  const lb_status st = check_layer(a, &p, &fmt, &scaled, &ranked);
-  if (st != LB_OK) return st;
-  // Dynamic LDS: the largest role (a 1536-long tile: staged row, scales, U rows, reductions, NF4
-  // table) or the attention (its rows and one float per cache slot).
-  const size_t smem = std::max<size_t>(9216, 2048 + (size_t)4 * p.capacity);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (fmt) {
-    case FMT_INT8: scaled ? launch_layer_t<FMT_INT8, true>(p, ranked, smem, s) : launch_layer_t<FMT_INT8, false>(p, ranked, smem, s); break;
-    case FMT_INT4: launch_layer_t<FMT_INT4, true>(p, ranked, smem, s); break;
-    case FMT_NF4: launch_layer_t<FMT_NF4, true>(p, ranked, smem, s); break;
-    default: launch_layer_t<FMT_FP16, false>(p, ranked, smem, s); break;
+  finish_params(&p, a->format, a->group_size, &fmt, &scaled, &ranked);
+  return launch_layers(who, layer_kernel<false>(fmt, scaled, ranked), p, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" lb_status lb_decode_stack_prepare(const lb_decode_stack_args *a, void *stream) {
+  const char *who = "lb_decode_stack_prepare";
+  if (const lb_status bad = refuse_if_failed(who); bad != LB_OK) return bad;
+  LayerParams p;
+  std::vector<LayerWeights> rows;
+  int fmt;
+  bool scaled, ranked;
+  if (const lb_status st = check_stack(who, a, &p, &rows, &fmt, &scaled, &ranked); st != LB_OK) return st;
+  // Residency: every workgroup of the stacked grid must be on the device at once.
+  int device = 0, cus = 0, per_cu = 0;
+  const void *fn = layer_kernel<true>(fmt, scaled, ranked);
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, layer_smem(p)) != hipSuccess)
+    return fail(LB_DEVICE_FAILED, "%s: device query failed", who);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(a->table, rows.data(), rows.size() * sizeof(LayerWeights), hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    mark_failed("lb_decode_stack_prepare: table copy failed");
+    return fail(LB_DEVICE_FAILED, "%s: table copy failed", who);
   }
-  return launch_status("lb_decode_layer");
+  std::lock_guard<std::mutex> lock(table_mutex());
+  table_registry()[a->table] = PreparedTable{std::move(rows), (long long)per_cu * cus >= p.end[R_COUNT - 1]};
+  return ok();
+}
+
+extern "C" lb_status lb_decode_stack(const lb_decode_stack_args *a, void *stream) {
+  const char *who = "lb_decode_stack";
+  if (const lb_status bad = refuse_if_failed(who); bad != LB_OK) return bad;
+  LayerParams p;
+  std::vector<LayerWeights> rows;
+  int fmt;
+  bool scaled, ranked;
+  if (const lb_status st = check_stack(who, a, &p, &rows, &fmt, &scaled, &ranked); st != LB_OK) return st;
+  {
+    std::lock_guard<std::mutex> lock(table_mutex());
+    const auto it = table_registry().find(a->table);
+    if (it == table_registry().end() || it->second.rows.size() != rows.size() ||
+        std::memcmp(it->second.rows.data(), rows.data(), rows.size() * sizeof(LayerWeights)) != 0)
+      return fail(LB_INVALID_ARGUMENT, "%s: table was not prepared (lb_decode_stack_prepare) for these layers", who);
+    if (!it->second.resident)
+      return fail(LB_UNSUPPORTED, "%s: the device cannot hold the %d workgroups of the stacked grid at once", who,
+                  p.end[R_COUNT - 1]);
+  }
+  return launch_layers(who, layer_kernel<true>(fmt, scaled, ranked), p, static_cast<const LayerWeights *>(a->table),
+                       static_cast<hipStream_t>(stream));
 }

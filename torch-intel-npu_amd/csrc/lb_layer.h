@@ -39,29 +39,51 @@ enum LayerRole { R_TQKV, R_ATTN, R_TO, R_TGU, R_ZD, R_TD, R_COUNT };
 enum LayerProj { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, P_COUNT };
 enum LayerSource { SRC_H, SRC_ATT, SRC_H1, SRC_GU };
 
-struct LayerProblem {
-  const uint8_t *codes;   // packed codes [N, K] (fp16 weights for FMT_FP16)
-  const f16 *scales;      // [N, G]
-  const f16 *down;        // V [rank, K] or null
-  const f16 *up;          // U [N, up_ld] or null
-  int N, rank, up_ld;
+// Device addresses of one layer's tensors (read by every role of that layer).
+struct LayerWeights {
+  const uint8_t *codes[P_COUNT];  // packed codes [N, K] (fp16 weights for FMT_FP16)
+  const f16 *scales[P_COUNT];     // [N, G]
+  const f16 *down[P_COUNT];       // V [rank, K] or null
+  const f16 *up[P_COUNT];         // U [N, up_ld] or null
+  const f16 *norm1, *norm2;       // [hidden] RMSNorm weights
+  f16 *keys, *values;             // [kv_heads, capacity, 64]
 };
 
 struct LayerParams {
-  f16 *h;                   // [hidden] residual row: the layer's input, overwritten by its output
-  const f16 *norm1, *norm2; // [hidden] RMSNorm weights
+  f16 *h;                   // [hidden] residual row: the first layer's input, overwritten by the last layer's output
   float eps;
   int hidden, inter;        // K of q/k/v/o/gate/up, K of down
   int G1, shift1, G2, shift2, per_row;
-  LayerProblem prob[P_COUNT];
+  int N[P_COUNT], rank[P_COUNT], up_ld[P_COUNT];  // the same in every layer
   const f16 *cos, *sin;     // [capacity, 64]
   const int64_t *position;  // device scalar: the slot of the new token
-  f16 *keys, *values;       // [kv_heads, capacity, 64]
   int heads, kv_heads, capacity;
   float scale;
-  uint64_t *ws;             // workspace words: [0] passed, [1] timeout, then the regions below
-  int w_z, w_qkv, w_att, w_h1, w_gu;
+  uint64_t *ws;             // workspace words: [0] passed, [1] timeout, then one region per layer
+  int layers, layer_words;  // layers of the launch, words per layer region
+  int w_z, w_qkv, w_att, w_h1, w_gu, w_h;  // word offsets within a layer's region
   int end[R_COUNT];         // exclusive prefix sums of workgroups per role
+  LayerWeights w;           // the layer of a single-layer launch (lb_decode_layer)
+};
+
+constexpr int kLayerHeaderWords = 8;
+
+// Entry i of a per-projection array by a chain of selects (i is wave-uniform), so no array of the
+// kernel parameters is indexed at run time (which would make the compiler copy them to scratch).
+template <class T, int N>
+__device__ __forceinline__ T pick(const T (&a)[N], int i) {
+  T v = a[0];
+#pragma unroll
+  for (int q = 1; q < N; ++q) v = i == q ? a[q] : v;
+  return v;
+}
+
+// Where one layer's words live: its region (word index into the workspace), the next layer's
+// region (whose h words receive this layer's output; -1 for the last layer, which writes h), and
+// whether the layer input is the plain row h (the first layer) or the previous layer's h words.
+struct LayerCtx {
+  int lw, nw;
+  bool first;
 };
 
 constexpr int kLayerSpinLimit = 1 << 18;
@@ -99,7 +121,9 @@ __device__ __forceinline__ uint64_t wait_word(const LayerParams &p, const uint64
   if (__builtin_expect(word_tag(w) != tag, 0)) {
 #pragma nounroll
     for (int it = 0; word_tag(w) != tag; ++it) {
-      if (it == kLayerSpinLimit) {
+      // Give up at the limit, or at once after any wait of the launch timed out (checked every 64
+      // polls), so a launch whose waits fail still ends promptly.
+      if (it == kLayerSpinLimit || ((it & 63) == 63 && (uint32_t)sys_load(p.ws + 1) != 0u)) {
         layer_timeout(p);
         break;
       }
@@ -120,13 +144,13 @@ __device__ __forceinline__ void wait_sentinel(const LayerParams &p, const uint64
 // coherence of the system-scope atomics above).
 constexpr int kSysCoherent = 17;
 
-// The workspace as a buffer (its last region, gate|up, ends the words the kernel touches).
+// The workspace as a buffer over the header and every layer region.
 // Built from readfirstlane copies, so the descriptor stays in scalar registers after the
 // divergent wait that precedes its use.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(const LayerParams &p) {
   const uint64_t a = reinterpret_cast<uint64_t>(p.ws);
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const uint32_t words = __builtin_amdgcn_readfirstlane((uint32_t)(p.w_gu + p.inter));
+  const uint32_t words = __builtin_amdgcn_readfirstlane((uint32_t)(kLayerHeaderWords + p.layers * p.layer_words));
   return buffer_rsrc(reinterpret_cast<const uint64_t *>(((uint64_t)hi << 32) | lo), (size_t)words * 8);
 }
 
@@ -162,11 +186,10 @@ __device__ __forceinline__ h8 words4_to_h8(const uint64_t (&w)[4]) {
 // and the prologue's second row (gamma, or the up half for SiLU-multiply).  Every word of the
 // thread is requested at once; only words still stale are then waited for one by one.
 template <int XB>
-__device__ __forceinline__ void layer_source_row(const LayerParams &p, int src, int K, uint32_t tag, h8 (&xv)[XB],
-                                                 h8 (&av)[XB]) {
+__device__ __forceinline__ void layer_source_row(const LayerParams &p, int base, int src, int K, uint32_t tag,
+                                                 h8 (&xv)[XB], h8 (&av)[XB]) {
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, blocks = K >> 3;
-  const int base = src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu;
   const int second = base + p.inter / 2;
   const __amdgpu_buffer_rsrc_t wb = workspace_rsrc(p);
   uint64_t wx[XB][4], wa[XB][4];
@@ -196,10 +219,15 @@ __device__ __forceinline__ void layer_source_row(const LayerParams &p, int src, 
 // The word a consumer of a word source polls before reading the rest: one chosen by the
 // workgroup's index, so the consumers of a stage spread their polls over the stage's words
 // instead of all polling one address.
-__device__ __forceinline__ const uint64_t *source_sentinel(const LayerParams &p, int src) {
+__device__ __forceinline__ const uint64_t *source_sentinel(const LayerParams &p, int base, int src) {
   const int words = src == SRC_GU ? p.inter : p.hidden / 2;
-  const int base = src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu;
   return p.ws + base + (int)((blockIdx.x * 37u) % (unsigned)words);
+}
+
+// The word index of a source's region in this layer, or -1 for the plain row h (first layer input).
+__device__ __forceinline__ int source_base(const LayerParams &p, const LayerCtx &c, int src) {
+  if (src == SRC_H) return c.first ? -1 : c.lw + p.w_h;
+  return c.lw + (src == SRC_ATT ? p.w_att : src == SRC_H1 ? p.w_h1 : p.w_gu);
 }
 
 __device__ __forceinline__ float layer_inv(int prologue, int K, float eps, float sumsq_total) {
@@ -242,21 +270,21 @@ struct RoleShape {
   int src, prologue, K;
   const f16 *gamma;
 };
-__device__ __forceinline__ RoleShape role_shape(const LayerParams &p, int pi) {
-  if (pi <= P_V) return {SRC_H, PRO_RMSNORM, p.hidden, p.norm1};
+__device__ __forceinline__ RoleShape role_shape(const LayerParams &p, const LayerWeights &W, int pi) {
+  if (pi <= P_V) return {SRC_H, PRO_RMSNORM, p.hidden, W.norm1};
   if (pi == P_O) return {SRC_ATT, PRO_NONE, p.hidden, nullptr};
-  if (pi <= P_UP) return {SRC_H1, PRO_RMSNORM, p.hidden, p.norm2};
+  if (pi <= P_UP) return {SRC_H1, PRO_RMSNORM, p.hidden, W.norm2};
   return {SRC_GU, PRO_SILU_MUL, p.inter, nullptr};
 }
 
 // Loads the plain source row (the layer input h) and the prologue's gamma row, straight-line.
 template <int XB>
-__device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const RoleShape &rs, h8 (&xv)[XB],
-                                                  h8 (&av)[XB]) {
+__device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const LayerCtx &c, const RoleShape &rs,
+                                                  h8 (&xv)[XB], h8 (&av)[XB]) {
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, blocks = rs.K >> 3;
   const size_t kb = (size_t)rs.K * 2;
-  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.h, rs.src == SRC_H ? kb : 0);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.h, rs.src == SRC_H && c.first ? kb : 0);
   const __amdgpu_buffer_rsrc_t gbuf = buffer_rsrc(rs.gamma, rs.gamma ? kb : 0);
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
@@ -269,22 +297,22 @@ __device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const Ro
 // ---------------------------------------------------------------- z workgroups
 // Ranks [6 zi, 6 zi + 6) of problem pi: z = fp16(x'.V^T), published as two tagged words.
 template <int KMAX>
-__device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int zi, uint64_t passed, f16 *xs,
-                                             float *wsum, f16 *zsh) {
+__device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W, int pi,
+                                             int zi, uint64_t passed, f16 *xs, float *wsum, f16 *zsh) {
   constexpr int TPR = 32;
   constexpr int ZI = (KMAX / 8 + TPR - 1) / TPR;
   constexpr int XB = (KMAX / 8 + 255) / 256;
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x;
-  const RoleShape rs = role_shape(p, pi);
-  const LayerProblem &Z = p.prob[pi];
+  const RoleShape rs = role_shape(p, W, pi);
   const int K = rs.K, blocks = K >> 3;
   const int r0 = zi * kFusedZRanks;
   const int rr = t / TPR, li = t % TPR;
-  const bool live = rr < kFusedZRanks && r0 + rr < Z.rank;
+  const int zrank = pick(p.rank, pi);
+  const bool live = rr < kFusedZRanks && r0 + rr < zrank;
   h8 xv[XB], av[XB];
-  layer_plain_loads(p, rs, xv, av);
-  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(Z.down, (size_t)Z.rank * K * 2);
+  layer_plain_loads(p, c, rs, xv, av);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(pick(W.down, pi), (size_t)zrank * K * 2);
   u4 vz[ZI];
 #pragma unroll
   for (int i = 0; i < ZI; ++i) {
@@ -293,13 +321,15 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int z
     vz[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // the previous layer's LDS reads are done before this layer writes
   const uint32_t tag = layer_tag(p, passed);
-  if (rs.src != SRC_H) {
+  const int src_base = source_base(p, c, rs.src);
+  if (src_base >= 0) {
     h8 gamma_rows[XB];
 #pragma unroll
     for (int i = 0; i < XB; ++i) gamma_rows[i] = av[i];
-    wait_sentinel(p, source_sentinel(p, rs.src), tag);
-    layer_source_row(p, rs.src, K, tag, xv, av);
+    wait_sentinel(p, source_sentinel(p, src_base, rs.src), tag);
+    layer_source_row(p, src_base, rs.src, K, tag, xv, av);
     if (rs.src != SRC_GU) {
 #pragma unroll
       for (int i = 0; i < XB; ++i) av[i] = gamma_rows[i];
@@ -336,7 +366,7 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int z
     const uint64_t word = (uint64_t)tag | ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t]) << 16) |
                           ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 1]) << 32) |
                           ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 2]) << 48);
-    sys_store(p.ws + p.w_z + pi * kLayerZWords + 2 * zi + t, word);
+    sys_store(p.ws + c.lw + p.w_z + pi * kLayerZWords + 2 * zi + t, word);
   }
 }
 
@@ -345,7 +375,8 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, int pi, int z
 // q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
 // residual h1).
 template <int FMT, bool SCALED, int KMAX, bool RANKED, bool OWN_Z>
-__device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, int n0, uint64_t passed, uint8_t *smem) {
+__device__ __forceinline__ void layer_tile_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W, int pi,
+                                                int n0, uint64_t passed, uint8_t *smem) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
   constexpr int KSTEP = 4 * CPL;
@@ -372,36 +403,35 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const RoleShape rs = role_shape(p, pi);
-  const LayerProblem &P = p.prob[pi];
-  const int K = rs.K;
+  const RoleShape rs = role_shape(p, W, pi);
+  const int K = rs.K, N = pick(p.N, pi), up_ld = pick(p.up_ld, pi);
   const int G = K == p.hidden ? p.G1 : p.G2;
   const int group_shift = K == p.hidden ? p.shift1 : p.shift2;
-  const int rows = min(16, P.N - n0);
+  const int rows = min(16, N - n0);
   const int row_bytes = K * BITS / 8;
-  const int rank = RANKED ? P.rank : 0;
+  const int rank = RANKED ? pick(p.rank, pi) : 0;
 
-  // Wave 0, lane r < rows: the row's per-row scale and (o) its residual h value.
+  // Wave 0, lane r < rows: the row's per-row scale and (o, first layer) its residual h value.
   const f16 rscale = __builtin_bit_cast(
-      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(P.scales, p.per_row && wave == 0 ? (size_t)P.N * 2 : 0),
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pick(W.scales, pi), p.per_row && wave == 0 ? (size_t)N * 2 : 0),
                                                 lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
   const f16 rres = __builtin_bit_cast(
-      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.h, pi == P_O && wave == 0 ? (size_t)P.N * 2 : 0),
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.h, pi == P_O && c.first && wave == 0 ? (size_t)N * 2 : 0),
                                                 lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
   u4 ureg = {0u, 0u, 0u, 0u};
   if constexpr (RANKED) {
     const int ur = 4 * wave + (lane >> 2), uq = lane & 3;
-    const int off = lane < 16 && ur < rows && uq * 8 < rank ? ((n0 + ur) * P.up_ld + uq * 8) * 2 : kOutOfRange;
+    const int off = lane < 16 && ur < rows && uq * 8 < rank ? ((n0 + ur) * up_ld + uq * 8) * 2 : kOutOfRange;
     ureg = __builtin_bit_cast(
-        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(P.up, rank > 0 ? (size_t)P.N * P.up_ld * 2 : 0), off, 0, 0));
+        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(pick(W.up, pi), rank > 0 ? (size_t)N * up_ld * 2 : 0), off, 0, 0));
   }
   h8 xv[XB], av[XB];
-  layer_plain_loads(p, rs, xv, av);
+  layer_plain_loads(p, c, rs, xv, av);
   // Own z: thread t holds blocks t % 8 + 8 i of V row t / 8 (zeros past the rank and K).
   const int vr = t >> 3, vpart = t & 7;
   u4 vreg[VB > 0 ? VB : 1];
   if constexpr (OWN_Z) {
-    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(P.down, rank > 0 ? (size_t)rank * K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(pick(W.down, pi), rank > 0 ? (size_t)rank * K * 2 : 0);
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const int k = (vpart + 8 * i) * 8;
@@ -411,12 +441,12 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   }
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
-    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)n0 * G, (size_t)rows * G * 2);
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(pick(W.scales, pi) + (size_t)n0 * G, (size_t)rows * G * 2);
 #pragma unroll
     for (int i = 0; i < SC; ++i)
       sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
   }
-  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(P.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(pick(W.codes, pi) + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
   u4 w[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) {
@@ -425,6 +455,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
     w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // the previous layer's epilogue has read the LDS this layer overwrites
   const uint32_t tag = layer_tag(p, passed);
 
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
@@ -437,13 +468,14 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
       if (t + i * 256 < 16 * GMAX) ss[t + i * 256] = sreg[i];
     if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;
   }
-  // The source row: the layer input (loaded above) or the words of an earlier role.
-  if (rs.src != SRC_H) {
+  // The source row: the first layer's input (loaded above) or the words of an earlier role.
+  const int src_base = source_base(p, c, rs.src);
+  if (src_base >= 0) {
     h8 gamma_rows[XB];
 #pragma unroll
     for (int i = 0; i < XB; ++i) gamma_rows[i] = av[i];
-    wait_sentinel(p, source_sentinel(p, rs.src), tag);
-    layer_source_row(p, rs.src, K, tag, xv, av);
+    wait_sentinel(p, source_sentinel(p, src_base, rs.src), tag);
+    layer_source_row(p, src_base, rs.src, K, tag, xv, av);
     if (rs.src != SRC_GU) {
 #pragma unroll
       for (int i = 0; i < XB; ++i) av[i] = gamma_rows[i];
@@ -520,7 +552,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   if constexpr (RANKED && !OWN_Z) {
     if (rank > 0) {
       const int words = (rank + 2) / 3;
-      const uint64_t *zw = p.ws + p.w_z + pi * kLayerZWords;
+      const uint64_t *zw = p.ws + c.lw + p.w_z + pi * kLayerZWords;
       if (lane < kFusedZWordsPerProblem) {  // every zs entry, zero from rank on
         const uint64_t word = lane < words ? wait_word(p, zw + lane, tag) : 0;
 #pragma unroll
@@ -531,9 +563,14 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
       __builtin_amdgcn_wave_barrier();
     }
   }
+  // Residuals: o adds the layer input h (plain in the first layer, else the h words, final since
+  // the attention words this tile read depend on them); down adds h1 (final: the gate|up words
+  // this tile read depend on it).
   f16 residual = rres;
-  if (pi == P_DOWN && lane < rows)  // h1 is final: the gate|up words this tile read depend on it
-    residual = word_half(wait_word(p, p.ws + p.w_h1 + (n0 + lane) / 2, tag), (n0 + lane) & 1);
+  if (((pi == P_O && !c.first) || pi == P_DOWN) && lane < rows) {
+    const int rw = c.lw + (pi == P_O ? p.w_h : p.w_h1) + (n0 + lane) / 2;
+    residual = word_half(wait_word(p, p.ws + rw, tag), (n0 + lane) & 1);
+  }
   float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
   if (p.per_row) sum *= (float)rscale;
   f16 hv = (f16)sum;
@@ -544,20 +581,21 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
   if (pi == P_O || pi == P_DOWN) hv = (f16)((float)residual + (float)hv);
   const f16 next = __builtin_bit_cast(f16, (uint16_t)dpp_move<kDppRowShl1>((int)__builtin_bit_cast(uint16_t, hv)));
   if (g != 0 || j >= rows) return;
-  if (pi == P_DOWN) {
+  if (pi == P_DOWN && c.nw < 0) {  // the last layer's output: the plain row h
     p.h[n0 + j] = hv;
     return;
   }
   if (j & 1) return;
-  int region, off;
+  int region, off = 0;
   if (pi <= P_V) {
-    region = p.w_qkv;
-    off = pi == P_Q ? 0 : pi == P_K ? p.prob[P_Q].N : p.prob[P_Q].N + p.prob[P_K].N;
+    region = c.lw + p.w_qkv;
+    off = pi == P_Q ? 0 : pi == P_K ? p.N[P_Q] : p.N[P_Q] + p.N[P_K];
   } else if (pi == P_O) {
-    region = p.w_h1;
-    off = 0;
+    region = c.lw + p.w_h1;
+  } else if (pi == P_DOWN) {
+    region = c.nw + p.w_h;  // the next layer's input
   } else {
-    region = p.w_gu;
+    region = c.lw + p.w_gu;
     off = pi == P_GATE ? 0 : p.inter;
   }
   sys_store(p.ws + region + (off + n0 + j) / 2, pair_word(tag, hv, next));
@@ -566,7 +604,8 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, int pi, in
 // ---------------------------------------------------------------- attention
 // Query head h, output dims [d0, d0 + kSliceDims): the staging of decode_attention_kernel on q, k
 // and v rows read from the q|k|v words; the output dims are published as att words.
-__device__ __forceinline__ void layer_attention_role(const LayerParams &p, int idx, uint64_t passed, uint8_t *smem) {
+__device__ __forceinline__ void layer_attention_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W,
+                                                     int idx, uint64_t passed, uint8_t *smem) {
   f16 *qs = reinterpret_cast<f16 *>(smem);               // [64] raw, then rotated
   f16 *kn = qs + kHeadDim;                               // [64]
   f16 *vn = kn + kHeadDim;                               // [64]
@@ -586,8 +625,8 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
   const int cpos = valid ? pos : 0;
   const size_t head_base = (size_t)kvh * p.capacity * kHeadDim;
   // Cached rows (slots below pos) and the RoPE row, issued before the wait for q, k, v.
-  const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(p.keys + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
-  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(p.values + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t kbuf = buffer_rsrc(W.keys + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(W.values + head_base, valid ? (size_t)pos * kHeadDim * 2 : 0);
   const int blk = t % kSliceBlocks, part = t / kSliceBlocks;
   u4 kreg[kScoreSlots][kHeadDim / 8];
   u4 vreg[kValueSlots];
@@ -617,11 +656,12 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
   const f16 cv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(cbuf, d * 2, 0, 0));
   const f16 sv = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(snbuf, d * 2, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // the previous layer's LDS reads are done before this layer writes
   const uint32_t tag = layer_tag(p, passed);
 
   // q of head h, k and v of KV head kvh: 96 words from the q|k|v region.
-  const int nq = p.prob[P_Q].N, nk = p.prob[P_K].N;
-  const uint64_t *qkv = p.ws + p.w_qkv;
+  const int nq = p.N[P_Q], nk = p.N[P_K];
+  const uint64_t *qkv = p.ws + c.lw + p.w_qkv;
   wait_sentinel(p, qkv + (nq + nk + (kvh + 1) * kHeadDim) / 2 - 1, tag);
   if (t < 3 * kHeadDim / 2) {
     const int part3 = t / (kHeadDim / 2), wi = t % (kHeadDim / 2);
@@ -644,13 +684,13 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
     if (t < kSliceDims) {
       f16 nan = (f16)__builtin_nanf("");
       if ((t & 1) == 0)
-        sys_store(p.ws + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, nan, nan));
+        sys_store(p.ws + c.lw + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, nan, nan));
     }
     return;
   }
   if (h % group == 0 && idx % kAttnDimSlices == 0 && t < 2 * kHeadDim) {
     const int dd = t & 63;
-    f16 *dst = (t < kHeadDim ? p.keys : p.values) + head_base + (size_t)pos * kHeadDim + dd;
+    f16 *dst = (t < kHeadDim ? W.keys : W.values) + head_base + (size_t)pos * kHeadDim + dd;
     *dst = t < kHeadDim ? kn[dd] : vn[dd];
   }
 
@@ -719,13 +759,21 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, int i
   __syncthreads();
   if (t < kSliceDims && (t & 1) == 0) {
     const f16 a = (f16)pv_total(pv, t), b = (f16)pv_total(pv, t + 1);
-    sys_store(p.ws + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, a, b));
+    sys_store(p.ws + c.lw + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, a, b));
   }
 }
 
 // ---------------------------------------------------------------- the kernel
-template <int FMT, bool SCALED, bool RANKED>
-__global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p) {
+// One layer (STACK false: the weights in the parameters) or p.layers layers (STACK true: the
+// weights in `table`, one entry per layer) per launch.  In a stacked launch every workgroup keeps
+// its role through all layers: after finishing its part of layer l it issues the loads of layer
+// l + 1 and waits there, so weights are fetched while earlier stages run, and layer l + 1's
+// inputs arrive as the h words of layer l's down tiles.  A workgroup then also waits for
+// workgroups dispatched after it (the previous layer's later roles), so a stacked grid must be
+// resident all at once: the host launches it only when the device holds every workgroup
+// together, and the bounded waits end the launch (with a timeout recorded) should it not.
+template <int FMT, bool SCALED, bool RANKED, bool STACK>
+__global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p, const LayerWeights *__restrict__ table) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float wsum[4];
   __shared__ f16 zsh[8];
@@ -733,37 +781,63 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p) {
   const uint64_t passed = sys_load(p.ws);  // waited for only where a role first needs the tag
   const int role = b < p.end[R_TQKV] ? R_TQKV : b < p.end[R_ATTN] ? R_ATTN : b < p.end[R_TO] ? R_TO
                    : b < p.end[R_TGU] ? R_TGU : b < p.end[R_ZD] ? R_ZD : R_TD;
-  const int i = b - (role == 0 ? 0 : p.end[role - 1]);
-  // Which problem a z or tile workgroup serves, by the per-problem counts within its role.
-  auto zsplit = [&](int p0, int count, int &pi, int &zi) {
-    pi = p0;
-    zi = i;
-    for (int q = 0; q < count - 1; ++q) {
-      const int n = (p.prob[pi].rank + kFusedZRanks - 1) / kFusedZRanks;
-      if (zi < n) break;
-      zi -= n;
-      ++pi;
-    }
-  };
-  auto tsplit = [&](int p0, int count, int &pi, int &n0) {
+  const int i = b - (role == R_TQKV ? 0 : role == R_ATTN ? p.end[R_TQKV] : role == R_TO ? p.end[R_ATTN]
+                     : role == R_TGU ? p.end[R_TO] : role == R_ZD ? p.end[R_TGU] : p.end[R_ZD]);
+  // Tile workgroups of q|k|v and gate|up: the problem and first row from the per-problem counts.
+  auto tile_of = [&](int p0, int count, int &pi, int &n0) {
     pi = p0;
     int ti = i;
     for (int q = 0; q < count - 1; ++q) {
-      const int n = (p.prob[pi].N + 15) / 16;
+      const int n = (pick(p.N, pi) + 15) / 16;
       if (ti < n) break;
       ti -= n;
       ++pi;
     }
     n0 = ti * 16;
   };
-  int pi = 0, k = 0;
+  // Each role runs its own loop over the layers (one layer unless STACK), so the compiler keeps
+  // one role's values live at a time; every role body is specialised for its problems.
+  const int layers = STACK ? p.layers : 1;
+  auto each_layer = [&](auto &&body) {
+    for (int l = 0; l < layers; ++l) {
+      const LayerCtx c{kLayerHeaderWords + l * p.layer_words,
+                       l + 1 < layers ? kLayerHeaderWords + (l + 1) * p.layer_words : -1, l == 0};
+      if constexpr (STACK) body(c, table[l]);
+      else body(c, p.w);
+    }
+  };
+  int pi = 0, n0 = 0;
   switch (role) {
-    case R_ZD: zsplit(P_DOWN, 1, pi, k); layer_z_role<kFusedMaxK>(p, pi, k, passed, reinterpret_cast<f16 *>(smem), wsum, zsh); break;
-    case R_TQKV: tsplit(P_Q, 3, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
-    case R_TO: tsplit(P_O, 1, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
-    case R_TGU: tsplit(P_GATE, 2, pi, k); layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, pi, k, passed, smem); break;
-    case R_TD: tsplit(P_DOWN, 1, pi, k); layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED, false>(p, pi, k, passed, smem); break;
-    default: layer_attention_role(p, i, passed, smem); break;
+    case R_TQKV:
+      tile_of(P_Q, 3, pi, n0);
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, pi, n0, passed, smem);
+      });
+      break;
+    case R_ATTN:
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) { layer_attention_role(p, c, W, i, passed, smem); });
+      break;
+    case R_TO:
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, P_O, i * 16, passed, smem);
+      });
+      break;
+    case R_TGU:
+      tile_of(P_GATE, 2, pi, n0);
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, pi, n0, passed, smem);
+      });
+      break;
+    case R_ZD:
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
+        layer_z_role<kFusedMaxK>(p, c, W, P_DOWN, i, passed, reinterpret_cast<f16 *>(smem), wsum, zsh);
+      });
+      break;
+    default:
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
+        layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED, false>(p, c, W, P_DOWN, i * 16, passed, smem);
+      });
+      break;
   }
   // Every workgroup counts itself once, after all of its work (thread 0 of wave 0 runs every role
   // to its end).

@@ -16,7 +16,7 @@ import torch
 
 LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve().parent.parent / 'liblowbit_hip.so'))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM = 0x1, 0x2, 0x4, 0x20
@@ -24,7 +24,8 @@ FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
-DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_decode_layer')
+DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_decode_layer',
+                  'lb_decode_stack_prepare', 'lb_decode_stack')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
 def attention_workspace_bytes(heads, capacity):
@@ -96,9 +97,46 @@ class DecodeLayerArgs(ctypes.Structure):
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
 
 
+def layer_words(hidden, intermediate, kv_heads):
+    """LB_DECODE_LAYER_WORDS: words of one layer's region of a decode-layer workspace."""
+    return (84 + (hidden + 128 * kv_heads) // 2 + 3 * hidden // 2 + intermediate + 31) // 32 * 32
+
+
 def layer_workspace_bytes(hidden, intermediate, kv_heads):
     """LB_DECODE_LAYER_WORKSPACE_BYTES."""
-    return 8 * (92 + (hidden + 128 * kv_heads) // 2 + hidden + intermediate)
+    return 8 * (8 + layer_words(hidden, intermediate, kv_heads))
+
+
+STACK_MAX_LAYERS = 64
+
+
+def stack_workspace_bytes(hidden, intermediate, kv_heads, layers):
+    """LB_DECODE_STACK_WORKSPACE_BYTES."""
+    return 8 * (8 + layers * layer_words(hidden, intermediate, kv_heads))
+
+
+def stack_table_bytes(layers):
+    """LB_DECODE_STACK_TABLE_BYTES."""
+    return 256 * layers
+
+
+class DecodeStackLayer(ctypes.Structure):
+    """Mirror of lb_decode_stack_layer."""
+    _fields_ = [('norm1', ctypes.c_void_p), ('norm2', ctypes.c_void_p), ('proj', FusedProblem * 7),
+                ('keys', ctypes.c_void_p), ('values', ctypes.c_void_p)]
+
+
+class DecodeStackArgs(ctypes.Structure):
+    """Mirror of lb_decode_stack_args."""
+    _fields_ = [('struct_size', ctypes.c_uint32), ('format', ctypes.c_uint32),
+                ('group_size', ctypes.c_int64), ('hidden', ctypes.c_int64), ('intermediate', ctypes.c_int64),
+                ('layers', ctypes.c_int64), ('layer', ctypes.POINTER(DecodeStackLayer)),
+                ('h', ctypes.c_void_p), ('eps', ctypes.c_float), ('reserved', ctypes.c_uint32),
+                ('heads', ctypes.c_int64), ('kv_heads', ctypes.c_int64), ('capacity', ctypes.c_int64),
+                ('cos', ctypes.c_void_p), ('sin', ctypes.c_void_p), ('position', ctypes.c_void_p),
+                ('scale', ctypes.c_float), ('reserved2', ctypes.c_uint32),
+                ('table', ctypes.c_void_p), ('table_bytes', ctypes.c_size_t),
+                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_size_t)]
 
 
 _lib = None
@@ -138,6 +176,9 @@ def library():
         lib.lb_decode_attention.argtypes = [ctypes.POINTER(DecodeAttentionArgs), ctypes.c_void_p]
         lib.lb_decode_layer.restype = ctypes.c_int
         lib.lb_decode_layer.argtypes = [ctypes.POINTER(DecodeLayerArgs), ctypes.c_void_p]
+        for name in ('lb_decode_stack_prepare', 'lb_decode_stack'):
+            getattr(lib, name).restype = ctypes.c_int
+            getattr(lib, name).argtypes = [ctypes.POINTER(DecodeStackArgs), ctypes.c_void_p]
         lib.lb_argmax_next.restype = ctypes.c_int
         lib.lb_argmax_next.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -554,6 +595,25 @@ class PreparedArgmax:
             _check(status, 'lb_argmax_next')
 
 
+def _fill_projections(proj, projections, keep):
+    """The seven lb_fused_problem entries of a layer (U padded to a row stride of 8 where needed)."""
+    for i, pr in enumerate(projections):
+        q = proj[i]
+        q.N = pr['N']
+        q.codes, q.scales = _ptr(pr['codes']), _ptr(pr.get('scales'))
+        keep += [pr['codes'], pr.get('scales')]
+        down, up = pr.get('down'), pr.get('up')
+        if down is not None:
+            down = down.contiguous()
+            if up.stride(-1) != 1 or up.stride(0) % 8:
+                padded = torch.zeros((up.shape[0], (up.shape[1] + 7) // 8 * 8), dtype=up.dtype, device=up.device)
+                padded[:, :up.shape[1]] = up
+                up = padded
+            q.rank = down.shape[0]
+            q.down, q.up, q.up_ld = _ptr(down), _ptr(up), up.stride(0)
+            keep += [down, up]
+
+
 class PreparedLayer(_Prepared):
     """lb_decode_layer: one decoder layer for one token in one launch.
 
@@ -574,21 +634,7 @@ class PreparedLayer(_Prepared):
         a.group_size, a.hidden, a.intermediate = group_size, hidden, intermediate
         keep = [_row(h, 'h', hidden), _row(norm1, 'norm1', hidden), _row(norm2, 'norm2', hidden)]
         a.h, a.norm1, a.norm2, a.eps = _ptr(h), _ptr(norm1), _ptr(norm2), eps
-        for i, pr in enumerate(projections):
-            q = a.proj[i]
-            q.N = pr['N']
-            q.codes, q.scales = _ptr(pr['codes']), _ptr(pr.get('scales'))
-            keep += [pr['codes'], pr.get('scales')]
-            down, up = pr.get('down'), pr.get('up')
-            if down is not None:
-                down = down.contiguous()
-                if up.stride(-1) != 1 or up.stride(0) % 8:
-                    padded = torch.zeros((up.shape[0], (up.shape[1] + 7) // 8 * 8), dtype=up.dtype, device=up.device)
-                    padded[:, :up.shape[1]] = up
-                    up = padded
-                q.rank = down.shape[0]
-                q.down, q.up, q.up_ld = _ptr(down), _ptr(up), up.stride(0)
-                keep += [down, up]
+        _fill_projections(a.proj, projections, keep)
         for t, name, count in ((cos, 'cos', capacity * 64), (sin, 'sin', capacity * 64),
                                (keys, 'keys', kv_heads * capacity * 64), (values, 'values', kv_heads * capacity * 64)):
             keep.append(_row(t, name, count))
@@ -601,6 +647,58 @@ class PreparedLayer(_Prepared):
         a.workspace, a.workspace_bytes = _ptr(self.workspace), size
         keep.append(self.workspace)
         self._bind('lb_decode_layer', 'lb_decode_layer', a, h.device, keep)
+        self.out = h
+
+    def counters(self):
+        """(workgroups counted over all calls so far, timeout word) of the workspace."""
+        return [int(self.workspace[:8].view(torch.int64)), int(self.workspace[8:12].view(torch.int32))]
+
+
+class PreparedStack(_Prepared):
+    """lb_decode_stack: every layer of a decoder stack for one token in one launch.
+
+    layers: sequence of dicts with norm1, norm2, keys, values and projections (the seven dicts of
+    PreparedLayer); the other arguments as PreparedLayer.  The call owns a zeroed workspace and the
+    device layer table, written once here by lb_decode_stack_prepare.
+    """
+
+    def __init__(self, h, layers, *, format, group_size, hidden, intermediate, eps, heads, kv_heads, cos, sin,
+                 position, scale=0.125):
+        if not 1 <= len(layers) <= STACK_MAX_LAYERS:
+            raise ValueError(f'1..{STACK_MAX_LAYERS} layers per stack')
+        keys0 = layers[0]['keys']
+        capacity = keys0.shape[-2]
+        a = DecodeStackArgs()
+        a.struct_size = ctypes.sizeof(DecodeStackArgs)
+        a.format = FORMATS[format]
+        a.group_size, a.hidden, a.intermediate, a.layers = group_size, hidden, intermediate, len(layers)
+        keep = [_row(h, 'h', hidden)]
+        self._rows = (DecodeStackLayer * len(layers))()
+        for row, layer in zip(self._rows, layers):
+            if len(layer['projections']) != 7:
+                raise ValueError('seven projections per layer: q, k, v, o, gate, up, down')
+            keep += [_row(layer['norm1'], 'norm1', hidden), _row(layer['norm2'], 'norm2', hidden),
+                     _row(layer['keys'], 'keys', kv_heads * capacity * 64),
+                     _row(layer['values'], 'values', kv_heads * capacity * 64)]
+            row.norm1, row.norm2 = _ptr(layer['norm1']), _ptr(layer['norm2'])
+            row.keys, row.values = _ptr(layer['keys']), _ptr(layer['values'])
+            _fill_projections(row.proj, layer['projections'], keep)
+        a.layer = self._rows
+        a.h, a.eps = _ptr(h), eps
+        for t, name in ((cos, 'cos'), (sin, 'sin')):
+            keep.append(_row(t, name, capacity * 64))
+        keep.append(_row(position, 'position', 1, torch.int64))
+        a.heads, a.kv_heads, a.capacity = heads, kv_heads, capacity
+        a.cos, a.sin, a.position, a.scale = _ptr(cos), _ptr(sin), _ptr(position), scale
+        self.table = torch.zeros(stack_table_bytes(len(layers)), dtype=torch.uint8, device=h.device)
+        a.table, a.table_bytes = _ptr(self.table), self.table.numel()
+        size = stack_workspace_bytes(hidden, intermediate, kv_heads, len(layers))
+        self.workspace = torch.zeros(size, dtype=torch.uint8, device=h.device)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+        keep += [self.table, self.workspace]
+        self._bind('lb_decode_stack', 'lb_decode_stack', a, h.device, keep)
+        handle = torch.cuda.current_stream(h.device).cuda_stream
+        _check(library().lb_decode_stack_prepare(self._ref, ctypes.c_void_p(handle)), 'lb_decode_stack_prepare')
         self.out = h
 
     def counters(self):

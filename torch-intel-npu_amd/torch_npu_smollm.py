@@ -560,12 +560,15 @@ class GraphDecoder:
     embedding (lb_argmax_next).  Projections of different formats (fp16-protected ones)
     get separate launches.  layer=True (default) runs those five steps of a layer as one
     lb_decode_layer launch whenever its seven projections share one format and group (the
-    reference's one graph per layer); the fused launches remain for other layers.  fused=False runs the same step as staged PyTorch-ROCm glue
+    reference's one graph per layer); the fused launches remain for other layers.  stack=True
+    (default) goes further when every layer has the same format, group and ranks: one
+    lb_decode_stack launch runs all layers of the token (the reference's whole fenced chain of
+    layer graphs, :644-654).  fused=False runs the same step as staged PyTorch-ROCm glue
     around one lb_linear per projection.  shared_z (default) gives every fused launch with
     corrections its own workspace, so each correction's z is computed once per launch.
     """
 
-    def __init__(self, stack, io, *, fused=True, shared_z=True, layer=True):
+    def __init__(self, stack, io, *, fused=True, shared_z=True, layer=True, stack_kernel=True):
         self.device = io.embedding.device
         if self.device.type != 'cuda':
             raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
@@ -582,6 +585,7 @@ class GraphDecoder:
         self.values = [z(1, KV_HEADS, cap, HEAD_DIM) for _ in stack.layers]
         self.states = [layer._dev(dev) for layer in stack.layers]
         self.layer_kernel = fused and layer and all(self._layer_ready(st) for st in self.states)
+        self.stack_kernel = self.layer_kernel and stack_kernel and self._stack_ready(self.states)
         if self.layer_kernel:
             self._build_layer(z)
         elif fused:
@@ -684,22 +688,52 @@ class GraphDecoder:
         group = groups.pop()
         return (group == 0 and fmt == 'int8') or (group >= 32 and group & (group - 1) == 0)
 
+    @classmethod
+    def _layer_key(cls, state):
+        """(format, group, ranks) of a layer: the launch shape lb_decode_stack needs shared."""
+        entries = [state['lin'][name] for name in cls._ORDER]
+        fmt = entries[0]['format']
+        group = 0 if fmt == 'fp16' or entries[0]['group'] == entries[0]['K'] else entries[0]['group']
+        return fmt, group, tuple(e.get('rank', 0) for e in entries)
+
+    @classmethod
+    def _stack_ready(cls, states):
+        import lowbit_hip as lb
+        return (len(states) <= lb.STACK_MAX_LAYERS and len({cls._layer_key(st) for st in states}) == 1
+                and all(torch.equal(st['cos'], states[0]['cos']) and torch.equal(st['sin'], states[0]['sin'])
+                        for st in states))
+
+    @classmethod
+    def _projections(cls, state):
+        projections = []
+        for name in cls._ORDER:
+            e = state['lin'][name]
+            pr = dict(codes=e['codes'], scales=e['scales'], N=e['N'])
+            if e.get('rank', 0):
+                pr.update(down=e['down'], up=e['up'])
+            projections.append(pr)
+        return projections
+
     def _build_layer(self, z):
-        """Each layer as one lb_decode_layer launch, then the fused head and the argmax."""
+        """Every layer in one lb_decode_stack launch (or each layer as one lb_decode_layer launch),
+        then the fused head and the argmax."""
         import lowbit_hip as lb
         io = self.io
         self.h = z(HIDDEN)
         self.calls = []
+        if self.stack_kernel:
+            fmt, group, _ = self._layer_key(self.states[0])
+            layers = [dict(norm1=st['norm1'], norm2=st['norm2'], keys=k, values=v, projections=self._projections(st))
+                      for st, k, v in zip(self.states, self.keys, self.values)]
+            self.calls.append([lb.PreparedStack(self.h, layers, format=fmt, group_size=group, hidden=HIDDEN,
+                                                intermediate=1536, eps=1e-5, heads=HEADS, kv_heads=KV_HEADS,
+                                                cos=self.states[0]['cos'], sin=self.states[0]['sin'],
+                                                position=self.pos, scale=0.125)])
+            self._build_head(io)
+            return
         for state, keys, values in zip(self.states, self.keys, self.values):
-            entries = [state['lin'][name] for name in self._ORDER]
-            fmt = entries[0]['format']
-            group = 0 if fmt == 'fp16' or entries[0]['group'] == entries[0]['K'] else entries[0]['group']
-            projections = []
-            for e in entries:
-                pr = dict(codes=e['codes'], scales=e['scales'], N=e['N'])
-                if e.get('rank', 0):
-                    pr.update(down=e['down'], up=e['up'])
-                projections.append(pr)
+            fmt, group, _ = self._layer_key(state)
+            projections = self._projections(state)
             self.calls.append([lb.PreparedLayer(self.h, projections, format=fmt, group_size=group, hidden=HIDDEN,
                                                 intermediate=1536, norm1=state['norm1'], norm2=state['norm2'],
                                                 eps=1e-5, heads=HEADS, kv_heads=KV_HEADS, cos=state['cos'],

@@ -468,6 +468,10 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
       if (t + i * 256 < 16 * GMAX) ss[t + i * 256] = sreg[i];
     if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;
   }
+  // Residual words (o after the first layer: the layer input h; down: h1) are requested with the
+  // source row, once its sentinel is current: both are published before the words polled for.
+  const int res_base = pi == P_DOWN ? c.lw + p.w_h1 : (pi == P_O && !c.first) ? c.lw + p.w_h : -1;
+  uint64_t resw = 0;
   // The source row: the first layer's input (loaded above) or the words of an earlier role.
   const int src_base = source_base(p, c, rs.src);
   if (src_base >= 0) {
@@ -475,6 +479,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
 #pragma unroll
     for (int i = 0; i < XB; ++i) gamma_rows[i] = av[i];
     wait_sentinel(p, source_sentinel(p, src_base, rs.src), tag);
+    if (res_base >= 0 && wave == 0 && lane < rows) resw = sys_load(p.ws + res_base + (n0 + lane) / 2);
     layer_source_row(p, src_base, rs.src, K, tag, xv, av);
     if (rs.src != SRC_GU) {
 #pragma unroll
@@ -563,13 +568,13 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
       __builtin_amdgcn_wave_barrier();
     }
   }
-  // Residuals: o adds the layer input h (plain in the first layer, else the h words, final since
-  // the attention words this tile read depend on them); down adds h1 (final: the gate|up words
-  // this tile read depend on it).
+  // Residuals: o adds the layer input h (plain in the first layer, else the h words), down adds
+  // h1; the words requested above are final by now (what this tile read depends on them), so the
+  // bounded re-read is a formality.
   f16 residual = rres;
-  if (((pi == P_O && !c.first) || pi == P_DOWN) && lane < rows) {
-    const int rw = c.lw + (pi == P_O ? p.w_h : p.w_h1) + (n0 + lane) / 2;
-    residual = word_half(wait_word(p, p.ws + rw, tag), (n0 + lane) & 1);
+  if (res_base >= 0 && lane < rows) {
+    if (word_tag(resw) != tag) resw = wait_word(p, p.ws + res_base + (n0 + lane) / 2, tag);
+    residual = word_half(resw, (n0 + lane) & 1);
   }
   float sum = ((acc[0] + red[j]) + red[16 + j]) + red[32 + j];
   if (p.per_row) sum *= (float)rscale;

@@ -71,6 +71,16 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+// SiLU from the hardware exp2 and reciprocal (about 1 fp32 ulp each; the result is rounded to
+// fp16 right after, as in the reference staging).
+__device__ __forceinline__ float silu_fast(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
+
+// c + a.b over fp16 pairs and blocks on v_dot2c_f32_f16 (exact fp16 products, fp32 sums).
+__device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+__device__ __forceinline__ h2 pair_of(const h8 &v, int i) { return h2{v[2 * i], v[2 * i + 1]}; }
+
 // One rotate-half RoPE element with the reference's three fp16 roundings,
 // fp16(fp16(x * c) + fp16(r * s)).  Contraction stays off: once x * c is narrowed to an fp16
 // multiply (exact, as both factors are fp16) the compiler would otherwise fuse it with the add

@@ -258,7 +258,7 @@ __device__ __forceinline__ h8 layer_prologue_apply(int prologue, const h8 &x, co
     for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)((float)x[e] * inv) * (float)a[e]);
   } else if (prologue == PRO_SILU_MUL) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu((float)x[e]) * (float)a[e]);
+    for (int e = 0; e < 8; ++e) v[e] = (f16)((float)(f16)silu_fast((float)x[e]) * (float)a[e]);
   } else {
     v = x;
   }
@@ -350,11 +350,8 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
       asm volatile("" : "+v"(vz[i]));
       const h8 vv = __builtin_bit_cast(h8, vz[i]);
       const h8 xx = *reinterpret_cast<const h8 *>(xs + blk * 8);
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        acc += (float)xx[e] * (float)vv[e];
-        acc2 += (float)xx[e + 1] * (float)vv[e + 1];
-      }
+      acc = dot2(pair_of(xx, 0), pair_of(vv, 0), dot2(pair_of(xx, 2), pair_of(vv, 2), acc));
+      acc2 = dot2(pair_of(xx, 1), pair_of(vv, 1), dot2(pair_of(xx, 3), pair_of(vv, 3), acc2));
     }
   }
   static_assert(TPR == 32, "two ranks per wave");
@@ -371,6 +368,21 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
 }
 
 // ---------------------------------------------------------------- GEMV tiles
+// d = z.U[row] over the rank (zs and U both fp16, zero past the rank), 8 ranks per step on dot2.
+__device__ __forceinline__ float correction_dot_h(const f16 *zs, const f16 *urow, int rank) {
+  float d = 0.0f;
+#pragma unroll
+  for (int r8 = 0; r8 < kFusedMaxRank / 8; ++r8) {
+    if (8 * r8 < rank) {
+      const h8 u = *reinterpret_cast<const h8 *>(urow + 8 * r8);
+      const h8 z = *reinterpret_cast<const h8 *>(zs + 8 * r8);
+      d = dot2(pair_of(z, 3), pair_of(u, 3), dot2(pair_of(z, 2), pair_of(u, 2),
+              dot2(pair_of(z, 1), pair_of(u, 1), dot2(pair_of(z, 0), pair_of(u, 0), d))));
+    }
+  }
+  return d;
+}
+
 // Rows [n0, n0 + 16) of problem pi, with the fused decode kernel's product and epilogue.  Output:
 // q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
 // residual h1).
@@ -395,8 +407,8 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   f16 *xs = reinterpret_cast<f16 *>(smem);                                  // [XLD]
   f16 *ss = xs + XLD;                                                       // [16 GMAX + 8]
   f16 *us = ss + (SCALED ? 16 * GMAX + 8 : 8);                              // [16 * 32]
-  float *zs = reinterpret_cast<float *>(us + 16 * kFusedMaxRank);           // [32]
-  float *red = zs + kFusedMaxRank;                                          // [48]
+  f16 *zs = us + 16 * kFusedMaxRank;                                        // [32] (a 32-float slot)
+  float *red = reinterpret_cast<float *>(zs + 2 * kFusedMaxRank);           // [48]
   float *wsum = red + (KG - 1) * 16;                                        // [4]
   uint32_t *nf4_table = reinterpret_cast<uint32_t *>(wsum + 4);             // [256]
 
@@ -510,14 +522,11 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
       for (int i = 0; i < VB; ++i) {
         asm volatile("" : "+v"(vreg[i]));
         const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          za += (float)xx[i][e] * (float)vv[e];
-          zb += (float)xx[i][e + 1] * (float)vv[e + 1];
-        }
+        za = dot2(pair_of(xx[i], 0), pair_of(vv, 0), dot2(pair_of(xx[i], 2), pair_of(vv, 2), za));
+        zb = dot2(pair_of(xx[i], 1), pair_of(vv, 1), dot2(pair_of(xx[i], 3), pair_of(vv, 3), zb));
       }
       za = sum8(za + zb);
-      if (vpart == 0) zs[vr] = vr < rank ? (float)(f16)za : 0.0f;
+      if (vpart == 0) zs[vr] = vr < rank ? (f16)za : (f16)0.0f;
     }
   }
 
@@ -562,7 +571,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
         const uint64_t word = lane < words ? wait_word(p, zw + lane, tag) : 0;
 #pragma unroll
         for (int e = 0; e < 3; ++e)
-          if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = 3 * lane + e < rank ? (float)word_half(word, e) : 0.0f;
+          if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = 3 * lane + e < rank ? word_half(word, e) : (f16)0.0f;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -580,7 +589,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   if (p.per_row) sum *= (float)rscale;
   f16 hv = (f16)sum;
   if (RANKED && rank > 0) {
-    const float d = correction_dot(zs, us + j * kFusedMaxRank, rank);
+    const float d = correction_dot_h(zs, us + j * kFusedMaxRank, rank);
     hv = (f16)((float)hv + (float)(f16)d);
   }
   if (pi == P_O || pi == P_DOWN) hv = (f16)((float)residual + (float)hv);
@@ -715,11 +724,8 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
         asm volatile("" : "+v"(kreg[i][b]));
         const h8 qq = qreg[b];
         const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * b) : __builtin_bit_cast(h8, kreg[i][b]);
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          acc0 += (float)qq[e] * (float)kk[e];
-          acc1 += (float)qq[e + 1] * (float)kk[e + 1];
-        }
+        acc0 = dot2(pair_of(qq, 0), pair_of(kk, 0), dot2(pair_of(qq, 2), pair_of(kk, 2), acc0));
+        acc1 = dot2(pair_of(qq, 1), pair_of(kk, 1), dot2(pair_of(qq, 3), pair_of(kk, 3), acc1));
       }
       if (s <= pos) {
         const float v = (float)(f16)((float)(f16)(acc0 + acc1) * p.scale);

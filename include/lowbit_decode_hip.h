@@ -163,7 +163,7 @@ typedef struct lb_decode_layer_args {
 /* Words of one layer's region of a decode-layer workspace (tagged hand-over words of every stage),
  * and the workspace of one layer: an 8-word header (launch count, timeout word) and one region. */
 #define LB_DECODE_LAYER_WORDS(hidden, intermediate, kv_heads)                                              \
-  (((size_t)84u + ((size_t)(hidden) + 128u * (size_t)(kv_heads)) / 2u + 3u * (size_t)(hidden) / 2u + \
+  (((size_t)224u + ((size_t)(hidden) + 128u * (size_t)(kv_heads)) / 2u + 3u * (size_t)(hidden) / 2u + \
     (size_t)(intermediate) + 31u) / 32u * 32u)
 #define LB_DECODE_LAYER_WORKSPACE_BYTES(hidden, intermediate, kv_heads) \
   ((size_t)8u * (8u + LB_DECODE_LAYER_WORDS(hidden, intermediate, kv_heads)))

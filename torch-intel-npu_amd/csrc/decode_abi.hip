@@ -740,7 +740,7 @@ lb_status check_overlaps(const char *who, const Range *in, int nin, const Range 
 
 // The role grid (T_QKV, ATTN, T_O, T_GU, Z_D, T_D) and the launch's template choice.
 void finish_params(LayerParams *p, uint32_t format, int64_t group_size, int *fmt, bool *scaled, bool *ranked) {
-  auto zc = [&](int i) { return (p->rank[i] + kFusedZRanks - 1) / kFusedZRanks; };
+  auto zc = [&](int i) { return p->rank[i]; };  // one z workgroup per rank
   auto tc = [&](int i) { return (p->N[i] + 15) / 16; };
   const int counts[R_COUNT] = {tc(P_Q) + tc(P_K) + tc(P_V), p->heads * kAttnDimSlices, tc(P_O),
                                tc(P_GATE) + tc(P_UP), zc(P_DOWN), tc(P_DOWN)};

@@ -87,7 +87,7 @@ struct LayerCtx {
 };
 
 constexpr int kLayerSpinLimit = 1 << 18;
-constexpr int kLayerZWords = 12;  // z words per problem (6 ranks per z workgroup, three per word)
+constexpr int kLayerZWords = 32;  // z words per problem: one rank per z workgroup and word
 
 __device__ __forceinline__ uint64_t sys_load(const uint64_t *a) {
   return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -295,31 +295,24 @@ __device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const La
 }
 
 // ---------------------------------------------------------------- z workgroups
-// Ranks [6 zi, 6 zi + 6) of problem pi: z = fp16(x'.V^T), published as two tagged words.
+// Rank r of problem pi: z = fp16(x'.V[r]^T), published as one tagged word (z in bits 16..31).
+// Thread t holds block t of the source row and of V[r] (K <= 2048), so no staging is needed:
+// each thread adds its eight products, the waves reduce on DPP and thread 0 adds the four waves.
 template <int KMAX>
 __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W, int pi,
-                                             int zi, uint64_t passed, f16 *xs, float *wsum, f16 *zsh) {
-  constexpr int TPR = 32;
-  constexpr int ZI = (KMAX / 8 + TPR - 1) / TPR;
+                                             int r, uint64_t passed, float *wsum) {
   constexpr int XB = (KMAX / 8 + 255) / 256;
+  static_assert(XB == 1, "one source block per thread");
   constexpr int kOutOfRange = (int)0x80000000u;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const RoleShape rs = role_shape(p, W, pi);
   const int K = rs.K, blocks = K >> 3;
-  const int r0 = zi * kFusedZRanks;
-  const int rr = t / TPR, li = t % TPR;
   const int zrank = pick(p.rank, pi);
-  const bool live = rr < kFusedZRanks && r0 + rr < zrank;
   h8 xv[XB], av[XB];
   layer_plain_loads(p, c, rs, xv, av);
   const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(pick(W.down, pi), (size_t)zrank * K * 2);
-  u4 vz[ZI];
-#pragma unroll
-  for (int i = 0; i < ZI; ++i) {
-    const int blk = li + TPR * i;
-    const int off = live && blk < blocks ? ((r0 + rr) * K + blk * 8) * 2 : kOutOfRange;
-    vz[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
-  }
+  u4 vz = __builtin_bit_cast(
+      u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, r < zrank && t < blocks ? (r * K + t * 8) * 2 : kOutOfRange, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the previous layer's LDS reads are done before this layer writes
   const uint32_t tag = layer_tag(p, passed);
@@ -336,34 +329,22 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
     }
   }
   const float inv = layer_prologue_inv(rs.prologue, K, p.eps, xv, wsum);
-#pragma unroll
-  for (int i = 0; i < XB; ++i) {
-    const int blk = t + 256 * i;
-    if (blk < blocks) *reinterpret_cast<h8 *>(xs + blk * 8) = layer_prologue_apply(rs.prologue, xv[i], av[i], inv);
+  float acc = 0.0f;
+  if (t < blocks) {
+    const h8 xx = layer_prologue_apply(rs.prologue, xv[0], av[0], inv);
+    asm volatile("" : "+v"(vz));
+    const h8 vv = __builtin_bit_cast(h8, vz);
+    acc = dot2(pair_of(xx, 0), pair_of(vv, 0), dot2(pair_of(xx, 2), pair_of(vv, 2), 0.0f));
+    acc = dot2(pair_of(xx, 1), pair_of(vv, 1), dot2(pair_of(xx, 3), pair_of(vv, 3), acc));
   }
+  acc = wave_sum(acc);
+  if (rs.prologue == PRO_RMSNORM) __syncthreads();  // wsum held the norm's partial sums
+  if (lane == 0) wsum[wave] = acc;
   __syncthreads();
-  float acc = 0.0f, acc2 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < ZI; ++i) {
-    const int blk = li + TPR * i;
-    if (blk < blocks) {
-      asm volatile("" : "+v"(vz[i]));
-      const h8 vv = __builtin_bit_cast(h8, vz[i]);
-      const h8 xx = *reinterpret_cast<const h8 *>(xs + blk * 8);
-      acc = dot2(pair_of(xx, 0), pair_of(vv, 0), dot2(pair_of(xx, 2), pair_of(vv, 2), acc));
-      acc2 = dot2(pair_of(xx, 1), pair_of(vv, 1), dot2(pair_of(xx, 3), pair_of(vv, 3), acc2));
-    }
-  }
-  static_assert(TPR == 32, "two ranks per wave");
-  acc = sum16(acc + acc2);
-  acc = (t & 63) < 32 ? lane_value(acc, 0) + lane_value(acc, 16) : lane_value(acc, 32) + lane_value(acc, 48);
-  if (li == 0 && rr < kFusedZRanks) zsh[rr] = live ? (f16)acc : (f16)0.0f;
-  __syncthreads();
-  if (t < 2) {
-    const uint64_t word = (uint64_t)tag | ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t]) << 16) |
-                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 1]) << 32) |
-                          ((uint64_t)__builtin_bit_cast(uint16_t, zsh[3 * t + 2]) << 48);
-    sys_store(p.ws + c.lw + p.w_z + pi * kLayerZWords + 2 * zi + t, word);
+  if (t == 0) {
+    const f16 z = r < zrank ? (f16)(((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) : (f16)0.0f;
+    sys_store(p.ws + c.lw + p.w_z + pi * kLayerZWords + r,
+              (uint64_t)tag | ((uint64_t)__builtin_bit_cast(uint16_t, z) << 16));
   }
 }
 
@@ -565,14 +546,9 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   // ---- epilogue: wave 0; lane j < rows owns row n0 + j ----
   if constexpr (RANKED && !OWN_Z) {
     if (rank > 0) {
-      const int words = (rank + 2) / 3;
       const uint64_t *zw = p.ws + c.lw + p.w_z + pi * kLayerZWords;
-      if (lane < kFusedZWordsPerProblem) {  // every zs entry, zero from rank on
-        const uint64_t word = lane < words ? wait_word(p, zw + lane, tag) : 0;
-#pragma unroll
-        for (int e = 0; e < 3; ++e)
-          if (3 * lane + e < kFusedMaxRank) zs[3 * lane + e] = 3 * lane + e < rank ? word_half(word, e) : (f16)0.0f;
-      }
+      if (lane < kFusedMaxRank)  // every zs entry, zero from rank on
+        zs[lane] = lane < rank ? word_half(wait_word(p, zw + lane, tag), 0) : (f16)0.0f;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
     }
@@ -787,7 +763,6 @@ template <int FMT, bool SCALED, bool RANKED, bool STACK>
 __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p, const LayerWeights *__restrict__ table) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float wsum[4];
-  __shared__ f16 zsh[8];
   const int b = blockIdx.x;
   const uint64_t passed = sys_load(p.ws);  // waited for only where a role first needs the tag
   const int role = b < p.end[R_TQKV] ? R_TQKV : b < p.end[R_ATTN] ? R_ATTN : b < p.end[R_TO] ? R_TO
@@ -840,9 +815,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p, const 
       });
       break;
     case R_ZD:
-      each_layer([&](const LayerCtx &c, const LayerWeights &W) {
-        layer_z_role<kFusedMaxK>(p, c, W, P_DOWN, i, passed, reinterpret_cast<f16 *>(smem), wsum, zsh);
-      });
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) { layer_z_role<kFusedMaxK>(p, c, W, P_DOWN, i, passed, wsum); });
       break;
     default:
       each_layer([&](const LayerCtx &c, const LayerWeights &W) {

@@ -99,7 +99,7 @@ class DecodeLayerArgs(ctypes.Structure):
 
 def layer_words(hidden, intermediate, kv_heads):
     """LB_DECODE_LAYER_WORDS: words of one layer's region of a decode-layer workspace."""
-    return (84 + (hidden + 128 * kv_heads) // 2 + 3 * hidden // 2 + intermediate + 31) // 32 * 32
+    return (224 + (hidden + 128 * kv_heads) // 2 + 3 * hidden // 2 + intermediate + 31) // 32 * 32
 
 
 def layer_workspace_bytes(hidden, intermediate, kv_heads):

@@ -81,6 +81,18 @@ __device__ __forceinline__ float silu_fast(float v) {
 __device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 __device__ __forceinline__ h2 pair_of(const h8 &v, int i) { return h2{v[2 * i], v[2 * i + 1]}; }
 
+// Problem pi (0..2, wave-uniform) of a fused launch, selected field by field: a copy chosen by
+// index would be kept in scratch memory.
+__device__ __forceinline__ FusedProblem problem_of(const FusedParams &p, int pi) {
+  const FusedProblem &a = p.prob[0], &b = p.prob[1], &c = p.prob[2];
+  FusedProblem r;
+#define LB_PICK(f) r.f = pi == 0 ? a.f : (pi == 1 ? b.f : c.f)
+  LB_PICK(codes); LB_PICK(scales); LB_PICK(y); LB_PICK(bias); LB_PICK(residual); LB_PICK(down); LB_PICK(up);
+  LB_PICK(N); LB_PICK(rank); LB_PICK(up_ld); LB_PICK(tiles_end); LB_PICK(zend);
+#undef LB_PICK
+  return r;
+}
+
 // One rotate-half RoPE element with the reference's three fp16 roundings,
 // fp16(fp16(x * c) + fp16(r * s)).  Contraction stays off: once x * c is narrowed to an fp16
 // multiply (exact, as both factors are fp16) the compiler would otherwise fuse it with the add
@@ -186,10 +198,10 @@ __device__ __forceinline__ void fused_z_block(const FusedParams &p, f16 *xs, flo
   const int K = p.K, blocks = K >> 3;
   const int b = blockIdx.x;
   const int zp = b < p.prob[0].zend ? 0 : (b < p.prob[1].zend ? 1 : 2);
-  FusedProblem Z = p.prob[0];
+  const FusedProblem Z = problem_of(p, zp);
   int zfirst = 0;
-  if (zp == 1) { Z = p.prob[1]; zfirst = p.prob[0].zend; }
-  if (zp == 2) { Z = p.prob[2]; zfirst = p.prob[1].zend; }
+  if (zp == 1) zfirst = p.prob[0].zend;
+  if (zp == 2) zfirst = p.prob[1].zend;
   const int zi = b - zfirst;                          // z workgroup of the problem: words 2 zi, 2 zi + 1
   const int r0 = zi * kFusedZRanks;
   const int rr = t / TPR, li = t % TPR;
@@ -341,10 +353,10 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   // Problem and tile of this workgroup (wave-uniform selects; no dynamic kernarg indexing).
   const int bid = (int)blockIdx.x - (SHARED_Z ? p.zblocks : 0);
   const int pi = bid < p.prob[0].tiles_end ? 0 : (bid < p.prob[1].tiles_end ? 1 : 2);
-  FusedProblem P = p.prob[0];
+  const FusedProblem P = problem_of(p, pi);
   int first = 0;
-  if (pi == 1) { P = p.prob[1]; first = p.prob[0].tiles_end; }
-  if (pi == 2) { P = p.prob[2]; first = p.prob[1].tiles_end; }
+  if (pi == 1) first = p.prob[0].tiles_end;
+  if (pi == 2) first = p.prob[1].tiles_end;
   const int n0 = (bid - first) * 16;
   const int rows = min(16, P.N - n0);
   const int row_bytes = K * BITS / 8;

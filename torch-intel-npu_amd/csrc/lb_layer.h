@@ -310,7 +310,7 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
   const int zrank = pick(p.rank, pi);
   h8 xv[XB], av[XB];
   layer_plain_loads(p, c, rs, xv, av);
-  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(pick(W.down, pi), (size_t)zrank * K * 2);
+  const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(W.down[pi], (size_t)zrank * K * 2);
   u4 vz = __builtin_bit_cast(
       u4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, r < zrank && t < blocks ? (r * K + t * 8) * 2 : kOutOfRange, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
@@ -406,7 +406,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
 
   // Wave 0, lane r < rows: the row's per-row scale and (o, first layer) its residual h value.
   const f16 rscale = __builtin_bit_cast(
-      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pick(W.scales, pi), p.per_row && wave == 0 ? (size_t)N * 2 : 0),
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(W.scales[pi], p.per_row && wave == 0 ? (size_t)N * 2 : 0),
                                                 lane < rows ? (n0 + lane) * 2 : kOutOfRange, 0, 0));
   const f16 rres = __builtin_bit_cast(
       f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.h, pi == P_O && c.first && wave == 0 ? (size_t)N * 2 : 0),
@@ -416,7 +416,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
     const int ur = 4 * wave + (lane >> 2), uq = lane & 3;
     const int off = lane < 16 && ur < rows && uq * 8 < rank ? ((n0 + ur) * up_ld + uq * 8) * 2 : kOutOfRange;
     ureg = __builtin_bit_cast(
-        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(pick(W.up, pi), rank > 0 ? (size_t)N * up_ld * 2 : 0), off, 0, 0));
+        u4, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(W.up[pi], rank > 0 ? (size_t)N * up_ld * 2 : 0), off, 0, 0));
   }
   h8 xv[XB], av[XB];
   layer_plain_loads(p, c, rs, xv, av);
@@ -424,7 +424,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   const int vr = t >> 3, vpart = t & 7;
   u4 vreg[VB > 0 ? VB : 1];
   if constexpr (OWN_Z) {
-    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(pick(W.down, pi), rank > 0 ? (size_t)rank * K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t vbuf = buffer_rsrc(W.down[pi], rank > 0 ? (size_t)rank * K * 2 : 0);
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const int k = (vpart + 8 * i) * 8;
@@ -434,12 +434,12 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   }
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
-    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(pick(W.scales, pi) + (size_t)n0 * G, (size_t)rows * G * 2);
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(W.scales[pi] + (size_t)n0 * G, (size_t)rows * G * 2);
 #pragma unroll
     for (int i = 0; i < SC; ++i)
       sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
   }
-  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(pick(W.codes, pi) + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_rsrc(W.codes[pi] + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
   u4 w[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) {

@@ -31,6 +31,8 @@ def command(output=LIBRARY, defines=()):
             *(f'-D{d}' for d in defines),
             # Packed fp32 VALU forms are kept out of the generated code on purpose.
             '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+            # Leading scalar kernel arguments (up to 14 dwords) arrive preloaded in registers.
+            '-mllvm', '-amdgpu-kernarg-preload-count=14',
             '-Wall', '-Wno-unused-function', '-Wno-unused-variable',
             '-o', str(output), *map(str, SOURCES)]
 

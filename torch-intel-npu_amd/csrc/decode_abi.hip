@@ -155,7 +155,9 @@ template <int FMT, bool SCALED, int KMAX, int RG>
 bool launch_rows_k(const FusedParams &p, int tiles, hipStream_t s) {
   constexpr int WSTEP = (4 / RG) * 4 * FormatTraits<FMT>::CPL;
   if constexpr ((KMAX + WSTEP - 1) / WSTEP <= 32) {  // all of a lane's loads fit in registers
-    hipLaunchKernelGGL((rows_gemv_kernel<FMT, SCALED, KMAX, RG>), dim3((tiles + RG - 1) / RG), dim3(256), 0, s, p);
+    const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
+    hipLaunchKernelGGL((rows_gemv_kernel<FMT, SCALED, KMAX, RG>), dim3((tiles + RG - 1) / RG), dim3(256), 0, s,
+                       p.prob[0].codes, p.x, p.prob[0].scales, aux, p.prob[0].N, p.K, p.G, p.prologue, p.group_shift, p);
     return true;
   }
   return false;

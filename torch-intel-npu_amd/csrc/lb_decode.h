@@ -515,9 +515,16 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
 // head, the Llama-shaped projections).  A workgroup holds RG 16-row tiles; wave (rg, kg) computes
 // tile rg over the k-steps kg, kg + KG, ... with KG = 4 / RG, so the staged activation row serves
 // RG tiles, and with RG = 4 every wave covers all of K and no cross-wave reduction is needed.
-// As in fused_gemv_kernel, every global load is issued straight-line before the first wait.
+// As in fused_gemv_kernel, every global load is issued straight-line before the first wait.  The
+// operands of those first loads come as leading scalar arguments, which the build preloads into
+// registers at wave launch (-amdgpu-kernarg-preload-count): workgroups dispatched while earlier ones
+// flood the memory system with weight requests would otherwise wait microseconds for their
+// argument block before issuing a single load.  The epilogue operands (residual, bias, per-row
+// scale) are loaded after the weights and staged behind a second barrier.
 template <int FMT, bool SCALED, int KMAX, int RG>
-__global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
+__global__ __launch_bounds__(256) void rows_gemv_kernel(const uint8_t *pre_codes, const f16 *pre_x, const f16 *pre_scales,
+                                                        const f16 *pre_aux, int pre_N, int pre_K, int pre_G,
+                                                        int pre_prologue, int pre_shift, FusedParams p) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
   constexpr int KSTEP = 4 * CPL;
@@ -544,26 +551,20 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int rg = wave % RG, kg = wave / RG;
   const int j = lane & 15, g = lane >> 4;
-  const int K = p.K;
+  const int K = pre_K;
   const FusedProblem &P = p.prob[0];
   const int w0 = blockIdx.x * ROWS;               // first row of the workgroup
-  const int wrows = min(ROWS, P.N - w0);
+  const int wrows = min(ROWS, pre_N - w0);
   const int n0 = w0 + 16 * rg;                    // first row of this wave's tile
-  const int rows = min(16, P.N - n0);             // <= 0: the tile lies past N (no loads, no stores)
+  const int rows = min(16, pre_N - n0);           // <= 0: the tile lies past N (no loads, no stores)
   const int row_bytes = K * BITS / 8;
 
   // Epilogue operands: wave 0 fetches the residual, wave 1 the bias, wave 2 the per-row scale
   // of the workgroup's rows (lane r < ROWS reads row w0 + r).
-  const f16 *ep = wave == 0 ? P.residual : (wave == 1 ? P.bias : (wave == 2 ? P.scales : nullptr));
-  const bool ep_on = wave == 0 ? P.residual != nullptr : (wave == 1 ? P.bias != nullptr : (wave == 2 && p.per_row));
-  const f16 ev = __builtin_bit_cast(
-      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(ep, ep_on ? (size_t)P.N * 2 : 0),
-                                                lane < wrows ? (w0 + lane) * 2 : kOutOfRange, 0, 0));
   const int blocks = K >> 3;
   const size_t kb_bytes = (size_t)K * 2;
-  const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
-  const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(aux, p.prologue == PRO_NONE ? 0 : kb_bytes);
-  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(p.x, kb_bytes);
+  const __amdgpu_buffer_rsrc_t abuf = buffer_rsrc(pre_aux, pre_prologue == PRO_NONE ? 0 : kb_bytes);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_rsrc(pre_x, kb_bytes);
   h8 av[XB], xv[XB];
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
@@ -577,13 +578,13 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
   }
   f16 sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
-    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(P.scales + (size_t)w0 * p.G, (size_t)max(wrows, 0) * p.G * 2);
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_rsrc(pre_scales + (size_t)w0 * pre_G, (size_t)max(wrows, 0) * pre_G * 2);
 #pragma unroll
     for (int i = 0; i < SC; ++i)
       sreg[i] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(sbuf, (t + i * 256) * 2, 0, 0));
   }
   const __amdgpu_buffer_rsrc_t wbuf =
-      buffer_rsrc(P.codes + (size_t)max(n0, 0) * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
+      buffer_rsrc(pre_codes + (size_t)max(n0, 0) * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
   u4 w[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) {
@@ -591,10 +592,14 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
     const int off = k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange;
     w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, off, 0, 0));
   }
+  const f16 *ep = wave == 0 ? P.residual : (wave == 1 ? P.bias : (wave == 2 ? P.scales : nullptr));
+  const bool ep_on = wave == 0 ? P.residual != nullptr : (wave == 1 ? P.bias != nullptr : (wave == 2 && p.per_row));
+  const f16 ev = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(ep, ep_on ? (size_t)pre_N * 2 : 0),
+                                                lane < wrows ? (w0 + lane) * 2 : kOutOfRange, 0, 0));
   __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
 
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
-  if (wave < 3 && lane < ROWS) es[wave * ROWS + lane] = ev;
   const float inv = prologue_inv(p, xv, wsum, lane, wave);
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
@@ -619,7 +624,7 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
     asm volatile("" : "+v"(w[u]));  // decode here, not at the load
     h2 s2 = {(f16)1.0f, (f16)1.0f};
     if constexpr (SCALED) {
-      const f16 sc = ss[(rg * 16 + j) * p.G + ((kb + g * CPL) >> p.group_shift)];
+      const f16 sc = ss[(rg * 16 + j) * pre_G + ((kb + g * CPL) >> pre_shift)];
       s2 = h2{sc, sc};
     }
 #pragma unroll
@@ -630,6 +635,8 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(FusedParams p) {
     }
   }
   // Lane (j, g) holds D rows 4g..4g+3 of column j; all rows are equal, row 0 (g == 0) is used.
+  if (wave < 3 && lane < ROWS) es[wave * ROWS + lane] = ev;
+  __syncthreads();  // the epilogue operands, loaded after the weights
   float sum = acc[0];
   if constexpr (KG > 1) {
     if (kg > 0 && g == 0) red[(kg - 1) * ROWS + rg * 16 + j] = acc[0];

@@ -174,6 +174,21 @@ bool launch_rows(const FusedParams &p, int tiles, hipStream_t s) {
   return false;
 }
 
+// One tile per workgroup (the four waves split K): the single-tile kernel's arithmetic in the same
+// order, with its first loads' operands preloaded, for one problem without a correction.
+template <int FMT, bool SCALED>
+bool launch_rows1(const FusedParams &p, int tiles, hipStream_t s) {
+  constexpr int LIMIT = fused_kmax_limit(FMT);
+  if (p.K <= 640) return launch_rows_k<FMT, SCALED, 640, 1>(p, tiles, s);
+  if (p.K <= kFusedMaxK) return launch_rows_k<FMT, SCALED, kFusedMaxK, 1>(p, tiles, s);
+  if (p.K <= 4096) return launch_rows_k<FMT, SCALED, 4096, 1>(p, tiles, s);
+  if constexpr (LIMIT >= 8192) {
+    if (p.K <= 8192) return launch_rows_k<FMT, SCALED, 8192, 1>(p, tiles, s);
+  }
+  if constexpr (LIMIT >= 16384) return launch_rows_k<FMT, SCALED, 16384, 1>(p, tiles, s);
+  return false;
+}
+
 // stream_gemv_kernel takes one-row INT4 calls with rows longer than LB_STREAM_MIN_K or at least
 // LB_STREAM_MIN_BYTES of weights, and INT8 rows longer than the single-tile kernel holds (measured
 // on MI355X: otherwise the single-tile kernels, whose workgroups issue every load at once, finish
@@ -321,6 +336,7 @@ void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s)
   if (!ranked && p.prob[0].tiles_end == tiles) {
     if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;
     if (tiles / 2 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 2>(p, tiles, s)) return;
+    if (launch_rows1<FMT, SCALED>(p, tiles, s)) return;
   }
   ranked ? launch_fused_r<FMT, SCALED, true>(p, tiles, s) : launch_fused_r<FMT, SCALED, false>(p, tiles, s);
 }

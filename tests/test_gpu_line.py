@@ -1,0 +1,166 @@
+"""GPU parity of the lane-linear one-row GEMV (line_gemv_kernel) against the CPU oracle.
+
+One-row INT4 / INT8 calls without a correction or prologue whose rows hold at least one segment
+(64 lanes x one 16-byte load: 2048 INT4 / 1024 INT8 codes) run there without any flag.  A wave
+reads 8 rows of one segment, 1 KB of each row per load, and the lane's activations once; the sum
+is the exact x . (q s) product (magic-bias codes on v_dot2_f32_f16 with the bias removed per
+lane; group scales per lane, or per lane quad once two reduction levels have summed it; per-row
+scales on the row total).  The bars are those of every linear path: rel-L2 <= 1e-3 against the
+oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for
+identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover 1..8
+INT4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,
+groups of one lane pair, one quad and longer, per-row scales, bias and residual.
+"""
+import numpy as np
+import pytest
+import torch
+
+import lowbit_hip
+from conftest import announce
+from oracle import lowbit_oracle as o
+from test_gpu_linear import check, problem, run, to_dev
+
+pytestmark = pytest.mark.gpu
+
+# (fmt, N, K, group)
+LINE_SHAPES = [
+    ('int4', 4096, 4096, 128),     # two segments, quad scales
+    ('int4', 37, 2176, 128),       # one quad in the second segment, a partial row group and workgroup
+    ('int4', 1000, 14336, 128),    # seven segments: one row group per workgroup
+    ('int4', 520, 16384, 128),     # eight segments
+    ('int4', 2056, 4096, 64),      # groups of two lanes: per-lane scales
+    ('int4', 77, 3072, 64),        # half a second segment
+    ('int4', 1032, 8192, 1024),    # groups of 32 lanes, four segments
+    ('int4', 4104, 4096, 4096),    # one scale per row (row total)
+    ('int8', 4096, 4096, 4096),    # per-row int8
+    ('int8', 129, 1056, 1056),     # per-row, two live lanes in the second segment
+    ('int8', 1040, 14336, 14336),  # fourteen segments (896-thread workgroups)
+    ('int8', 528, 16384, 128),     # sixteen segments, quad scales
+    ('int8', 2048, 4096, 64),      # groups of one lane quad
+    ('int8', 2048, 1536, 32),      # groups of two lanes
+    ('int8', 3000, 1024, 1024),    # exactly one segment
+]
+
+
+@pytest.mark.parametrize('spec', LINE_SHAPES, ids=lambda s: '-'.join(map(str, s)))
+def test_line_matches_oracle(device, spec):
+    fmt, n, k, group = spec
+    announce('line', spec)
+    rng = np.random.default_rng(n + 7 * k + group)
+    p = problem(rng, fmt, 1, n, k, group)
+    check(p, run(p, device), f'line {spec}')
+
+
+@pytest.mark.parametrize('spec', [('int4', 4096, 4096, 128), ('int4', 77, 3072, 64), ('int8', 2048, 4096, 4096)],
+                         ids=lambda s: '-'.join(map(str, s)))
+def test_line_with_bias(device, spec):
+    fmt, n, k, group = spec
+    announce('line bias', spec)
+    rng = np.random.default_rng(3 * n + k)
+    p = problem(rng, fmt, 1, n, k, group, bias=True)
+    check(p, run(p, device), f'line bias {spec}')
+
+
+@pytest.mark.parametrize('fmt,group', [('int4', 128), ('int4', 64), ('int4', 4096), ('int8', 4096), ('int8', 64)])
+def test_line_identity_is_bit_exact(device, fmt, group):
+    """One-hot activations and power-of-two scales: y is the dequantized column, bit for bit, for
+    columns in every slot of a 16-byte load (even and odd INT4 nibbles) and in both segments."""
+    n, k = 1000, 4096
+    announce('line identity', fmt, group)
+    rng = np.random.default_rng(group + (fmt == 'int8'))
+    codes = rng.integers(0, 16, n * k).astype(np.uint8) if fmt == 'int4' else rng.integers(-128, 128, n * k)
+    data = o.pack(codes) if fmt == 'int4' else codes.astype(np.int8).tobytes()
+    g = k // group
+    scales = (2.0 ** rng.integers(-12, 3, n * g)).astype(np.float16)
+    w = o.dequantize(fmt, (n, k), group, data, scales.tobytes())
+    dev_codes = to_dev(np.frombuffer(data, np.uint8), device)
+    dev_scales = to_dev(scales, device)
+    for col in (0, 1, 2, 3, 4, 5, 6, 7, 15, 31, 32, 33, 127, 128, 2047, 2048, 2049, k // 2 + 77, k - 1):
+        x = np.zeros((1, k), np.float16)
+        x[0, col] = 1.0
+        y = lowbit_hip.linear(to_dev(x, device), dev_codes, dev_scales, format=fmt, N=n, K=k, group_size=group)
+        np.testing.assert_array_equal(y.cpu().numpy()[0].view(np.uint16), w[:, col].view(np.uint16),
+                                      err_msg=f'column {col}')
+
+
+def test_line_zero_input_gives_zero(device):
+    announce('line zero input')
+    rng = np.random.default_rng(5)
+    p = problem(rng, 'int4', 1, 8192, 4096, 128)
+    p['x'] = np.zeros_like(p['x'])
+    got = run(p, device)
+    assert (got == 0).all()
+
+
+@pytest.mark.parametrize('xscale', [1e-3, 30.0])
+@pytest.mark.parametrize('fmt,group', [('int4', 128), ('int8', 4096)])
+def test_line_activation_magnitudes(device, xscale, fmt, group):
+    """Small (fp16-subnormal after the 1/16 staging of odd INT4 codes) and large activations."""
+    announce('line xscale', xscale, fmt)
+    rng = np.random.default_rng(11)
+    p = problem(rng, fmt, 1, 8192, 4096, group, xscale=xscale)
+    check(p, run(p, device), f'line xscale {xscale} {fmt}')
+
+
+def test_line_agrees_with_tiled_gemv(device):
+    """The forced tiled GEMV (fp16(q s) weights) and the line kernel (exact q s) on one problem."""
+    announce('line vs gemv')
+    rng = np.random.default_rng(31)
+    p = problem(rng, 'int4', 1, 16384, 4096, 128)
+    a = run(p, device)
+    b = run(p, device, lowbit_hip.FLAG_FORCE_GEMV)
+    assert o.rel_l2(a, b) <= 1e-3
+
+
+@pytest.mark.parametrize('group', [1536, 32])
+def test_line_residual_through_fused_linear(device, group):
+    """One INT8 problem without prologue or correction in lb_fused_linear (K = 1536, one and a half
+    segments): y = fp16(residual + fp16(x W^T)), with y and residual the same buffer."""
+    n, k = 3000, 1536
+    announce('line residual', group)
+    rng = np.random.default_rng(21 + group)
+    data = rng.integers(-127, 128, n * k).astype(np.int8).tobytes()
+    g = k // group
+    scales = (rng.uniform(0.5, 1.5, n * g) * (0.02 / 127)).astype(np.float16)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    residual = (rng.standard_normal(n) * 0.5).astype(np.float16)
+    y = to_dev(residual, device)
+    lowbit_hip.fused_linear(to_dev(x[0], device), [dict(codes=to_dev(np.frombuffer(data, np.uint8), device),
+                                                        scales=to_dev(scales, device), N=n, y=y, residual=y)],
+                            format='int8', K=k, group_size=group)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    plain = o.linear(x, 'int8', (n, k), group, data, scales.tobytes())[0]
+    want = (residual.astype(np.float32) + plain.astype(np.float32)).astype(np.float16)
+    assert o.rel_l2(got, want) <= 1e-3
+    budget = o.rounding_budget(x, 'int8', (n, k), group, data, scales.tobytes())[0]
+    ulp = (np.abs(want.astype(np.float64)) + np.abs(plain.astype(np.float64))) * 2.0 ** -10 + 2.0 ** -24
+    assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= budget + ulp).all()
+
+
+def test_line_repeated_calls_are_deterministic(device):
+    """Segment sums meet in a fixed order: the same call twice gives the same bits."""
+    announce('line determinism')
+    rng = np.random.default_rng(41)
+    p = problem(rng, 'int4', 1, 4096, 14336, 128)
+    a = run(p, device)
+    b = run(p, device)
+    np.testing.assert_array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+@pytest.mark.parametrize('spec', [('int4', 1000, 4096, 128), ('int4', 77, 3072, 64), ('int8', 129, 1056, 1056)],
+                         ids=lambda s: '-'.join(map(str, s)))
+def test_line_row_reversal_is_bit_exact(device, spec):
+    """Each row's sum has one association whatever its position in a wave's row group: the weight
+    rows reversed give the outputs reversed, bit for bit."""
+    fmt, n, k, group = spec
+    announce('line row reversal', spec)
+    rng = np.random.default_rng(53 + n)
+    p = problem(rng, fmt, 1, n, k, group)
+    row_bytes = k // 2 if fmt == 'int4' else k
+    rev = dict(p)
+    rev['data'] = np.frombuffer(p['data'], np.uint8).reshape(n, row_bytes)[::-1].tobytes()
+    rev['scales'] = np.frombuffer(p['scales'], np.float16).reshape(n, k // group)[::-1].tobytes()
+    a = run(p, device)
+    b = run(rev, device)
+    np.testing.assert_array_equal(b[0][::-1].view(np.uint16), a[0].view(np.uint16))

@@ -191,7 +191,7 @@ SHAPES = [
     ('int8', 256, 576, 576, 576),
     ('int8', 33, 1536, 576, 32),      # grouped int8
     ('int4', 130, 129, 96, 32),
-    ('int4', 1, 130, 16384, 128),     # one row, long K (single-tile kernel, 16384-row staging)
+    ('int4', 1, 130, 16384, 128),     # one row, long K (lane-linear kernel: eight segments)
     ('int8', 1, 300, 8192, 8192),     # one row, long K, per-row W8
     ('nf4', 1, 64, 5000 // 32 * 32, 64),
     ('int4', 1, 100, 4096, 32),       # one row, long K, group 32: falls back to the split GEMV
@@ -203,11 +203,12 @@ SHAPES = [
     ('int8', 3, 1100, 2048, 64),      # grouped int8
     ('int4', 8, 40000, 1024, 128),    # enough 64-row tiles to fill the chip: no K split
     ('nf4', 16, 33000, 2048, 64),     # no K split, K walked in LDS chunks
-    # one row over many rows: several 16-row tiles per workgroup (rows_gemv_kernel)
+    # one row over many rows: several 16-row tiles per workgroup (rows_gemv_kernel) ...
     ('int4', 1, 49152, 576, 64),      # config-2 lm_head: 4 tiles per workgroup
-    ('int8', 1, 33000, 1024, 1024),   # per-row W8, partial last workgroup (a wave past N)
     ('nf4', 1, 20000, 4096, 128),     # 2 tiles per workgroup, waves split K in two
-    ('int4', 1, 32768, 2048, 128),    # 32 loads per lane
+    # ... or, with rows of a whole segment, the lane-linear kernel
+    ('int8', 1, 33000, 1024, 1024),   # per-row W8, one segment, row groups past N
+    ('int4', 1, 32768, 2048, 128),    # one segment, quad scales
 ]
 
 

@@ -1,7 +1,8 @@
 """GPU parity of the streaming one-row GEMV (stream_gemv_kernel) against the CPU oracle.
 
-One-row lb_linear calls with rows longer than 4096 codes or at least 64 MB of INT4 / INT8
-weights run there; the tests force it (LB_FLAG_FORCE_STREAM) on smaller shapes.  It sums
+One-row lb_linear calls over at least 64 MB of INT4 weights whose rows are shorter than a segment
+of the lane-linear kernel (2048 codes) run there; the tests force it (LB_FLAG_FORCE_STREAM) on
+other shapes.  It sums
 x . (q + magic bias) on MFMA and applies the group scale per 32- or 16-code block, so its
 value is the exact x . (q s) product; the bars are those of every linear path: rel-L2 <= 1e-3
 against the oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106),
@@ -147,14 +148,14 @@ def test_stream_agrees_with_tiled_gemv(device):
 
 @pytest.mark.parametrize('spec', [('int8', 1040, 14336, 14336), ('int8', 528, 16384, 128), ('int4', 1024, 8192, 64)],
                          ids=lambda s: '-'.join(map(str, s)))
-def test_long_rows_take_stream_unforced(device, spec):
-    """One-row calls past the single-tile kernels' K limit (int8 K > 8192) or with K > 4096 run on
-    the stream kernel without any flag; same bars."""
+def test_stream_long_rows(device, spec):
+    """Rows past the single-tile kernels' K limit (int8 K > 8192) or longer than 4096 codes, forced
+    onto the stream kernel (unforced they take the lane-linear kernel); same bars."""
     fmt, n, k, group = spec
     announce('stream long rows', spec)
     rng = np.random.default_rng(n + k)
     p = problem(rng, fmt, 1, n, k, group)
-    check(p, run(p, device), f'long rows {spec}')
+    check(p, run(p, device, STREAM), f'long rows {spec}')
 
 
 # Several activation rows (2 <= M <= 16, K <= 4096): each MFMA A row spans more code blocks as M

@@ -12,6 +12,7 @@
 #include "abi_util.h"
 #include "lb_decode.h"
 #include "lb_layer.h"
+#include "lb_line.h"
 #include "lb_stream.h"
 
 using namespace lb;
@@ -327,11 +328,59 @@ bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
   }
 }
 
+#ifndef LB_LINE_WAVES
+#define LB_LINE_WAVES 4  // waves per line_gemv_kernel workgroup: whole row groups of every segment
+#endif
+#ifndef LB_LINE_ROWS
+#define LB_LINE_ROWS 8  // rows per line_gemv_kernel wave
+#endif
+
+// One problem, one activation row, no prologue or correction, INT4 / INT8 codes whose 16-byte lane
+// loads each lie in one group (one group per row, or power-of-two groups of at least CPL codes),
+// rows of at least one segment (64 lanes x CPL codes) and at most 16: launched in line_gemv_kernel,
+// which measured faster than the single-tile, multi-tile and streaming kernels on every such
+// shape (MI355X, one-row INT4 g128 and INT8 per-row GEMVs of 1024-128256 rows, K = 2048-14336).
+template <int FMT, bool SCALED>
+bool try_line(const FusedParams &p, hipStream_t s) {
+  if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
+    return false;
+  } else {
+    constexpr int CPL = LineTraits<FMT>::CPL, SEG = 64 * CPL, R = LB_LINE_ROWS;
+    const FusedProblem &q = p.prob[0];
+    if (p.force_stream || p.prologue != PRO_NONE || q.rank > 0 || p.G <= 0 || p.K % p.G != 0) return false;
+    const int group = p.K / p.G;
+    if (p.K < SEG || p.K > kLineMaxWaves * SEG || stream_group_span(FMT, p.K, group) == 0 ||
+        (group != p.K && group < CPL) || !aligned(q.codes, 16) || !aligned(p.x, 16))
+      return false;
+    const int nseg = (p.K + SEG - 1) / SEG;
+    const int groups = std::max(1, std::min(LB_LINE_WAVES, kLineMaxWaves) / nseg);  // row groups per workgroup
+    const int rows_wg = groups * R;
+    StreamParams sp{};
+    sp.y = q.y;
+    sp.bias = q.bias;
+    sp.residual = q.residual;
+    sp.M = 1;
+    sp.N = q.N;
+    sp.K = p.K;
+    sp.G = p.G;
+    sp.group_shift = p.group_shift;
+    const dim3 grid((q.N + rows_wg - 1) / rows_wg), block(64 * nseg * groups);
+    if (SCALED && group >= 4 * CPL)
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, R, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
+                         p.group_shift, nseg, groups, sp);
+    else
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, R, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
+                         p.group_shift, nseg, groups, sp);
+    return true;
+  }
+}
+
 // RANKED instantiations carry the correction (V and U loads); the others have none at all.  One
 // problem without a correction over many rows runs with several tiles per workgroup, or, when it
 // is long enough, in stream_gemv_kernel.
 template <int FMT, bool SCALED>
 void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
+  if (!ranked && p.prob[0].tiles_end == tiles && try_line<FMT, SCALED>(p, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles && try_stream<FMT, SCALED>(p, tiles, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles) {
     if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;

@@ -21,7 +21,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 32] [--quick] [--no-cp
        python bench.py --profile-kernel   (dominant kernel + a copy kernel, for rocprofv3 --pmc)
        python bench.py --decode-only      (config-4 decode leg alone, for rocprofv3 --kernel-trace)
        python bench.py --profile-gemm     (prefill GEMMs + hipBLASLt fp16 of the same shapes, for --pmc)
-       python bench.py --profile-stream   (config-5 128256x4096 INT4 GEMV at M=1 + a copy, for rocprofv3)
+       python bench.py --profile-llama 14336x4096  (one config-5 INT4 GEMV at M=1 + a copy, for rocprofv3)
        python bench.py --profile-multirow (multi-row GEMVs and a split-K GEMM, for rocprofv3 --kernel-trace)
 """
 import argparse
@@ -461,8 +461,8 @@ def main():
     ap.add_argument('--profile-gemm', action='store_true', help='prefill GEMMs alone (for rocprofv3 --pmc)')
     ap.add_argument('--profile-multirow', action='store_true',
                     help='multi-row GEMV paths and a split-K prefill GEMM alone (for rocprofv3 --kernel-trace)')
-    ap.add_argument('--profile-stream', action='store_true',
-                    help='the config-5 128256x4096 INT4 GEMV (M=1, stream kernel) alone, for rocprofv3')
+    ap.add_argument('--profile-llama', choices=[s[0] for s in LLAMA_SHAPES],
+                    help='one config-5 INT4 g128 GEMV at M=1 (its default kernel) alone, then a copy, for rocprofv3')
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -483,8 +483,8 @@ def main():
     if args.profile_gemm:
         profile_gemm(device, stream)
         return
-    if args.profile_stream:
-        profile_kernel(device, stream, LLAMA_SHAPES[-1])
+    if args.profile_llama:
+        profile_kernel(device, stream, next(s for s in LLAMA_SHAPES if s[0] == args.profile_llama))
         return
     if args.profile_multirow:
         profile_multirow(device, stream)

@@ -64,8 +64,8 @@ typedef enum lb_format {
 #define LB_FLAG_FORCE_GEMV    0x1u /* decode-regime kernel regardless of M (M <= 32) */
 #define LB_FLAG_FORCE_GEMM    0x2u /* prefill-regime MFMA GEMM regardless of M */
 #define LB_FLAG_FORCE_GENERIC 0x4u /* shape-agnostic fallback kernel (any N, K, group) */
-/* Streaming GEMVs (the kernels one-row calls over long rows or >= 64 MB of INT4 weights, and
- * 2..32-row calls over >= 64 MB, take by themselves) regardless of size: INT4/INT8 codes, no
+/* Streaming GEMVs (the kernels one-row calls over >= 64 MB of INT4 weights with rows shorter than
+ * 2048 codes, and 2..32-row calls over >= 64 MB, take by themselves) regardless of size: INT4/INT8 codes, no
  * correction or variant, 16-byte aligned codes and x rows, K a multiple of 32 (INT4) or 16 (INT8),
  * groups of one per row or a power of two, each 128-code (INT4) / 64-code (INT8) piece of a row
  * spanning 1, 2 or 4 whole groups; M == 1 or 17 <= M <= 32 with K <= 16384, or 2 <= M <= 16 with

@@ -548,9 +548,9 @@ def main():
             'hbm_frac_of_pass': round(head['gbs'] / HBM_PEAK_GBS, 4),
         },
         'roofline': {
-            'kernel': 'rows_gemv_kernel<INT4, KMAX 640, 4 tiles per workgroup> (one-row lb_linear) '
-                      'lm_head 49152x576 g64, M=1',
-            'profile': 'profiles/rows_gemv_int4_lm_head_49152x576_m1.md',
+            'kernel': 'pack_gemv_kernel<INT4, scaled, 4 loads per wave> (one-row lb_linear, 3 rows per '
+                      'wave-wide load) lm_head 49152x576 g64, M=1',
+            'profile': 'profiles/pack_gemv_int4_lm_head_49152x576_m1.md',
             'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
             'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': traffic_per_launch(),
             'algorithmic_bytes_per_launch': lm.bytes, 'avg_launch_us': dominant['us'],

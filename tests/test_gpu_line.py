@@ -1,4 +1,5 @@
-"""GPU parity of the lane-linear one-row GEMV (line_gemv_kernel) against the CPU oracle.
+"""GPU parity of the lane-linear one-row GEMVs (line_gemv_kernel, pack_gemv_kernel) against the CPU
+oracle.
 
 One-row INT4 / INT8 calls without a correction or prologue whose rows hold at least one segment
 (64 lanes x one 16-byte load: 2048 INT4 / 1024 INT8 codes) run there without any flag.  A wave
@@ -9,7 +10,9 @@ scales on the row total).  The bars are those of every linear path: rel-L2 <= 1e
 oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for
 identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover 1..8
 INT4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,
-groups of one lane pair, one quad and longer, per-row scales, bias and residual.
+groups of one lane pair, one quad and longer, per-row scales, bias and residual.  Rows shorter
+than a segment over at least 16384 rows (the SmolLM tied head) take pack_gemv_kernel, which packs
+whole rows across a wave's lanes; its cases follow the same bars.
 """
 import numpy as np
 import pytest
@@ -164,3 +167,93 @@ def test_line_row_reversal_is_bit_exact(device, spec):
     a = run(p, device)
     b = run(rev, device)
     np.testing.assert_array_equal(b[0][::-1].view(np.uint16), a[0].view(np.uint16))
+
+
+# Rows shorter than a segment over at least 16384 rows: pack_gemv_kernel packs whole rows across a
+# wave's lanes (P = 64 // S rows of S 16-byte slots per wave-wide load).  (fmt, N, K, group)
+PACK_SHAPES = [
+    ('int4', 49152, 576, 64),      # the SmolLM tied head: 3 rows in 54 lanes
+    ('int4', 16400, 576, 576),     # one scale per row, a partial last workgroup
+    ('int4', 20000, 1536, 128),    # one row per load (48 lanes)
+    ('int4', 16416, 256, 32),      # eight rows per load, groups of one lane
+    ('int4', 16390, 992, 32),      # two rows per load (62 lanes), ragged N
+    ('int8', 20000, 576, 576),     # per-row int8, one row per load (36 lanes)
+    ('int8', 16400, 992, 32),      # int8 groups of two lanes, 62 lanes
+]
+
+
+@pytest.mark.parametrize('spec', PACK_SHAPES, ids=lambda s: '-'.join(map(str, s)))
+def test_pack_matches_oracle(device, spec):
+    fmt, n, k, group = spec
+    announce('pack', spec)
+    rng = np.random.default_rng(n + 3 * k + group)
+    p = problem(rng, fmt, 1, n, k, group)
+    check(p, run(p, device), f'pack {spec}')
+
+
+def test_pack_with_bias(device):
+    announce('pack bias')
+    rng = np.random.default_rng(17)
+    p = problem(rng, 'int4', 1, 16400, 576, 64, bias=True)
+    check(p, run(p, device), 'pack bias')
+
+
+@pytest.mark.parametrize('fmt,group', [('int4', 64), ('int8', 576)])
+def test_pack_identity_is_bit_exact(device, fmt, group):
+    n, k = 16384, 576
+    announce('pack identity', fmt, group)
+    rng = np.random.default_rng(group + 5)
+    codes = rng.integers(0, 16, n * k).astype(np.uint8) if fmt == 'int4' else rng.integers(-128, 128, n * k)
+    data = o.pack(codes) if fmt == 'int4' else codes.astype(np.int8).tobytes()
+    g = k // group
+    scales = (2.0 ** rng.integers(-12, 3, n * g)).astype(np.float16)
+    w = o.dequantize(fmt, (n, k), group, data, scales.tobytes())
+    dev_codes = to_dev(np.frombuffer(data, np.uint8), device)
+    dev_scales = to_dev(scales, device)
+    for col in (0, 1, 7, 31, 32, 33, 287, 288, 289, k - 1):
+        x = np.zeros((1, k), np.float16)
+        x[0, col] = 1.0
+        y = lowbit_hip.linear(to_dev(x, device), dev_codes, dev_scales, format=fmt, N=n, K=k, group_size=group)
+        np.testing.assert_array_equal(y.cpu().numpy()[0].view(np.uint16), w[:, col].view(np.uint16),
+                                      err_msg=f'column {col}')
+
+
+@pytest.mark.parametrize('spec', [('int4', 16390, 576, 64), ('int4', 16390, 992, 32)], ids=lambda s: '-'.join(map(str, s)))
+def test_pack_row_reversal_is_bit_exact(device, spec):
+    """A row's sum is its slots' partials in slot order, whatever lanes the row falls to."""
+    fmt, n, k, group = spec
+    announce('pack row reversal', spec)
+    rng = np.random.default_rng(59 + k)
+    p = problem(rng, fmt, 1, n, k, group)
+    row_bytes = k // 2
+    rev = dict(p)
+    rev['data'] = np.frombuffer(p['data'], np.uint8).reshape(n, row_bytes)[::-1].tobytes()
+    rev['scales'] = np.frombuffer(p['scales'], np.float16).reshape(n, k // group)[::-1].tobytes()
+    a = run(p, device)
+    b = run(rev, device)
+    np.testing.assert_array_equal(b[0][::-1].view(np.uint16), a[0].view(np.uint16))
+
+
+def test_pack_residual_through_fused_linear(device):
+    """One INT4 problem without prologue or correction in lb_fused_linear over 20000 rows of 576:
+    y = fp16(residual + fp16(x W^T)), y and residual the same buffer."""
+    n, k, group = 20000, 576, 64
+    announce('pack residual')
+    rng = np.random.default_rng(23)
+    data = rng.integers(0, 256, n * k // 2).astype(np.uint8).tobytes()
+    g = k // group
+    scales = (rng.uniform(0.5, 1.5, n * g) * (0.02 / 7)).astype(np.float16)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    residual = (rng.standard_normal(n) * 0.5).astype(np.float16)
+    y = to_dev(residual, device)
+    lowbit_hip.fused_linear(to_dev(x[0], device), [dict(codes=to_dev(np.frombuffer(data, np.uint8), device),
+                                                        scales=to_dev(scales, device), N=n, y=y, residual=y)],
+                            format='int4', K=k, group_size=group)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    plain = o.linear(x, 'int4', (n, k), group, data, scales.tobytes())[0]
+    want = (residual.astype(np.float32) + plain.astype(np.float32)).astype(np.float16)
+    assert o.rel_l2(got, want) <= 1e-3
+    budget = o.rounding_budget(x, 'int4', (n, k), group, data, scales.tobytes())[0]
+    ulp = (np.abs(want.astype(np.float64)) + np.abs(plain.astype(np.float64))) * 2.0 ** -10 + 2.0 ** -24
+    assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= budget + ulp).all()

@@ -375,12 +375,54 @@ bool try_line(const FusedParams &p, hipStream_t s) {
   }
 }
 
+#ifndef LB_PACK_MIN_ROWS
+#define LB_PACK_MIN_ROWS 16384  // rows from which one-row calls of short rows take pack_gemv_kernel
+#endif
+#ifndef LB_PACK_ROWS
+#define LB_PACK_ROWS 4  // wave-wide loads per pack_gemv_kernel wave
+#endif
+
+// One problem, one activation row, no prologue or correction, INT4 / INT8 rows of 8 .. 63 16-byte
+// slots (shorter than a line_gemv_kernel segment) whose lane loads each lie in one group: launched
+// in pack_gemv_kernel (false otherwise).
+template <int FMT, bool SCALED>
+bool try_pack(const FusedParams &p, hipStream_t s) {
+  if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
+    return false;
+  } else {
+    constexpr int CPL = LineTraits<FMT>::CPL, R = LB_PACK_ROWS, WAVES = 4;
+    const FusedProblem &q = p.prob[0];
+    if (p.force_stream || p.prologue != PRO_NONE || q.rank > 0 || p.G <= 0 || p.K % p.G != 0 || q.N < LB_PACK_MIN_ROWS)
+      return false;
+    const int group = p.K / p.G;
+    const int row_bytes = p.K * LineTraits<FMT>::BITS / 8;
+    const int slots = row_bytes / 16, per_load = slots > 0 ? 64 / slots : 0;
+    if (row_bytes % 16 != 0 || slots < 8 || slots >= 64 || per_load * R > 64 || stream_group_span(FMT, p.K, group) == 0 ||
+        (group != p.K && group < CPL) || !aligned(q.codes, 16) || !aligned(p.x, 16))
+      return false;
+    StreamParams sp{};
+    sp.y = q.y;
+    sp.bias = q.bias;
+    sp.residual = q.residual;
+    sp.M = 1;
+    sp.N = q.N;
+    sp.K = p.K;
+    sp.G = p.G;
+    sp.group_shift = p.group_shift;
+    const int rows_wg = WAVES * R * per_load;
+    hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R>), dim3((q.N + rows_wg - 1) / rows_wg), dim3(64 * WAVES), 0, s,
+                       p.x, q.codes, q.scales, q.N, p.K, p.G, p.group_shift, sp);
+    return true;
+  }
+}
+
 // RANKED instantiations carry the correction (V and U loads); the others have none at all.  One
 // problem without a correction over many rows runs with several tiles per workgroup, or, when it
 // is long enough, in stream_gemv_kernel.
 template <int FMT, bool SCALED>
 void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
   if (!ranked && p.prob[0].tiles_end == tiles && try_line<FMT, SCALED>(p, s)) return;
+  if (!ranked && p.prob[0].tiles_end == tiles && try_pack<FMT, SCALED>(p, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles && try_stream<FMT, SCALED>(p, tiles, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles) {
     if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;

@@ -228,4 +228,97 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
   }
 }
 
+// One-row GEMV for rows of at most 64 16-byte slots (up to 2048 INT4 / 1024 INT8 codes, the
+// SmolLM shapes): the same lane-linear loads with whole rows packed across a wave's lanes.  A row
+// of S slots takes S lanes, so P = 64 / S consecutive rows fill P S lanes of a wave-wide load
+// (P S x 16 contiguous bytes; the SmolLM K = 576 INT4 rows: 3 rows in 54 lanes).  Lane l always
+// holds slot l % S of its row, so its activations are loaded once and serve all R loads (R P rows
+// per wave).  Each lane's partial per load is scaled by its group's scale (groups of at least CPL
+// codes) and goes to the wave's own LDS rows; lane q of the wave then adds the S partials of row q
+// in slot order.  Waves are independent: no barrier.
+template <int FMT, bool SCALED, int R>
+__global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const uint8_t *pre_codes,
+                                                        const f16 *pre_scales, int pre_N, int pre_K, int pre_G,
+                                                        int pre_shift, StreamParams p) {
+  using TR = LineTraits<FMT>;
+  constexpr int CPL = TR::CPL, XL = TR::XL;
+  constexpr int kOutOfRange = (int)0x80000000u;
+  constexpr int WAVES = 4;
+  __shared__ float part[WAVES][R][64];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int N = pre_N, K = pre_K;
+  const int row_bytes = K * TR::BITS / 8;
+  const int S = row_bytes >> 4;        // 16-byte slots per row (1 .. 64)
+  const int P = 64 / S;                // rows per wave-wide load
+  const int slot = lane % S, ro = lane / S;
+  const bool live = ro < P;
+  const int n0 = (blockIdx.x * WAVES + wave) * R * P;  // first row of this wave
+  const int rows = min(R * P, N - n0);                  // <= 0 past N
+
+  // ---- loads: scales, activations, weights, epilogue operands ----
+  const size_t base_row = rows > 0 ? (size_t)n0 : 0;
+  f16 sc[SCALED ? R : 1];
+  if constexpr (SCALED) {
+    const __amdgpu_buffer_rsrc_t sb =
+        buffer_rsrc(pre_scales + base_row * pre_G, rows > 0 ? (size_t)rows * pre_G * 2 : 0);
+    const int gi = (slot * CPL) >> pre_shift;
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+      sc[u] = __builtin_bit_cast(
+          f16, __builtin_amdgcn_raw_buffer_load_b16(sb, live ? ((u * P + ro) * pre_G + gi) * 2 : kOutOfRange, 0, 0));
+  }
+  u4 xv[XL];
+  {
+    const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(pre_x, (size_t)K * 2);
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      xv[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (slot * CPL + 8 * i) * 2 : kOutOfRange, 0, 0));
+  }
+  u4 w[R];
+  {
+    const __amdgpu_buffer_rsrc_t wb =
+        buffer_rsrc(pre_codes + base_row * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
+#pragma unroll
+    for (int u = 0; u < R; ++u)  // rows u P .. u P + P - 1 of the wave, contiguous
+      w[u] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(wb, live ? u * P * row_bytes + lane * 16 : kOutOfRange, 0, 0));
+  }
+  const int en = n0 + lane;  // the epilogue row of lane q < R P
+  const size_t ebytes = (size_t)N * 2;
+  const int eoff = lane < R * P && en < N ? en * 2 : kOutOfRange;
+  const f16 e_bias =
+      __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? ebytes : 0), eoff, 0, 0));
+  const f16 e_res = __builtin_bit_cast(
+      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.residual, p.residual ? ebytes : 0), eoff, 0, 0));
+  const f16 e_scale =
+      SCALED ? (f16)1.0f
+             : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pre_scales, ebytes), eoff, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first wait
+
+  // ---- arithmetic: one chain per load from -B, scaled by the lane's group scale ----
+  h2 xp[4 * XL];
+  const float bsum = line_pairs<FMT>(xv, xp);
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    const float a = line_dot<FMT>(w[u], xp, -bsum);
+    part[wave][u][lane] = SCALED ? (float)sc[u] * a : a;
+  }
+
+  // ---- row sums: lane q adds row q's S partials in slot order (the wave's own LDS rows) ----
+  if (lane < R * P && en < N) {
+    const int u = lane / P, r = lane % P;
+    const float *src = &part[wave][u][r * S];
+    float a = 0.0f;
+    for (int c = 0; c < S; ++c) a += src[c];
+    if constexpr (!SCALED) a *= (float)e_scale;
+    f16 h = (f16)a;
+    if (p.bias) h = (f16)((float)h + (float)e_bias);
+    if (p.residual) h = (f16)((float)e_res + (float)h);
+    p.y[en] = h;
+  }
+}
+
 }  // namespace lb

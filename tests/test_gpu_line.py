@@ -3,10 +3,10 @@ oracle.
 
 One-row INT4 / INT8 calls without a correction or prologue whose rows hold at least one segment
 (64 lanes x one 16-byte load: 2048 INT4 / 1024 INT8 codes) run there without any flag.  A wave
-reads 8 rows of one segment, 1 KB of each row per load, and the lane's activations once; the sum
-is the exact x . (q s) product (magic-bias codes on v_dot2_f32_f16 with the bias removed per
-lane; group scales per lane, or per lane quad once two reduction levels have summed it; per-row
-scales on the row total).  The bars are those of every linear path: rel-L2 <= 1e-3 against the
+reads 4 (rows of up to 4 segments) or 8 rows of one segment, 1 KB of each row per load, and the
+lane's activations once; the sum is the exact x . (q s) product (magic-bias codes on
+v_dot2_f32_f16 with the bias removed per lane; group scales per lane, or per lane quad once two
+reduction levels have summed it; per-row scales on the row total).  The bars are those of every linear path: rel-L2 <= 1e-3 against the
 oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for
 identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover 1..8
 INT4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,

@@ -331,8 +331,8 @@ bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
 #ifndef LB_LINE_WAVES
 #define LB_LINE_WAVES 4  // waves per line_gemv_kernel workgroup: whole row groups of every segment
 #endif
-#ifndef LB_LINE_ROWS
-#define LB_LINE_ROWS 8  // rows per line_gemv_kernel wave
+#ifndef LB_LINE_FEW_SEGMENTS
+#define LB_LINE_FEW_SEGMENTS 4  // rows of at most this many segments: 4 rows per wave (more waves), else 8
 #endif
 
 // One problem, one activation row, no prologue or correction, INT4 / INT8 codes whose 16-byte lane
@@ -345,7 +345,7 @@ bool try_line(const FusedParams &p, hipStream_t s) {
   if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
     return false;
   } else {
-    constexpr int CPL = LineTraits<FMT>::CPL, SEG = 64 * CPL, R = LB_LINE_ROWS;
+    constexpr int CPL = LineTraits<FMT>::CPL, SEG = 64 * CPL;
     const FusedProblem &q = p.prob[0];
     if (p.force_stream || p.prologue != PRO_NONE || q.rank > 0 || p.G <= 0 || p.K % p.G != 0) return false;
     const int group = p.K / p.G;
@@ -354,6 +354,7 @@ bool try_line(const FusedParams &p, hipStream_t s) {
       return false;
     const int nseg = (p.K + SEG - 1) / SEG;
     const int groups = std::max(1, std::min(LB_LINE_WAVES, kLineMaxWaves) / nseg);  // row groups per workgroup
+    const int R = nseg <= LB_LINE_FEW_SEGMENTS ? 4 : 8;
     const int rows_wg = groups * R;
     StreamParams sp{};
     sp.y = q.y;
@@ -365,12 +366,19 @@ bool try_line(const FusedParams &p, hipStream_t s) {
     sp.G = p.G;
     sp.group_shift = p.group_shift;
     const dim3 grid((q.N + rows_wg - 1) / rows_wg), block(64 * nseg * groups);
-    if (SCALED && group >= 4 * CPL)
-      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, R, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
+    const bool qs = SCALED && group >= 4 * CPL;
+    if (R == 4 && qs)
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, 4, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
+                         p.group_shift, nseg, groups, sp);
+    else if (R == 4)
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, 4, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
+                         p.G, p.group_shift, nseg, groups, sp);
+    else if (qs)
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, 8, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
                          p.group_shift, nseg, groups, sp);
     else
-      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, R, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K, p.G,
-                         p.group_shift, nseg, groups, sp);
+      hipLaunchKernelGGL((line_gemv_kernel<FMT, SCALED, 8, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
+                         p.G, p.group_shift, nseg, groups, sp);
     return true;
   }
 }

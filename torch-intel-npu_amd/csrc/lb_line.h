@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
   using TR = LineTraits<FMT>;
   constexpr int CPL = TR::CPL, XL = TR::XL, SEG = 64 * CPL;
   constexpr int kOutOfRange = (int)0x80000000u;
-  static_assert(R == 8 || R == 16, "rows per wave");
+  static_assert(R == 4 || R == 8 || R == 16, "rows per wave");
   __shared__ float part[kLineMaxWaves * R];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -207,7 +207,13 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
 #pragma unroll
     for (int i = 0; i < R / 4; ++i) v[i] *= (float)sc[i];
   }
-  line_fold<2, R / 4>(v, lane);
+  if constexpr (R >= 8) {
+    line_fold<2, R / 4>(v, lane);
+  } else {  // one value left: add lane ^ 4's copy (both moves under the full wave, then a select)
+    float down = dpp_move<kDppRowRor4>(v[0]), up = dpp_move<kDppRowRor12>(v[0]);
+    asm volatile("" : "+v"(down), "+v"(up));
+    v[0] += ((lane >> 2) & 1) ? down : up;
+  }
   if constexpr (R == 16) line_fold<3, 2>(v, lane);
   else v[0] += dpp_move<kDppRowRor8>(v[0]);
   v[0] += __shfl_xor(v[0], 16, 64);

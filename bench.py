@@ -176,21 +176,23 @@ class Group:
                                                        group_size=first.group))
 
 
-def smol_pass(m, device, stream, steps, warmup, grouped=False):
+def smol_pass(m, device, stream, steps, warmup, grouped=False, group=None):
     """One pass over the eight config-2 linears: per shape (8 launches) or, for M=1, in the decode
-    step's launch groups (5 launches)."""
+    step's launch groups (5 launches).  `group` replaces every shape's group size (32: the SmolLM
+    default the survey's config-2 row also asks for)."""
     linears = []
-    total = sum(algorithmic_bytes('int4', m, n, k, g) for _, n, k, g in SMOL_SHAPES)
+    shapes = [(name, n, k, group or g) for name, n, k, g in SMOL_SHAPES]
+    total = sum(algorithmic_bytes('int4', m, n, k, g) for _, n, k, g in shapes)
     copies = copies_for(total)
-    for i, (name, n, k, g) in enumerate(SMOL_SHAPES):
+    for i, (name, n, k, g) in enumerate(shapes):
         linears.append(Linear(make_weight('int4', n, k, g, 100 + i), m, copies, device, 200 + i))
-    by_name = {name: lin for (name, *_), lin in zip(SMOL_SHAPES, linears)}
+    by_name = {name: lin for (name, *_), lin in zip(shapes, linears)}
     if grouped:
         units = [(label, Group([by_name[n] for n in names], device) if len(names) > 1 else by_name[names[0]])
                  for label, names in DECODE_GROUPS]
         total = sum(u.bytes for _, u in units)
     else:
-        units = [(name, lin) for (name, *_), lin in zip(SMOL_SHAPES, linears)]
+        units = [(name, lin) for (name, *_), lin in zip(shapes, linears)]
     for _, unit in units:
         unit.calls[0].run()
     ms = time_passes(lambda r: [unit.calls[r % copies].run for _, unit in units], copies, steps, warmup, stream)
@@ -507,6 +509,12 @@ def main():
     del flat['linears']
     others = {'M=1 per shape': dict(gbs=round(flat['gbs'], 1), us_per_step=round(flat['ms_per_step'] * 1e3, 2),
                                     launches=flat['launches'], per_kernel=flat['per_kernel'])}
+    torch.cuda.empty_cache()
+    log('config-2 pass, M=1, group 32 (decode launch groups)')
+    g32 = smol_pass(1, device, stream, max(32, args.steps // 4), 8, grouped=True, group=32)
+    del g32['linears']
+    others['M=1 g32'] = dict(gbs=round(g32['gbs'], 1), us_per_step=round(g32['ms_per_step'] * 1e3, 2),
+                             launches=g32['launches'], per_kernel=g32['per_kernel'])
     torch.cuda.empty_cache()
     for m in (4, 16):
         log(f'config-2 pass, M={m}')

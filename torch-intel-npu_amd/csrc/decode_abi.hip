@@ -509,13 +509,21 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
   else launch_stream_wide_f<FMT_INT8, false>(p, s);
 }
 
-// tile_rows_kernel: one workgroup per 16-row tile, the staged row length for K.
+// tile_rows_kernel: TT 16-row tiles per workgroup, the staged row length for K.
+template <int FMT, bool SCALED, int MP, int TT>
+void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
+  const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT), block(256 * TT);
+  if (p.K <= 640) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT>), grid, block, 0, s, p);
+  else if (MP == 16 || p.K <= 2048) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT>), grid, block, 0, s, p);
+  else if constexpr (MP < 16) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT>), grid, block, 0, s, p);
+}
+
 template <int FMT, bool SCALED, int MP>
 void launch_tile_rows_mp(const StreamParams &p, hipStream_t s) {
-  const dim3 grid((p.N + 15) / 16);
-  if (p.K <= 640) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP>), grid, dim3(256), 0, s, p);
-  else if (MP == 16 || p.K <= 2048) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP>), grid, dim3(256), 0, s, p);
-  else if constexpr (MP < 16) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP>), grid, dim3(256), 0, s, p);
+  const int tt = tile_rows_per_wg((p.N + 15) / 16);
+  if (tt == 4) launch_tile_rows_tt<FMT, SCALED, MP, 4>(p, s);
+  else if (tt == 2) launch_tile_rows_tt<FMT, SCALED, MP, 2>(p, s);
+  else launch_tile_rows_tt<FMT, SCALED, MP, 1>(p, s);
 }
 
 template <int FMT, bool SCALED>

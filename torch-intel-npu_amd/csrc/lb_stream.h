@@ -686,38 +686,42 @@ __global__ __launch_bounds__(64 * WAVES) void stream_wide_kernel(StreamParams p)
 // Launches stream_wide_kernel for 17 <= p.M <= 32 rows.
 void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t stream);
 
-// One 16-row tile per workgroup for 2 .. MP activation rows (MP = 4, 8 or 16), the multi-row
-// form of the single-tile one-row kernels: the four waves split K (wave w takes k steps w, w + 4,
-// ...), every weight load of a lane is issued straight-line before the first wait (up to 32 x 16
-// bytes), the M activation rows are staged once in LDS in the decode8 slot order (zero from K on,
-// and a zero row that A rows past M read), the scales of the tile's 16 rows too.  The reference's
-// weights fp16(q * s) (decode8); the waves' partial sums are added in a fixed order through LDS.
+// TT 16-row tiles per workgroup for 2 .. MP activation rows (MP = 4, 8 or 16), the multi-row
+// form of the single-tile one-row kernels: four waves per tile split K (wave 4 i + w of tile i
+// takes k steps w, w + 4, ...), every weight load of a lane is issued straight-line before the
+// first wait (up to 32 x 16 bytes), the M activation rows are staged once per workgroup in LDS in
+// the decode8 slot order (zero from K on, and a zero row that A rows past M read) and serve its TT
+// tiles, the scales of each tile's 16 rows too.  The reference's weights fp16(q * s) (decode8);
+// each tile's four partial sums are added in a fixed order through LDS.
 // y[m, n] = fp16(sum) (* per-row scale before rounding for per-row int8) (+ bias, fp16).
-template <int FMT, bool SCALED, int KMAX, int MP>
-__global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
+template <int FMT, bool SCALED, int KMAX, int MP, int TT>
+__global__ __launch_bounds__(256 * TT) void tile_rows_kernel(StreamParams p) {
   constexpr int CPL = FormatTraits<FMT>::CPL, BITS = FormatTraits<FMT>::BITS, T8 = CPL / 8;
   constexpr int KSTEP = 4 * CPL, KG = 4, WSTEP = KG * KSTEP;
   constexpr int D = (KMAX + WSTEP - 1) / WSTEP;      // weight loads per lane
   static_assert(D <= 32, "KMAX too long for one tile per workgroup");
   constexpr int XLD = KMAX + KSTEP + 8;              // staged row pitch (halves)
   constexpr int NBR = KMAX / 8;                      // 8-code blocks per staged row
-  constexpr int XT = (MP * NBR + 255) / 256;         // activation loads per thread
+  constexpr int NT = 256 * TT;                       // threads of the workgroup
+  constexpr int XT = (MP * NBR + NT - 1) / NT;       // activation loads per thread
   static_assert(XT <= 16, "the staged rows are loaded in one batch");
   constexpr int GMAX = KMAX / 32;                    // groups per row at most (groups >= 32)
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
   constexpr int kOutOfRange = (int)0x80000000u;
   static_assert(MP == 4 || MP == 8 || MP == 16, "MP is 4, 8 or 16");
   __shared__ __align__(16) f16 xs[(MP + 1) * XLD];   // MP rows, then the zero row
-  __shared__ __align__(16) f16 ss[SCALED ? 16 * GMAX + 8 : 8];
-  __shared__ float red[(KG - 1) * 64 * 4];
+  __shared__ __align__(16) f16 ss[TT][SCALED ? 16 * GMAX + 8 : 8];
+  __shared__ float red[TT][(KG - 1) * 64 * 4];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((t >> 6) & 3);    // k split within the tile
+  const int tile = __builtin_amdgcn_readfirstlane(t >> 8);          // tile of the workgroup
+  const int tt = t & 255;                                           // thread within the tile
   const int j = lane & 15, g = lane >> 4;
   const int K = p.K;
-  const int n0 = blockIdx.x * 16;
-  const int rows = min(16, p.N - n0);
+  const int n0 = (blockIdx.x * TT + tile) * 16;
+  const int rows = min(16, p.N - n0);  // <= 0: the tile lies past N (no loads, no stores)
   const int row_bytes = K * BITS / 8;
   const int blocks = K >> 3;
 
@@ -731,7 +735,7 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
   h8 xv[XT];
 #pragma unroll
   for (int i = 0; i < XT; ++i) {
-    const int idx = i * 256 + t;
+    const int idx = i * NT + t;
     const int m = idx / NBR, b = idx - m * NBR;
     const bool live = m < p.M && b < blocks;
     xv[i] = __builtin_bit_cast(
@@ -741,11 +745,13 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
   // Scales of the tile's rows (16 x G halves), weights of this wave's k steps.
   uint32_t sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
-    const __amdgpu_buffer_rsrc_t sb = buffer_rsrc(p.scales + (size_t)n0 * p.G, (size_t)rows * p.G * 2);
+    const __amdgpu_buffer_rsrc_t sb =
+        buffer_rsrc(p.scales + (size_t)(rows > 0 ? n0 : 0) * p.G, (size_t)max(rows, 0) * p.G * 2);
 #pragma unroll
-    for (int i = 0; i < SC; ++i) sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, (t + 256 * i) * 2, 0, 0);
+    for (int i = 0; i < SC; ++i) sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, (tt + 256 * i) * 2, 0, 0);
   }
-  const __amdgpu_buffer_rsrc_t wb = buffer_rsrc(p.codes + (size_t)n0 * row_bytes, (size_t)rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t wb =
+      buffer_rsrc(p.codes + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)max(rows, 0) * row_bytes);
   u4 w[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) {
@@ -755,21 +761,21 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
   __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
 #pragma unroll
   for (int i = 0; i < XT; ++i) {
-    const int idx = i * 256 + t;
+    const int idx = i * NT + t;
     const int m = idx / NBR, b = idx - m * NBR;
     if (m < p.M) *reinterpret_cast<h8 *>(xs + m * XLD + 8 * b) = permute_block<FMT>(xv[i]);
   }
   // Zero tails (k from KMAX on) of the staged rows and the whole zero row.
-  for (int i = t; i < MP * ((XLD - KMAX) / 8); i += 256) {
+  for (int i = t; i < MP * ((XLD - KMAX) / 8); i += NT) {
     const int m = i / ((XLD - KMAX) / 8), b = i - m * ((XLD - KMAX) / 8);
     if (m < p.M) *reinterpret_cast<h8 *>(xs + m * XLD + KMAX + 8 * b) = h8{};
   }
-  for (int i = t; i < XLD / 8; i += 256) *reinterpret_cast<h8 *>(xs + MP * XLD + 8 * i) = h8{};
+  for (int i = t; i < XLD / 8; i += NT) *reinterpret_cast<h8 *>(xs + MP * XLD + 8 * i) = h8{};
   if constexpr (SCALED) {
 #pragma unroll
     for (int i = 0; i < SC; ++i)
-      if (t + 256 * i < 16 * GMAX) ss[t + 256 * i] = __builtin_bit_cast(f16, (unsigned short)sreg[i]);
-    if (t < 8) ss[16 * GMAX + t] = (f16)0.0f;
+      if (tt + 256 * i < 16 * GMAX) ss[tile][tt + 256 * i] = __builtin_bit_cast(f16, (unsigned short)sreg[i]);
+    if (tt < 8) ss[tile][16 * GMAX + tt] = (f16)0.0f;
   }
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
   __syncthreads();
@@ -785,7 +791,7 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
     if constexpr (SCALED) {
       // past K the scale is zero (index past the row's groups reads the next row or the pad,
       // and the codes there are zero: only the zero scale makes fp16(q * s) zero for every format)
-      const f16 sc = kb + g * CPL < K ? ss[j * p.G + ((kb + g * CPL) >> p.group_shift)] : (f16)0.0f;
+      const f16 sc = kb + g * CPL < K ? ss[tile][j * p.G + ((kb + g * CPL) >> p.group_shift)] : (f16)0.0f;
       s2 = h2{sc, sc};
     }
 #pragma unroll
@@ -794,16 +800,16 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, decode8<FMT, !SCALED>(w[u], q, s2, nf4_table), acc, 0, 0, 0);
     }
   }
-  // Partial sums of waves 1..3 through LDS; wave 0 adds them in order and writes the tile.
+  // Partial sums of waves 1..3 of each tile through LDS; its wave 0 adds them in order and writes it.
   if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[((wave - 1) * 64 + lane) * 4 + r] = acc[r];
+    for (int r = 0; r < 4; ++r) red[tile][((wave - 1) * 64 + lane) * 4 + r] = acc[r];
   }
   __syncthreads();
   if (wave > 0) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    acc[r] = ((acc[r] + red[lane * 4 + r]) + red[(64 + lane) * 4 + r]) + red[(128 + lane) * 4 + r];
+    acc[r] = ((acc[r] + red[tile][lane * 4 + r]) + red[tile][(64 + lane) * 4 + r]) + red[tile][(128 + lane) * 4 + r];
   // Lane (j, g) holds rows 4g .. 4g+3 of column j (weight row n0 + j).  The bias / per-row
   // scale of column j sit in lane j (group 0).
   const f16 bias = __builtin_bit_cast(f16, (unsigned short)__shfl((int)ebias, j, 64));
@@ -819,6 +825,15 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(StreamParams p) {
     if (p.bias) h = (f16)((float)h + (float)bias);
     p.y[(size_t)m * p.ldy + n0 + j] = h;
   }
+}
+
+#ifndef LB_TILE_ROWS_MIN_WGS
+#define LB_TILE_ROWS_MIN_WGS 224  // tile_rows_kernel groups 4 (or 2) tiles per workgroup while this many remain
+#endif
+// Tiles per tile_rows_kernel workgroup for `tiles` 16-row tiles: the staged activation rows are
+// shared by more tiles as long as the grid keeps LB_TILE_ROWS_MIN_WGS workgroups.
+inline int tile_rows_per_wg(long long tiles) {
+  return tiles >= 4ll * LB_TILE_ROWS_MIN_WGS ? 4 : tiles >= 2ll * LB_TILE_ROWS_MIN_WGS ? 2 : 1;
 }
 
 // Launches tile_rows_kernel for 2 <= p.M <= 16 rows with M * K <= 32768 (K <= 4096): the staged

@@ -309,12 +309,14 @@ bool stream_rows_eligible(const lb_linear_args *a) {
 #endif
 
 // Several activation rows, no correction, rows the one-tile kernel stages whole (K <= 4096, and
-// K <= 2048 beyond 8 rows), int4 / nf4 / int8 codes.  Every tile stages all M rows, so the tiles
-// together read the activations (N / 16) times: past LB_TILE_ROWS_MAX_X_BYTES of those reads the
-// tiled GEMV, whose workgroups share the staged rows over more tiles, measured faster.
+// K <= 2048 beyond 8 rows), int4 / nf4 / int8 codes.  Every workgroup stages all M rows for its 1,
+// 2 or 4 tiles, so the workgroups together read the activations that many times: past
+// LB_TILE_ROWS_MAX_X_BYTES of those reads the tiled GEMV, whose workgroups share the staged rows
+// over more tiles, measured faster.
 bool tile_rows_eligible(const lb_linear_args *a) {
   if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16 || a->K > 4096 || (a->M > 8 && a->K > 2048)) return false;
-  if ((a->N + 15) / 16 * a->M * a->K * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
+  const int64_t tiles = (a->N + 15) / 16, wgs = (tiles + tile_rows_per_wg(tiles) - 1) / tile_rows_per_wg(tiles);
+  if (wgs * a->M * a->K * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
   return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
 }
 

@@ -165,11 +165,22 @@ __device__ __forceinline__ void load_words4(__amdgpu_buffer_rsrc_t wb, int byte_
   }
 }
 
-// Re-reads (bounded wait) each of the four words whose tag is not current.
-__device__ __forceinline__ void settle_words4(const LayerParams &p, const uint64_t *a, uint32_t tag, uint64_t (&w)[4]) {
+// Makes the four words current: when any is stale, waits (bounded) for the first stale one, then
+// re-reads the four in one round trip (consecutive words come from one producer, so they are
+// current together), and only a word still stale after that is waited for on its own.
+__device__ __forceinline__ void settle_words4(const LayerParams &p, __amdgpu_buffer_rsrc_t wb, int byte_off,
+                                              const uint64_t *a, uint32_t tag, uint64_t (&w)[4]) {
+  int first = -1;
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    if (__builtin_expect(word_tag(w[q]) != tag, 0)) w[q] = wait_word(p, a + q, tag);
+  for (int q = 3; q >= 0; --q)
+    if (word_tag(w[q]) != tag) first = q;
+  if (__builtin_expect(first >= 0, 0)) {
+    (void)wait_word(p, a + first, tag);
+    load_words4(wb, byte_off, w);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (__builtin_expect(word_tag(w[q]) != tag, 0)) w[q] = wait_word(p, a + q, tag);
+  }
 }
 
 __device__ __forceinline__ h8 words4_to_h8(const uint64_t (&w)[4]) {
@@ -184,7 +195,7 @@ __device__ __forceinline__ h8 words4_to_h8(const uint64_t (&w)[4]) {
 
 // The source row of a role's products (K values, 8 per block, thread t holding blocks t + 256 i)
 // and the prologue's second row (gamma, or the up half for SiLU-multiply).  Every word of the
-// thread is requested at once; only words still stale are then waited for one by one.
+// thread is requested at once; a quad with a stale word is re-read once that word is current.
 template <int XB>
 __device__ __forceinline__ void layer_source_row(const LayerParams &p, int base, int src, int K, uint32_t tag,
                                                  h8 (&xv)[XB], h8 (&av)[XB]) {
@@ -203,10 +214,10 @@ __device__ __forceinline__ void layer_source_row(const LayerParams &p, int base,
   for (int i = 0; i < XB; ++i) {
     const int b = t + 256 * i;
     if (b < blocks) {
-      settle_words4(p, p.ws + base + 4 * b, tag, wx[i]);
+      settle_words4(p, wb, (base + 4 * b) * 8, p.ws + base + 4 * b, tag, wx[i]);
       xv[i] = words4_to_h8(wx[i]);
       if (src == SRC_GU) {
-        settle_words4(p, p.ws + second + 4 * b, tag, wa[i]);
+        settle_words4(p, wb, (second + 4 * b) * 8, p.ws + second + 4 * b, tag, wa[i]);
         av[i] = words4_to_h8(wa[i]);
       }
     } else {

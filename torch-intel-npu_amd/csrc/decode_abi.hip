@@ -418,8 +418,13 @@ bool try_pack(const FusedParams &p, hipStream_t s) {
     sp.G = p.G;
     sp.group_shift = p.group_shift;
     const int rows_wg = WAVES * R * per_load;
-    hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R>), dim3((q.N + rows_wg - 1) / rows_wg), dim3(64 * WAVES), 0, s,
-                       p.x, q.codes, q.scales, q.N, p.K, p.G, p.group_shift, sp);
+    const dim3 grid((q.N + rows_wg - 1) / rows_wg), block(64 * WAVES);
+    if (q.bias || q.residual)
+      hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
+                         p.G, p.group_shift, sp);
+    else
+      hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
+                         p.G, p.group_shift, sp);
     return true;
   }
 }

@@ -240,9 +240,12 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
 // (P S x 16 contiguous bytes; the SmolLM K = 576 INT4 rows: 3 rows in 54 lanes).  Lane l always
 // holds slot l % S of its row, so its activations are loaded once and serve all R loads (R P rows
 // per wave).  Each lane's partial per load is scaled by its group's scale (groups of at least CPL
-// codes) and goes to the wave's own LDS rows; lane q of the wave then adds the S partials of row q
-// in slot order.  Waves are independent: no barrier.
-template <int FMT, bool SCALED, int R>
+// codes).  Where S is even (a multiple of 4), pairs (quads) of neighbouring slot partials are
+// added by DPP first: a row's lanes start at an even (4-aligned) lane, so partners stay within
+// the row, in the same order for every row.  The sums go to the wave's own LDS rows, contiguous
+// per row, and lane q of the wave adds row q's in slot order.  Waves are independent: no barrier.
+// Bias and residual loads are compiled in only with EPI (either present).
+template <int FMT, bool SCALED, int R, bool EPI>
 __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const uint8_t *pre_codes,
                                                         const f16 *pre_scales, int pre_N, int pre_K, int pre_G,
                                                         int pre_shift, StreamParams p) {
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const 
   const int n0 = (blockIdx.x * WAVES + wave) * R * P;  // first row of this wave
   const int rows = min(R * P, N - n0);                  // <= 0 past N
 
-  // ---- loads: scales, activations, weights, epilogue operands ----
+  // ---- loads: scales, activations, epilogue operands, weights ----
   const size_t base_row = rows > 0 ? (size_t)n0 : 0;
   f16 sc[SCALED ? R : 1];
   if constexpr (SCALED) {
@@ -283,6 +286,19 @@ __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const 
       xv[i] = __builtin_bit_cast(
           u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (slot * CPL + 8 * i) * 2 : kOutOfRange, 0, 0));
   }
+  const int en = n0 + lane;  // the epilogue row of lane q < R P
+  const size_t ebytes = (size_t)N * 2;
+  const int eoff = lane < R * P && en < N ? en * 2 : kOutOfRange;
+  f16 e_bias = (f16)0.0f, e_res = (f16)0.0f;
+  if constexpr (EPI) {  // an absent operand is an empty buffer (reads zeros)
+    e_bias = __builtin_bit_cast(
+        f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? ebytes : 0), eoff, 0, 0));
+    e_res = __builtin_bit_cast(
+        f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.residual, p.residual ? ebytes : 0), eoff, 0, 0));
+  }
+  const f16 e_scale =
+      SCALED ? (f16)1.0f
+             : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pre_scales, ebytes), eoff, 0, 0));
   u4 w[R];
   {
     const __amdgpu_buffer_rsrc_t wb =
@@ -292,37 +308,34 @@ __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const 
       w[u] = __builtin_bit_cast(
           u4, __builtin_amdgcn_raw_buffer_load_b128(wb, live ? u * P * row_bytes + lane * 16 : kOutOfRange, 0, 0));
   }
-  const int en = n0 + lane;  // the epilogue row of lane q < R P
-  const size_t ebytes = (size_t)N * 2;
-  const int eoff = lane < R * P && en < N ? en * 2 : kOutOfRange;
-  const f16 e_bias =
-      __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? ebytes : 0), eoff, 0, 0));
-  const f16 e_res = __builtin_bit_cast(
-      f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.residual, p.residual ? ebytes : 0), eoff, 0, 0));
-  const f16 e_scale =
-      SCALED ? (f16)1.0f
-             : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pre_scales, ebytes), eoff, 0, 0));
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first wait
 
   // ---- arithmetic: one chain per load from -B, scaled by the lane's group scale ----
   h2 xp[4 * XL];
   const float bsum = line_pairs<FMT>(xv, xp);
+  const int lg = S % 4 == 0 ? 2 : S % 2 == 0 ? 1 : 0;  // log2 of the slots per LDS sum
 #pragma unroll
   for (int u = 0; u < R; ++u) {
     const float a = line_dot<FMT>(w[u], xp, -bsum);
-    part[wave][u][lane] = SCALED ? (float)sc[u] * a : a;
+    float v = SCALED ? (float)sc[u] * a : a;
+    // Both moves under the full wave, then uniform selects.
+    const float o1 = dpp_move<kDppXor1>(v);
+    v = lg >= 1 ? v + o1 : v;
+    const float o2 = dpp_move<kDppXor2>(v);
+    v = lg == 2 ? v + o2 : v;
+    if ((lane & ((1 << lg) - 1)) == 0) part[wave][u][lane >> lg] = v;
   }
 
-  // ---- row sums: lane q adds row q's S partials in slot order (the wave's own LDS rows) ----
+  // ---- row sums: lane q adds row q's sums in slot order (the wave's own LDS rows) ----
   if (lane < R * P && en < N) {
     const int u = lane / P, r = lane % P;
-    const float *src = &part[wave][u][r * S];
+    const float *src = &part[wave][u][(r * S) >> lg];
     float a = 0.0f;
-    for (int c = 0; c < S; ++c) a += src[c];
+    for (int c = 0; c < (S >> lg); ++c) a += src[c];
     if constexpr (!SCALED) a *= (float)e_scale;
     f16 h = (f16)a;
-    if (p.bias) h = (f16)((float)h + (float)e_bias);
-    if (p.residual) h = (f16)((float)e_res + (float)h);
+    if (EPI && p.bias) h = (f16)((float)h + (float)e_bias);
+    if (EPI && p.residual) h = (f16)((float)e_res + (float)h);
     p.y[en] = h;
   }
 }

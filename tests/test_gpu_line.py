@@ -11,8 +11,10 @@ oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106
 identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover 1..8
 INT4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,
 groups of one lane pair, one quad and longer, per-row scales, bias and residual.  Rows shorter
-than a segment over at least 16384 rows (the SmolLM tied head) take pack_gemv_kernel, which packs
-whole rows across a wave's lanes; its cases follow the same bars.
+than a segment take pack_gemv_kernel, which packs whole rows across a wave's lanes: four loads per
+wave over at least 16384 rows (the SmolLM tied head), one load per wave for INT4 below that (the
+SmolLM projections), and one to three problems sharing the activation row in one lb_fused_linear
+(q|k|v, gate|up); its cases follow the same bars.
 """
 import numpy as np
 import pytest
@@ -179,6 +181,13 @@ PACK_SHAPES = [
     ('int4', 16390, 992, 32),      # two rows per load (62 lanes), ragged N
     ('int8', 20000, 576, 576),     # per-row int8, one row per load (36 lanes)
     ('int8', 16400, 992, 32),      # int8 groups of two lanes, 62 lanes
+    # below 16384 rows (INT4): one load per wave
+    ('int4', 576, 576, 64),        # SmolLM q / o: 3 rows per wave
+    ('int4', 192, 576, 64),        # SmolLM k / v
+    ('int4', 576, 1536, 128),      # SmolLM down: one row per wave (48 lanes)
+    ('int4', 1536, 576, 32),       # SmolLM gate / up with groups of one lane
+    ('int4', 5, 992, 32),          # two rows per load, one partly filled wave
+    ('int4', 16383, 576, 64),      # one row short of the four-load kernel
 ]
 
 
@@ -218,7 +227,8 @@ def test_pack_identity_is_bit_exact(device, fmt, group):
                                       err_msg=f'column {col}')
 
 
-@pytest.mark.parametrize('spec', [('int4', 16390, 576, 64), ('int4', 16390, 992, 32)], ids=lambda s: '-'.join(map(str, s)))
+@pytest.mark.parametrize('spec', [('int4', 16390, 576, 64), ('int4', 16390, 992, 32), ('int4', 578, 576, 64),
+                                  ('int4', 1000, 1536, 128)], ids=lambda s: '-'.join(map(str, s)))
 def test_pack_row_reversal_is_bit_exact(device, spec):
     """A row's sum is its slots' partials in slot order, whatever lanes the row falls to."""
     fmt, n, k, group = spec
@@ -257,3 +267,77 @@ def test_pack_residual_through_fused_linear(device):
     budget = o.rounding_budget(x, 'int4', (n, k), group, data, scales.tobytes())[0]
     ulp = (np.abs(want.astype(np.float64)) + np.abs(plain.astype(np.float64))) * 2.0 ** -10 + 2.0 ** -24
     assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= budget + ulp).all()
+
+
+# Several problems sharing the activation row in one lb_fused_linear call (no prologue or
+# correction): each problem's rows over its own waves of pack_gemv_kernel.  (fmt, group, K, rows of
+# each problem, bias on, residual on)
+PACK_MULTI = [
+    ('int4', 64, 576, (576, 192, 192), (), ()),            # SmolLM q|k|v: one load per wave
+    ('int4', 64, 576, (1536, 1536), (), ()),               # SmolLM gate|up
+    ('int4', 32, 576, (100, 7, 33), (1,), (0, 2)),         # ragged rows, bias and residual
+    ('int4', 128, 1536, (10000, 8000), (0,), ()),          # 18000 rows: four loads per wave
+    ('int8', 576, 576, (9000, 8000, 5), (), (1,)),         # per-row int8 over 17005 rows
+]
+
+
+@pytest.mark.parametrize('spec', PACK_MULTI, ids=lambda s: f'{s[0]}-g{s[1]}-k{s[2]}-' + 'x'.join(map(str, s[3])))
+def test_pack_problems_through_fused_linear(device, spec):
+    """Every problem equals its own one-problem product: fp16(x W^T) (+ bias) (+ residual, y and
+    residual the same buffer), checked against the oracle at the linear path's bars."""
+    fmt, group, k, rows, with_bias, with_res = spec
+    announce('pack problems', spec)
+    rng = np.random.default_rng(sum(rows) + k + group)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    problems, refs = [], []
+    for j, n in enumerate(rows):
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        data, scales = o.quantize(w, fmt, group)
+        bias = (rng.standard_normal(n) * 0.1).astype(np.float16) if j in with_bias else None
+        res = (rng.standard_normal(n) * 0.5).astype(np.float16) if j in with_res else None
+        y = to_dev(res, device) if res is not None else torch.empty(n, dtype=torch.float16, device=device)
+        pr = dict(codes=to_dev(np.frombuffer(data, np.uint8), device),
+                  scales=to_dev(np.frombuffer(scales, np.float16), device), N=n, y=y)
+        if bias is not None:
+            pr['bias'] = to_dev(bias, device)
+        if res is not None:
+            pr['residual'] = y
+        problems.append(pr)
+        refs.append((data, scales, bias, res))
+    outs = lowbit_hip.fused_linear(to_dev(x[0], device), problems, format=fmt, K=k, group_size=group)
+    torch.cuda.synchronize()
+    for j, (n, out, (data, scales, bias, res)) in enumerate(zip(rows, outs, refs)):
+        got = out.cpu().numpy()
+        plain = o.linear(x, fmt, (n, k), group, data, scales)[0]
+        want = plain
+        if bias is not None:
+            want = (want.astype(np.float32) + bias.astype(np.float32)).astype(np.float16)
+        if res is not None:
+            want = (res.astype(np.float32) + want.astype(np.float32)).astype(np.float16)
+        assert np.isfinite(got).all(), f'problem {j}'
+        assert o.rel_l2(got, want) <= 1e-3, f'problem {j}: rel-L2 {o.rel_l2(got, want):.3e}'
+        if bias is None and res is None:
+            budget = o.rounding_budget(x, fmt, (n, k), group, data, scales)[0]
+            ulp = np.abs(want.astype(np.float64)) * 2.0 ** -10 + 2.0 ** -24
+            assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= budget + ulp).all(), f'problem {j}'
+
+
+def test_pack_problems_match_single_calls(device):
+    """q|k|v in one call gives, bit for bit, what three one-problem calls give."""
+    announce('pack problems vs single')
+    k, group, rows = 576, 64, (576, 192, 192)
+    rng = np.random.default_rng(71)
+    x = to_dev(rng.standard_normal(k).astype(np.float16), device)
+    problems, singles = [], []
+    for n in rows:
+        data, scales = o.quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32), 'int4', group)
+        codes = to_dev(np.frombuffer(data, np.uint8), device)
+        sc = to_dev(np.frombuffer(scales, np.float16), device)
+        problems.append(dict(codes=codes, scales=sc, N=n, y=torch.empty(n, dtype=torch.float16, device=device)))
+        singles.append(lowbit_hip.fused_linear(x, [dict(codes=codes, scales=sc, N=n,
+                                                        y=torch.empty(n, dtype=torch.float16, device=device))],
+                                               format='int4', K=k, group_size=group)[0])
+    outs = lowbit_hip.fused_linear(x, problems, format='int4', K=k, group_size=group)
+    torch.cuda.synchronize()
+    for a, b in zip(outs, singles):
+        np.testing.assert_array_equal(a.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16))

@@ -384,47 +384,89 @@ bool try_line(const FusedParams &p, hipStream_t s) {
 }
 
 #ifndef LB_PACK_MIN_ROWS
-#define LB_PACK_MIN_ROWS 16384  // rows from which one-row calls of short rows take pack_gemv_kernel
+#define LB_PACK_MIN_ROWS 16384  // INT8: rows (over the problems) from which pack_gemv_kernel takes the call
 #endif
 #ifndef LB_PACK_ROWS
-#define LB_PACK_ROWS 4  // wave-wide loads per pack_gemv_kernel wave
+#define LB_PACK_ROWS 4  // wave-wide loads per pack_gemv_kernel wave from LB_PACK_MIN_ROWS rows on
+#endif
+#ifndef LB_PACK_SMALL
+#define LB_PACK_SMALL 1  // INT4 below LB_PACK_MIN_ROWS rows: pack_gemv_kernel with one load per wave
 #endif
 
-// One problem, one activation row, no prologue or correction, INT4 / INT8 rows of 8 .. 63 16-byte
-// slots (shorter than a line_gemv_kernel segment) whose lane loads each lie in one group: launched
-// in pack_gemv_kernel (false otherwise).
+template <int FMT, bool SCALED, int R, int NP>
+void launch_pack(const FusedParams &p, const PackTable &tab, int waves, bool epi, hipStream_t s) {
+  const FusedProblem &q = p.prob[0];
+  StreamParams sp{};
+  sp.y = q.y;
+  sp.bias = q.bias;
+  sp.residual = q.residual;
+  sp.M = 1;
+  sp.N = q.N;
+  sp.K = p.K;
+  sp.G = p.G;
+  sp.group_shift = p.group_shift;
+  const dim3 grid((waves + 3) / 4), block(256);
+  if (epi)
+    hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, true, NP>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
+                       p.G, p.group_shift, sp, tab);
+  else
+    hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, false, NP>), grid, block, 0, s, p.x, q.codes, q.scales, q.N,
+                       p.K, p.G, p.group_shift, sp, tab);
+}
+
+// One activation row, no prologue or correction, INT4 / INT8 rows of 8 .. 63 16-byte slots
+// (shorter than a line_gemv_kernel segment) whose lane loads each lie in one group, one to three
+// problems: launched in pack_gemv_kernel (false otherwise).  Four loads per wave from
+// LB_PACK_MIN_ROWS rows over the problems on; below that INT4 calls take one load per wave (more,
+// shorter waves: the latency of one load and its sum is what such calls cost), INT8 calls decline.
 template <int FMT, bool SCALED>
-bool try_pack(const FusedParams &p, hipStream_t s) {
+bool try_pack(const FusedParams &p, int tiles, hipStream_t s) {
   if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
     return false;
   } else {
-    constexpr int CPL = LineTraits<FMT>::CPL, R = LB_PACK_ROWS, WAVES = 4;
-    const FusedProblem &q = p.prob[0];
-    if (p.force_stream || p.prologue != PRO_NONE || q.rank > 0 || p.G <= 0 || p.K % p.G != 0 || q.N < LB_PACK_MIN_ROWS)
-      return false;
+    constexpr int CPL = LineTraits<FMT>::CPL;
+    if (p.force_stream || p.prologue != PRO_NONE || p.G <= 0 || p.K % p.G != 0) return false;
+    const int np = 1 + (p.prob[0].tiles_end < tiles) + (p.prob[1].tiles_end < tiles);
     const int group = p.K / p.G;
     const int row_bytes = p.K * LineTraits<FMT>::BITS / 8;
     const int slots = row_bytes / 16, per_load = slots > 0 ? 64 / slots : 0;
-    if (row_bytes % 16 != 0 || slots < 8 || slots >= 64 || per_load * R > 64 || stream_group_span(FMT, p.K, group) == 0 ||
-        (group != p.K && group < CPL) || !aligned(q.codes, 16) || !aligned(p.x, 16))
+    if (row_bytes % 16 != 0 || slots < 8 || slots >= 64 || per_load * LB_PACK_ROWS > 64 ||
+        stream_group_span(FMT, p.K, group) == 0 || (group != p.K && group < CPL) || !aligned(p.x, 16))
       return false;
-    StreamParams sp{};
-    sp.y = q.y;
-    sp.bias = q.bias;
-    sp.residual = q.residual;
-    sp.M = 1;
-    sp.N = q.N;
-    sp.K = p.K;
-    sp.G = p.G;
-    sp.group_shift = p.group_shift;
-    const int rows_wg = WAVES * R * per_load;
-    const dim3 grid((q.N + rows_wg - 1) / rows_wg), block(64 * WAVES);
-    if (q.bias || q.residual)
-      hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, true>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
-                         p.G, p.group_shift, sp);
-    else
-      hipLaunchKernelGGL((pack_gemv_kernel<FMT, SCALED, R, false>), grid, block, 0, s, p.x, q.codes, q.scales, q.N, p.K,
-                         p.G, p.group_shift, sp);
+    long long rows = 0;
+    for (int j = 0; j < np; ++j) {
+      const FusedProblem &q = p.prob[j];
+      if (q.rank > 0 || q.N < 1 || !aligned(q.codes, 16)) return false;
+      rows += q.N;
+    }
+    const bool big = rows >= LB_PACK_MIN_ROWS;
+    if (!big && (FMT != FMT_INT4 || !LB_PACK_SMALL)) return false;
+    const int R = big ? LB_PACK_ROWS : 1, per_wave = R * per_load;
+    PackTable tab{};
+    int waves = 0;
+    bool epi = false;
+    for (int j = 0; j < np; ++j) {
+      const FusedProblem &q = p.prob[j];
+      tab.codes[j] = q.codes;
+      tab.scales[j] = q.scales;
+      tab.y[j] = q.y;
+      tab.bias[j] = q.bias;
+      tab.residual[j] = q.residual;
+      tab.N[j] = q.N;
+      waves += (q.N + per_wave - 1) / per_wave;
+      tab.wave_end[j] = waves;
+      epi = epi || q.bias || q.residual;
+    }
+    for (int j = np; j < kPackMaxProblems; ++j) tab.wave_end[j] = waves;
+    const bool r4 = R == LB_PACK_ROWS;
+    switch (np) {
+      case 1: r4 ? launch_pack<FMT, SCALED, LB_PACK_ROWS, 1>(p, tab, waves, epi, s)
+                 : launch_pack<FMT, SCALED, 1, 1>(p, tab, waves, epi, s); break;
+      case 2: r4 ? launch_pack<FMT, SCALED, LB_PACK_ROWS, 2>(p, tab, waves, epi, s)
+                 : launch_pack<FMT, SCALED, 1, 2>(p, tab, waves, epi, s); break;
+      default: r4 ? launch_pack<FMT, SCALED, LB_PACK_ROWS, 3>(p, tab, waves, epi, s)
+                  : launch_pack<FMT, SCALED, 1, 3>(p, tab, waves, epi, s); break;
+    }
     return true;
   }
 }
@@ -435,7 +477,7 @@ bool try_pack(const FusedParams &p, hipStream_t s) {
 template <int FMT, bool SCALED>
 void launch_fused_t(const FusedParams &p, int tiles, bool ranked, hipStream_t s) {
   if (!ranked && p.prob[0].tiles_end == tiles && try_line<FMT, SCALED>(p, s)) return;
-  if (!ranked && p.prob[0].tiles_end == tiles && try_pack<FMT, SCALED>(p, s)) return;
+  if (!ranked && try_pack<FMT, SCALED>(p, tiles, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles && try_stream<FMT, SCALED>(p, tiles, s)) return;
   if (!ranked && p.prob[0].tiles_end == tiles) {
     if (tiles / 4 >= LB_ROWS_MIN_WGS && launch_rows<FMT, SCALED, 4>(p, tiles, s)) return;

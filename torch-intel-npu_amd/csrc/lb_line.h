@@ -234,6 +234,19 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
   }
 }
 
+// Problems of one pack_gemv_kernel launch past the first: weights sharing the activation row, K and
+// the group size (q|k|v, gate|up), each over its own range of waves.
+constexpr int kPackMaxProblems = 3;
+struct PackTable {
+  const uint8_t *codes[kPackMaxProblems];
+  const f16 *scales[kPackMaxProblems];
+  f16 *y[kPackMaxProblems];
+  const f16 *bias[kPackMaxProblems];
+  const f16 *residual[kPackMaxProblems];
+  int N[kPackMaxProblems];
+  int wave_end[kPackMaxProblems];  // exclusive prefix sums of the problems' waves
+};
+
 // One-row GEMV for rows of at most 64 16-byte slots (up to 2048 INT4 / 1024 INT8 codes, the
 // SmolLM shapes): the same lane-linear loads with whole rows packed across a wave's lanes.  A row
 // of S slots takes S lanes, so P = 64 / S consecutive rows fill P S lanes of a wave-wide load
@@ -244,65 +257,84 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
 // added by DPP first: a row's lanes start at an even (4-aligned) lane, so partners stay within
 // the row, in the same order for every row.  The sums go to the wave's own LDS rows, contiguous
 // per row, and lane q of the wave adds row q's in slot order.  Waves are independent: no barrier.
-// Bias and residual loads are compiled in only with EPI (either present).
-template <int FMT, bool SCALED, int R, bool EPI>
+// Bias and residual loads are compiled in only with EPI (any present).  With NP > 1 problems the
+// waves are dealt to the problems by the table's prefix sums (a wave's problem is uniform) and
+// the activations are loaded first, while the problem's pointers arrive from the argument block;
+// with one problem every pointer of the first loads is a preloaded argument.
+template <int FMT, bool SCALED, int R, bool EPI, int NP>
 __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const uint8_t *pre_codes,
                                                         const f16 *pre_scales, int pre_N, int pre_K, int pre_G,
-                                                        int pre_shift, StreamParams p) {
+                                                        int pre_shift, StreamParams p, PackTable tab) {
   using TR = LineTraits<FMT>;
   constexpr int CPL = TR::CPL, XL = TR::XL;
   constexpr int kOutOfRange = (int)0x80000000u;
   constexpr int WAVES = 4;
+  static_assert(NP >= 1 && NP <= kPackMaxProblems, "problems per launch");
   __shared__ float part[WAVES][R][64];
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int N = pre_N, K = pre_K;
+  const int K = pre_K;
   const int row_bytes = K * TR::BITS / 8;
   const int S = row_bytes >> 4;        // 16-byte slots per row (1 .. 64)
   const int P = 64 / S;                // rows per wave-wide load
   const int slot = lane % S, ro = lane / S;
   const bool live = ro < P;
-  const int n0 = (blockIdx.x * WAVES + wave) * R * P;  // first row of this wave
-  const int rows = min(R * P, N - n0);                  // <= 0 past N
+  int gw = blockIdx.x * WAVES + wave;  // the wave's index within its problem
+  const uint8_t *codes = pre_codes;
+  const f16 *scales = pre_scales;
+  f16 *y = p.y;
+  const f16 *bias = p.bias, *residual = p.residual;
+  int N = pre_N;
 
-  // ---- loads: scales, activations, epilogue operands, weights ----
+  // ---- loads: (NP > 1: activations first), scales, activations, epilogue operands, weights ----
+  u4 xv[XL];
+  auto load_x = [&] {
+    const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(pre_x, (size_t)K * 2);
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      xv[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (slot * CPL + 8 * i) * 2 : kOutOfRange, 0, 0));
+  };
+  if constexpr (NP > 1) {
+    load_x();
+    const int j = (gw >= tab.wave_end[0]) + (NP > 2 && gw >= tab.wave_end[1]);
+    gw -= j == 0 ? 0 : tab.wave_end[j - 1];
+    codes = tab.codes[j];
+    scales = tab.scales[j];
+    y = tab.y[j];
+    bias = tab.bias[j];
+    residual = tab.residual[j];
+    N = tab.N[j];
+  }
+  const int n0 = gw * R * P;              // first row of this wave
+  const int rows = min(R * P, N - n0);    // <= 0 past N
   const size_t base_row = rows > 0 ? (size_t)n0 : 0;
   f16 sc[SCALED ? R : 1];
   if constexpr (SCALED) {
-    const __amdgpu_buffer_rsrc_t sb =
-        buffer_rsrc(pre_scales + base_row * pre_G, rows > 0 ? (size_t)rows * pre_G * 2 : 0);
+    const __amdgpu_buffer_rsrc_t sb = buffer_rsrc(scales + base_row * pre_G, rows > 0 ? (size_t)rows * pre_G * 2 : 0);
     const int gi = (slot * CPL) >> pre_shift;
 #pragma unroll
     for (int u = 0; u < R; ++u)
       sc[u] = __builtin_bit_cast(
           f16, __builtin_amdgcn_raw_buffer_load_b16(sb, live ? ((u * P + ro) * pre_G + gi) * 2 : kOutOfRange, 0, 0));
   }
-  u4 xv[XL];
-  {
-    const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(pre_x, (size_t)K * 2);
-#pragma unroll
-    for (int i = 0; i < XL; ++i)
-      xv[i] = __builtin_bit_cast(
-          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (slot * CPL + 8 * i) * 2 : kOutOfRange, 0, 0));
-  }
+  if constexpr (NP == 1) load_x();
   const int en = n0 + lane;  // the epilogue row of lane q < R P
   const size_t ebytes = (size_t)N * 2;
   const int eoff = lane < R * P && en < N ? en * 2 : kOutOfRange;
   f16 e_bias = (f16)0.0f, e_res = (f16)0.0f;
   if constexpr (EPI) {  // an absent operand is an empty buffer (reads zeros)
-    e_bias = __builtin_bit_cast(
-        f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? ebytes : 0), eoff, 0, 0));
+    e_bias = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(bias, bias ? ebytes : 0), eoff, 0, 0));
     e_res = __builtin_bit_cast(
-        f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.residual, p.residual ? ebytes : 0), eoff, 0, 0));
+        f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(residual, residual ? ebytes : 0), eoff, 0, 0));
   }
   const f16 e_scale =
       SCALED ? (f16)1.0f
-             : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pre_scales, ebytes), eoff, 0, 0));
+             : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(scales, ebytes), eoff, 0, 0));
   u4 w[R];
   {
-    const __amdgpu_buffer_rsrc_t wb =
-        buffer_rsrc(pre_codes + base_row * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
+    const __amdgpu_buffer_rsrc_t wb = buffer_rsrc(codes + base_row * row_bytes, rows > 0 ? (size_t)rows * row_bytes : 0);
 #pragma unroll
     for (int u = 0; u < R; ++u)  // rows u P .. u P + P - 1 of the wave, contiguous
       w[u] = __builtin_bit_cast(
@@ -334,9 +366,9 @@ __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const 
     for (int c = 0; c < (S >> lg); ++c) a += src[c];
     if constexpr (!SCALED) a *= (float)e_scale;
     f16 h = (f16)a;
-    if (EPI && p.bias) h = (f16)((float)h + (float)e_bias);
-    if (EPI && p.residual) h = (f16)((float)e_res + (float)h);
-    p.y[en] = h;
+    if (EPI && bias) h = (f16)((float)h + (float)e_bias);
+    if (EPI && residual) h = (f16)((float)e_res + (float)h);
+    y[en] = h;
   }
 }
 

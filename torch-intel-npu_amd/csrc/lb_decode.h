@@ -448,24 +448,18 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   __syncthreads();
 
   // ---- correction activations z = fp16(x . V^T), 8 threads per rank row ----
-  if constexpr (OWN_Z) {
-    float acc = 0.0f, acc2 = 0.0f;
+  if constexpr (OWN_Z) {  // v_dot2 chains, then the 8 threads' sums by DPP
+    float za = 0.0f, zb = 0.0f;
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       asm volatile("" : "+v"(vreg[i]));  // V is consumed here, after the barrier, not at its load
       const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
       const h8 xx = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        acc += (float)xx[e] * (float)vv[e];
-        acc2 += (float)xx[e + 1] * (float)vv[e + 1];
-      }
+      za = dot2(pair_of(xx, 0), pair_of(vv, 0), dot2(pair_of(xx, 2), pair_of(vv, 2), za));
+      zb = dot2(pair_of(xx, 1), pair_of(vv, 1), dot2(pair_of(xx, 3), pair_of(vv, 3), zb));
     }
-    acc += acc2;
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
-    acc += __shfl_xor(acc, 4, 64);
-    if (vpart == 0) zs[vr] = (float)(f16)acc;
+    za = sum8(za + zb);
+    if (vpart == 0) zs[vr] = (float)(f16)za;
   }
 
   // ---- the product on MFMA: every A row is the activation row, B = decoded weights ----

@@ -187,6 +187,7 @@ PACK_SHAPES = [
     ('int4', 576, 1536, 128),      # SmolLM down: one row per wave (48 lanes)
     ('int4', 1536, 576, 32),       # SmolLM gate / up with groups of one lane
     ('int4', 5, 992, 32),          # two rows per load, one partly filled wave
+    ('int4', 1000, 256, 64),       # eight rows per load, 125 waves
     ('int4', 16383, 576, 64),      # one row short of the four-load kernel
 ]
 

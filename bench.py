@@ -463,6 +463,8 @@ def main():
     ap.add_argument('--profile-gemm', action='store_true', help='prefill GEMMs alone (for rocprofv3 --pmc)')
     ap.add_argument('--profile-multirow', action='store_true',
                     help='multi-row GEMV paths and a split-K prefill GEMM alone (for rocprofv3 --kernel-trace)')
+    ap.add_argument('--profile-pass', action='store_true',
+                    help='only the config-2 M=1 pass in its decode launch groups (for rocprofv3 --kernel-trace)')
     ap.add_argument('--profile-llama', choices=[s[0] for s in LLAMA_SHAPES],
                     help='one config-5 INT4 g128 GEMV at M=1 (its default kernel) alone, then a copy, for rocprofv3')
     args = ap.parse_args()
@@ -490,6 +492,11 @@ def main():
         return
     if args.profile_multirow:
         profile_multirow(device, stream)
+        return
+    if args.profile_pass:
+        one = smol_pass(1, device, stream, args.steps, args.warmup, grouped=True)
+        del one['linears']
+        print(json.dumps(dict(config2_pass_m1=one)), flush=True)
         return
     if args.decode_only:
         decode = decode_leg(device, args.decode_steps, 0)

@@ -41,7 +41,7 @@ namespace lb {
 #define LB_GEMM4_SCHED_VALU 0  // VALU instructions after each MFMA (0: by block size, below)
 #endif
 #ifndef LB_GEMM4_SCHED_DSR
-#define LB_GEMM4_SCHED_DSR 1
+#define LB_GEMM4_SCHED_DSR 0  // LDS reads after each MFMA (0: 2 with eight or more waves, else 1)
 #endif
 #ifndef LB_GEMM_IGLP_VALU
 #define LB_GEMM_IGLP_VALU 4
@@ -266,8 +266,9 @@ __device__ __forceinline__ void static_for(F &&f) {
 // lds; the two stages are separate arrays so the compiler sees no alias with the stage being
 // read), issued at the start of the step and complete before its closing barrier; the packed
 // weights of the step after it are loaded into registers and decoded into the other B stage
-// between the MFMA groups.  Each MFMA of a substep is followed by a share of the other work (one
-// LDS read, up to 8 VALU, one LDS write, one global load: sched_group_barrier), so the MFMA pipe
+// between the MFMA groups.  Each MFMA of a substep is followed by a share of the other work (one or,
+// with eight waves, two LDS reads, up to 8 VALU, one LDS write, one global load:
+// sched_group_barrier), so the MFMA pipe
 // is fed while the decode and the transfers proceed.  Fragment reads of substep kk + 1 are issued
 // before the MFMAs of substep kk.  With split-K (p.splits > 1, grid z = split) a workgroup covers
 // k in [z * kslice, z * kslice + kslice) and writes fp32 sums to p.partial.
@@ -294,6 +295,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   // smaller blocks (fewer MFMAs per substep) take it in larger shares.
   constexpr int SCHED_VALU =
       LB_GEMM4_SCHED_VALU > 0 ? LB_GEMM4_SCHED_VALU : (TM * TN >= 8 ? (WAVES >= 8 ? 8 : 4) : 16);
+  // LDS reads placed after each MFMA: two with eight waves (1-4% on the 256-wide tiles), one with four.
+  constexpr int SCHED_DSR = LB_GEMM4_SCHED_DSR > 0 ? LB_GEMM4_SCHED_DSR : (WAVES >= 8 ? 2 : 1);
   static_assert((WAVES == 4 || WAVES == 8 || WAVES == 16) && WAVES % WM == 0 && TM >= 1 && TN >= 1 && B_PER >= 1 &&
                     A_PER >= 1 && BN * B_ROW_CHUNKS % NT == 0 && BM * (BK / 8) % NT == 0 && (CB == 16 || BITS == 4),
                 "tile constants");
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
 #pragma unroll
       for (int i = 0; i < TM * TN; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, LB_GEMM4_SCHED_DSR, 0);   // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x100, SCHED_DSR, 0);            // LDS reads
         __builtin_amdgcn_sched_group_barrier(0x002, SCHED_VALU, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // one LDS write
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // one global load

@@ -106,8 +106,11 @@ GemvShape gemv_shape_rows(int fmt, int64_t M, int64_t N, int64_t K) {
   const int64_t room = (int64_t)((kGemvRowsLds - 8 * 1024) / 2 / (M + 1)) - 4 * cpl - 8;  // 8 KB for scales
   const int64_t ks_max = std::max<int64_t>(kstep, room / kstep * kstep);
   gs.kg = 1;
+  // From 16 rows on, twice the workgroups (shorter K slices): M = 16 4096x14336 29.8 -> 26.1 us, while
+  // M = 8 keeps 512 (20.7 us against 24.6 with 1024).
+  const int64_t target = M >= 16 ? 2 * LB_GEMV_M_TARGET_WGS : LB_GEMV_M_TARGET_WGS;
   int64_t s = std::max<int64_t>((K + ks_max - 1) / ks_max,
-                                std::min<int64_t>((LB_GEMV_M_TARGET_WGS + wg_tiles - 1) / wg_tiles,
+                                std::min<int64_t>((target + wg_tiles - 1) / wg_tiles,
                                                   std::max<int64_t>(1, ksteps / 4)));
   const int64_t ks = round_up((K + s - 1) / s, kstep);
   gs.splits = (int)((K + ks - 1) / ks);

@@ -359,9 +359,15 @@ def decode_leg(device, steps, cpu_steps):
         stop.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(stop)
-        out.update(decode_steps=steps, tokens_per_graph=per_graph, decode_ms_per_token=round(ms / steps, 4),
-                   decode_tokens_per_s=round(steps * 1000.0 / ms, 1),
+        # A hand-over wait that gave up ends its launch early with stale words: such a run's time
+        # is not a decode rate, so it is reported as the failure it is, without tokens/s.
+        timeouts = decoder.timeouts()
+        out.update(decode_steps=steps, tokens_per_graph=per_graph, decode_timeouts=timeouts,
                    first_tokens=decoder.tokens[256:256 + 8].tolist())
+        if timeouts:
+            out['decode_error'] = f'{timeouts} hand-over wait(s) timed out: tokens/s not reported'
+        else:
+            out.update(decode_ms_per_token=round(ms / steps, 4), decode_tokens_per_s=round(steps * 1000.0 / ms, 1))
     if cpu_steps:
         from oracle import smollm_oracle as so
         packed = lambda l: {n: (q.format, q.shape, q.group_size, q.data, q.scales) for n, q in l._packed.items()}
@@ -427,6 +433,31 @@ def profile_gemm(device, stream):
                               flops_per_launch=2 * m * n * k)), flush=True)
 
 
+def profile_linears(device, specs, launches=16):
+    """Each `fmt:M:N:K:group` spec (group 0: per row) alone on its default dispatch, `launches`
+    launches over its replica pool, then a 256 MiB copy (the PMC calibration kernel); for
+    rocprofv3 --kernel-trace and --pmc FETCH_SIZE / WRITE_SIZE."""
+    for i, spec in enumerate(specs):
+        fmt, m, n, k, g = spec.split(':')
+        m, n, k, g = int(m), int(n), int(k), int(g)
+        g = g or k
+        wb = algorithmic_bytes(fmt, 0, n, k, g)
+        lin = Linear(make_weight(fmt, n, k, g, 900 + i), m, copies_for(wb, cap=16), device, 950 + i)
+        for r in range(launches):
+            lin.calls[r % len(lin.calls)].run()
+        torch.cuda.synchronize()
+        print(json.dumps(dict(profile='linear', fmt=fmt, M=m, N=n, K=k, group=g, launches=launches,
+                              algorithmic_bytes=lin.bytes, flops_per_launch=2 * m * n * k)), flush=True)
+        del lin
+        torch.cuda.empty_cache()
+    src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(profile='copy', copy_bytes=src.numel(), launches=4)), flush=True)
+
+
 MULTIROW_PROFILE_SHAPES = [('int4', 8, 4096, 4096, 128), ('int4', 16, 128256, 4096, 128),
                            ('int4', 32, 128256, 4096, 128), ('nf4', 512, 960, 2560, 64)]
 
@@ -465,6 +496,9 @@ def main():
                     help='multi-row GEMV paths and a split-K prefill GEMM alone (for rocprofv3 --kernel-trace)')
     ap.add_argument('--profile-pass', action='store_true',
                     help='only the config-2 M=1 pass in its decode launch groups (for rocprofv3 --kernel-trace)')
+    ap.add_argument('--profile-linear', nargs='+', metavar='FMT:M:N:K:GROUP',
+                    help='these linears alone on their default dispatch (group 0: per row), then a copy, '
+                         'for rocprofv3')
     ap.add_argument('--profile-llama', choices=[s[0] for s in LLAMA_SHAPES],
                     help='one config-5 INT4 g128 GEMV at M=1 (its default kernel) alone, then a copy, for rocprofv3')
     args = ap.parse_args()
@@ -489,6 +523,9 @@ def main():
         return
     if args.profile_llama:
         profile_kernel(device, stream, next(s for s in LLAMA_SHAPES if s[0] == args.profile_llama))
+        return
+    if args.profile_linear:
+        profile_linears(device, args.profile_linear)
         return
     if args.profile_multirow:
         profile_multirow(device, stream)

@@ -176,8 +176,13 @@ lb_status lb_decode_layer(const lb_decode_layer_args *args, void *stream);
  * The counterpart of the reference's per-token chain of layer graphs, submitted in fenced groups
  * (torch_npu_smollm.py:644-654, torch_intel_npu.py:560-570).  Every workgroup keeps its stage
  * through all layers and fetches the next layer's weights while earlier stages run; the grid must
- * be resident on the device all at once (lb_decode_stack returns LB_UNSUPPORTED where it is not).
- * All layers share shapes, format, group size and per-projection ranks.
+ * be resident on the device all at once (lb_decode_stack returns LB_UNSUPPORTED where the device
+ * cannot hold it).  That check is made once, from the kernel's occupancy on the stream's device,
+ * at lb_decode_stack_prepare: it cannot see kernels that other streams or processes run on the
+ * device at the same time, which can keep part of the grid waiting for compute units.  Its waits
+ * then time out (see lb_decode_check), so run the stack without concurrent kernels on the device
+ * and check the workspace after use.  All layers share shapes, format, group size and
+ * per-projection ranks.
  *
  * lb_decode_stack_prepare validates the arguments and writes the layer table (device addresses of
  * every layer's tensors) into `table`, synchronously on `stream`; it is a set-up call, made once
@@ -219,6 +224,38 @@ typedef struct lb_decode_stack_args {
 
 lb_status lb_decode_stack_prepare(const lb_decode_stack_args *args, void *stream);
 lb_status lb_decode_stack(const lb_decode_stack_args *args, void *stream);
+
+/*
+ * Forgets a table written by lb_decode_stack_prepare: a later lb_decode_stack with that table
+ * returns LB_INVALID_ARGUMENT until it is prepared again.  Call it before the table's memory is
+ * freed, so that a new table allocated at the same address is never taken for the old one.
+ * LB_INVALID_ARGUMENT if the table was not prepared.
+ */
+lb_status lb_decode_stack_release(const void *table);
+
+/*
+ * Hand-over health of the calls that use a workspace (lb_fused_linear and lb_decode_attention
+ * with a workspace, lb_decode_layer, lb_decode_stack).  Their workgroups hand data to later
+ * workgroups of the same launch through tagged words in the workspace, and every wait for such a
+ * word is bounded: a wait that gives up sets the workspace's timeout word and the launch goes on
+ * with the stale word, so its outputs (and those of every later call on the workspace) are not
+ * valid.  A wait gives up only when its producer never ran in time.  The producers are dispatched
+ * first and the stacked grid is checked to fit the device at lb_decode_stack_prepare, so this
+ * happens only when something else holds the compute units the grid needs -- kernels of other
+ * streams or processes running concurrently on the device -- or after a device problem.
+ *
+ * lb_decode_check synchronises `stream`, then reads the timeout word at byte `timeout_offset` of
+ * the workspace (LB_*_TIMEOUT_OFFSET below).  Zero: LB_OK.  Nonzero: the library enters its failed
+ * state, as after a launch error (every later call returns LB_DEVICE_FAILED, like the reference's
+ * failed context, npunlock-probe/torch-device/backend.cpp:280-292), and the call returns
+ * LB_DEVICE_FAILED.  *timeouts (may be NULL) receives the word.  Call it after the calls, or graph
+ * replays, whose outputs are about to be used.
+ */
+#define LB_FUSED_TIMEOUT_OFFSET 392u
+#define LB_ATTN_TIMEOUT_OFFSET(heads, capacity) (LB_ATTN_WORKSPACE_BYTES(heads, capacity) - 8u)
+#define LB_DECODE_TIMEOUT_OFFSET 8u /* lb_decode_layer and lb_decode_stack workspaces */
+
+lb_status lb_decode_check(const void *workspace, size_t timeout_offset, void *stream, uint32_t *timeouts);
 
 /*
  * Greedy step: t = first index of the largest logit (NaN logits are never chosen);

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LB_ABI_VERSION 4
+#define LB_ABI_VERSION 5
 
 typedef enum lb_status {
   LB_OK = 0,

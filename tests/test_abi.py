@@ -387,6 +387,25 @@ def test_noalloc_entry_refuses_workspace_and_oversized_calls():
     assert lib.lb_linear_noalloc(None, None) == lowbit_hip.INVALID_ARGUMENT
 
 
+def test_decode_check_and_release_argument_errors():
+    """lb_decode_check and lb_decode_stack_release reject bad arguments before any device call;
+    the timeout offsets match the header's workspace layouts."""
+    lib = lowbit_hip.library()
+    word = ctypes.c_uint32(7)
+    for ws, offset in ((None, 8), (0x10010, 8), (0x10000, 6)):
+        assert lib.lb_decode_check(ws, offset, None, ctypes.byref(word)) == lowbit_hip.INVALID_ARGUMENT
+        assert '256-byte aligned' in lib.lb_last_error().decode()
+        assert word.value == 0
+    assert lib.lb_decode_stack_release(0x10000) == lowbit_hip.INVALID_ARGUMENT
+    assert 'not prepared' in lib.lb_last_error().decode()
+    assert lib.lb_decode_stack_release(None) == lowbit_hip.INVALID_ARGUMENT
+    assert lowbit_hip.FUSED_TIMEOUT_OFFSET == 392 < lowbit_hip.FUSED_WORKSPACE_BYTES
+    assert lowbit_hip.DECODE_TIMEOUT_OFFSET == 8
+    assert lowbit_hip.attention_timeout_offset(9, 384) == 9 * 8 * 128 + 8
+    header = (HEADERS[0].parent / 'lowbit_decode_hip.h').read_text()
+    assert '#define LB_FUSED_TIMEOUT_OFFSET 392u' in header and '#define LB_DECODE_TIMEOUT_OFFSET 8u' in header
+
+
 def test_failed_state_refuses_every_enqueueing_entry():
     """After a reported device failure the library refuses work (reference backend.cpp:58-60,
     280-292).  Forced from the host in a child process: the state lasts until the process ends."""

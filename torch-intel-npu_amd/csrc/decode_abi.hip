@@ -1045,13 +1045,14 @@ extern "C" lb_status lb_decode_stack_prepare(const lb_decode_stack_args *a, void
   bool scaled, ranked;
   if (const lb_status st = check_stack(who, a, &p, &rows, &fmt, &scaled, &ranked); st != LB_OK) return st;
   // Residency: every workgroup of the stacked grid must be on the device at once.
+  // The device is the stream's (the current device for the null stream).
   int device = 0, cus = 0, per_cu = 0;
   const void *fn = layer_kernel<true>(fmt, scaled, ranked);
-  if (hipGetDevice(&device) != hipSuccess ||
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipStreamGetDevice(s, &device) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, layer_smem(p)) != hipSuccess)
     return fail(LB_DEVICE_FAILED, "%s: device query failed", who);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   if (hipMemcpyAsync(a->table, rows.data(), rows.size() * sizeof(LayerWeights), hipMemcpyHostToDevice, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess) {
     mark_failed("lb_decode_stack_prepare: table copy failed");
@@ -1082,4 +1083,39 @@ extern "C" lb_status lb_decode_stack(const lb_decode_stack_args *a, void *stream
   }
   return launch_layers(who, layer_kernel<true>(fmt, scaled, ranked), p, static_cast<const LayerWeights *>(a->table),
                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" lb_status lb_decode_stack_release(const void *table) {
+  std::lock_guard<std::mutex> lock(table_mutex());
+  if (!table || table_registry().erase(table) == 0)
+    return fail(LB_INVALID_ARGUMENT, "lb_decode_stack_release: the table was not prepared");
+  return ok();
+}
+
+extern "C" lb_status lb_decode_check(const void *workspace, size_t timeout_offset, void *stream, uint32_t *timeouts) {
+  const char *who = "lb_decode_check";
+  if (timeouts) *timeouts = 0;
+  if (const lb_status bad = refuse_if_failed(who); bad != LB_OK) return bad;
+  if (!workspace || !aligned(workspace, 256) || timeout_offset % 4 != 0)
+    return fail(LB_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned and the offset a multiple of 4", who);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t word = 0;
+  if (hipMemcpyAsync(&word, static_cast<const char *>(workspace) + timeout_offset, sizeof word, hipMemcpyDeviceToHost,
+                     s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    char reason[256];
+    snprintf(reason, sizeof reason, "%s: synchronisation failed: %s", who, hipGetErrorString(hipGetLastError()));
+    mark_failed(reason);
+    return fail(LB_DEVICE_FAILED, "%s", reason);
+  }
+  if (timeouts) *timeouts = word;
+  if (word != 0) {
+    mark_failed("a bounded hand-over wait of a decode launch gave up: the outputs of the calls on that workspace are "
+                "not valid");
+    return fail(LB_DEVICE_FAILED,
+                "%s: a bounded hand-over wait gave up (timeout word %u): outputs since are not valid; the library is "
+                "now failed",
+                who, word);
+  }
+  return ok();
 }

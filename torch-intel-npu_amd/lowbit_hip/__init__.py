@@ -16,7 +16,7 @@ import torch
 
 LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve().parent.parent / 'liblowbit_hip.so'))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM = 0x1, 0x2, 0x4, 0x20
@@ -25,7 +25,7 @@ EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
 DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_decode_layer',
-                  'lb_decode_stack_prepare', 'lb_decode_stack')
+                  'lb_decode_stack_prepare', 'lb_decode_stack', 'lb_decode_stack_release', 'lb_decode_check')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
 def attention_workspace_bytes(heads, capacity):
@@ -34,6 +34,13 @@ def attention_workspace_bytes(heads, capacity):
 
 
 FUSED_WORKSPACE_BYTES = 512  # LB_FUSED_WORKSPACE_BYTES: tagged z words [3][12] u64, launch count u64, timeout u32
+FUSED_TIMEOUT_OFFSET = 392   # LB_FUSED_TIMEOUT_OFFSET
+DECODE_TIMEOUT_OFFSET = 8    # LB_DECODE_TIMEOUT_OFFSET (lb_decode_layer / lb_decode_stack workspaces)
+
+
+def attention_timeout_offset(heads, capacity):
+    """LB_ATTN_TIMEOUT_OFFSET: the timeout word of a split-attention workspace."""
+    return attention_workspace_bytes(heads, capacity) - 8
 
 
 class LinearArgs(ctypes.Structure):
@@ -179,6 +186,11 @@ def library():
         for name in ('lb_decode_stack_prepare', 'lb_decode_stack'):
             getattr(lib, name).restype = ctypes.c_int
             getattr(lib, name).argtypes = [ctypes.POINTER(DecodeStackArgs), ctypes.c_void_p]
+        lib.lb_decode_stack_release.restype = ctypes.c_int
+        lib.lb_decode_stack_release.argtypes = [ctypes.c_void_p]
+        lib.lb_decode_check.restype = ctypes.c_int
+        lib.lb_decode_check.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                        ctypes.POINTER(ctypes.c_uint32)]
         lib.lb_argmax_next.restype = ctypes.c_int
         lib.lb_argmax_next.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -447,8 +459,25 @@ def _row(t, name, count, dtype=torch.float16):
     return t
 
 
+def check_workspace(workspace, timeout_offset, what='lb_decode_check', stream=None):
+    """lb_decode_check: synchronise the stream, then read the workspace's timeout word.  Nonzero
+    means a bounded hand-over wait of a call on it gave up, so its outputs are not valid: the
+    library enters its failed state (every later call raises) and this raises RuntimeError, as the
+    reference's failed context does (npunlock-probe/torch-device/backend.cpp:280-292)."""
+    handle = torch.cuda.current_stream(workspace.device).cuda_stream if stream is None else stream
+    word = ctypes.c_uint32(0)
+    status = library().lb_decode_check(_ptr(workspace), timeout_offset, ctypes.c_void_p(handle), ctypes.byref(word))
+    if status != OK:
+        _check(status, what)
+
+
 class _Prepared:
-    """A fixed call of one decode-step entry point; run() enqueues it on the current stream."""
+    """A fixed call of one decode-step entry point; run() enqueues it on the current stream.
+    Calls with a hand-over workspace (`workspace`, timeout word at `_timeout_offset`) are checked by
+    check() after a synchronisation."""
+
+    workspace = None
+    _timeout_offset = None
 
     def _bind(self, fn, what, args, device, keep):
         self.args, self._keep, self._device, self._what = args, keep, device, what
@@ -460,6 +489,12 @@ class _Prepared:
         status = self._fn(self._ref, ctypes.c_void_p(handle))
         if status != OK:
             _check(status, self._what)
+
+    def check(self, stream=None):
+        """Raise RuntimeError (and leave the library failed) if a bounded wait of any run() so far
+        gave up; synchronises the stream.  Calls without a workspace have no waits to check."""
+        if self.workspace is not None:
+            check_workspace(self.workspace, self._timeout_offset, f'{self._what} (workspace check)', stream)
 
 
 class PreparedFused(_Prepared):
@@ -512,6 +547,7 @@ class PreparedFused(_Prepared):
         if shared_z and any(pr.get('down') is not None for pr in problems):
             self.workspace = torch.zeros(FUSED_WORKSPACE_BYTES, dtype=torch.uint8, device=x.device)
             a.workspace, a.workspace_bytes = _ptr(self.workspace), FUSED_WORKSPACE_BYTES
+            self._timeout_offset = FUSED_TIMEOUT_OFFSET
             keep.append(self.workspace)
         self._bind('lb_fused_linear', 'lb_fused_linear', a, x.device, keep)
         self.outputs = [pr['y'] for pr in problems]
@@ -557,6 +593,7 @@ class PreparedAttention(_Prepared):
             size = attention_workspace_bytes(heads, capacity)
             self.workspace = torch.zeros(size, dtype=torch.uint8, device=q.device)
             a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+            self._timeout_offset = attention_timeout_offset(heads, capacity)
             keep.append(self.workspace)
         self._bind('lb_decode_attention', 'lb_decode_attention', a, q.device, keep)
         self.out = out
@@ -645,6 +682,7 @@ class PreparedLayer(_Prepared):
         size = layer_workspace_bytes(hidden, intermediate, kv_heads)
         self.workspace = torch.zeros(size, dtype=torch.uint8, device=h.device)
         a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+        self._timeout_offset = DECODE_TIMEOUT_OFFSET
         keep.append(self.workspace)
         self._bind('lb_decode_layer', 'lb_decode_layer', a, h.device, keep)
         self.out = h
@@ -695,11 +733,26 @@ class PreparedStack(_Prepared):
         size = stack_workspace_bytes(hidden, intermediate, kv_heads, len(layers))
         self.workspace = torch.zeros(size, dtype=torch.uint8, device=h.device)
         a.workspace, a.workspace_bytes = _ptr(self.workspace), size
+        self._timeout_offset = DECODE_TIMEOUT_OFFSET
         keep += [self.table, self.workspace]
         self._bind('lb_decode_stack', 'lb_decode_stack', a, h.device, keep)
         handle = torch.cuda.current_stream(h.device).cuda_stream
         _check(library().lb_decode_stack_prepare(self._ref, ctypes.c_void_p(handle)), 'lb_decode_stack_prepare')
+        self._prepared = True
         self.out = h
+
+    def release(self):
+        """Forget the prepared table (lb_decode_stack_release); run() then raises ValueError.  Done
+        by the garbage collector too, before the table's memory returns to the allocator."""
+        if getattr(self, '_prepared', False):
+            self._prepared = False
+            _check(library().lb_decode_stack_release(_ptr(self.table)), 'lb_decode_stack_release')
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:  # interpreter shutdown: the library may already be gone
+            pass
 
     def counters(self):
         """(workgroups counted over all calls so far, timeout word) of the workspace."""

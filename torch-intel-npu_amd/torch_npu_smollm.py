@@ -741,11 +741,24 @@ class GraphDecoder:
                                                 scale=0.125)])
         self._build_head(io)
 
+    def _waiting_calls(self):
+        """The calls that hand data between workgroups through a workspace (bounded waits)."""
+        import lowbit_hip as lb
+        for seq in self.calls:
+            for call in (seq.values() if isinstance(seq, dict) else seq):
+                if isinstance(call, lb._Prepared) and call.workspace is not None:
+                    yield call
+
     def timeouts(self):
-        """Timed-out waits recorded by the layer launches since construction (0 when healthy)."""
-        if not self.layer_kernel:
-            return 0
-        return sum(seq[0].counters()[1] for seq in self.calls)
+        """Timed-out waits recorded by the launches since construction (0 when healthy)."""
+        return sum(call.counters()[1] for call in self._waiting_calls())
+
+    def check(self):
+        """Synchronise, then raise RuntimeError if a bounded hand-over wait of any launch gave up
+        (its outputs, and so the tokens, are not valid); the library is then failed and refuses
+        every later call, as the reference's failed context (backend.cpp:280-292)."""
+        for call in self._waiting_calls():
+            call.check()
 
     # ---------------------------------------------------------------- staged launches
     def _build_staged(self, z):
@@ -877,4 +890,5 @@ class GraphDecoder:
         for _ in range(steps // self.graph_tokens):
             self.graph.replay()
         lowbit_hip.synchronize(self.device)  # a device fault of the replays marks the library failed here
+        self.check()  # and so does a hand-over wait that gave up
         return self.tokens[start:start + steps].tolist()

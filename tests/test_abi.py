@@ -242,7 +242,7 @@ W8 = dict(format=0, group_size=128, K=128, flags=lowbit_hip.FLAG_W8A8, activatio
 
 
 @pytest.mark.parametrize('over,status,needle', [
-    (dict(flags=0x40), lowbit_hip.INVALID_ARGUMENT, 'unknown flags'),
+    (dict(flags=0x80), lowbit_hip.INVALID_ARGUMENT, 'unknown flags'),
     # compact groups (reference QuantizedLinear: at most 32 groups, packed weights only)
     (dict(K=4096, ldx=4096, group_size=32, flags=lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.INVALID_ARGUMENT,
      'at most 32 groups'),
@@ -292,6 +292,32 @@ def test_force_stream_argument_errors(over, status, needle):
     got, _, message = workspace(args(**over))
     assert got == status, message
     assert needle in message
+
+
+@pytest.mark.parametrize('over,needle', [
+    (dict(K=4096 + 256, ldx=4352), 'LB_FLAG_FORCE_WIDE'),
+    (dict(K=4096, ldx=4096, group_size=32), 'LB_FLAG_FORCE_WIDE'),
+    (dict(K=4096, ldx=4096, format=2), 'LB_FLAG_FORCE_WIDE'),
+    (dict(K=4096, ldx=4096, M=33), 'LB_FLAG_FORCE_WIDE'),
+    (dict(K=4096, ldx=4096, rank=8, down=0x50000, up=0x60000, up_ld=8), 'LB_FLAG_FORCE_WIDE'),
+])
+def test_force_wide_argument_errors(over, needle):
+    status, _, message = workspace(args(flags=lowbit_hip.FLAG_FORCE_WIDE, x=0x1000000, y=0x2000000, scales=0x3000000,
+                                        codes=0x4000000, **over))
+    assert status == lowbit_hip.UNSUPPORTED and needle in message, message
+
+
+def test_force_wide_workspace_holds_the_slices():
+    """One K slice needs no workspace; several need their fp32 partials [slices, M, N]."""
+    far = dict(x=0x1000000, y=0x8000000, scales=0x10000000, codes=0x20000000)
+    status, size, _ = workspace(args(M=32, N=65536, K=4096, ldx=4096, ldy=65536, group_size=128,
+                                     flags=lowbit_hip.FLAG_FORCE_WIDE, **far))
+    assert status == 0 and size == 0
+    status, size, _ = workspace(args(M=32, N=4096, K=4096, ldx=4096, ldy=4096, group_size=128,
+                                     flags=lowbit_hip.FLAG_FORCE_WIDE, **far))
+    assert status == 0 and size == 8 * 32 * 4096 * 4   # 32 row blocks: 8 one-chunk slices
+    status, size, _ = workspace(args(M=24, N=14336, K=4096, ldx=4096, ldy=14336, group_size=128, **far))
+    assert status == 0 and size == 2 * 24 * 14336 * 4   # the default dispatch at 17..32 rows: 2 slices
 
 
 @pytest.mark.parametrize('over', [dict(), dict(group_size=64), dict(group_size=128), dict(K=4096, ldx=4096, group_size=4096),

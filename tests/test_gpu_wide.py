@@ -1,0 +1,124 @@
+"""GPU parity of the several-row GEMV on 32x32 MFMA tiles (wide_rows_kernel) against the CPU oracle.
+
+INT4 / INT8 calls of 17..32 rows over >= 4 MB of weights run there by default; the tests force it
+(LB_FLAG_FORCE_WIDE) on other shapes and row counts.  Every code is decoded to its exact integer q
+and a group's (or, for per-row INT8, the whole row's) integer sum is scaled in fp32, so its value
+is the exact x . (q s) product: the bars are those of every linear path, rel-L2 <= 1e-3 against
+the oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), and bit
+for bit on one-hot inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes
+cover one K slice and several (fp32 partials added in slice order), partial 32-row blocks, every
+group span (1, 2, 4, 8 loads per group, and per row), bias, and strided activation / output rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+import lowbit_hip
+from conftest import announce
+from oracle import lowbit_oracle as o
+from test_gpu_linear import check, problem, run, to_dev
+
+pytestmark = pytest.mark.gpu
+WIDE = lowbit_hip.FLAG_FORCE_WIDE
+
+# (fmt, N, K, group): K a multiple of the 512-code (INT4) / 256-code (INT8) chunk
+WIDE_SHAPES = [
+    ('int4', 300, 1024, 128),      # 3 blocks (the last partial), K split in 2
+    ('int4', 4096, 4096, 128),     # 32 blocks, split into 8 one-chunk slices
+    ('int4', 14336, 1024, 128),    # 112 blocks, 2 slices
+    ('int4', 28000, 512, 64),      # one load per group, one slice, a partial block
+    ('int4', 1000, 2048, 256),     # four loads per group
+    ('int4', 520, 1536, 512),      # eight loads per group, 3 chunks
+    ('int8', 4096, 4096, 4096),    # per-row int8, split
+    ('int8', 26000, 256, 256),     # per-row int8, one chunk, one slice, partial block
+    ('int8', 2048, 2048, 32),      # one load per group
+    ('int8', 1030, 1024, 64),      # two loads per group
+    ('int8', 777, 768, 256),       # eight loads per group
+]
+ROWS = [1, 2, 5, 16, 17, 31, 32]
+
+
+@pytest.mark.parametrize('m', ROWS)
+@pytest.mark.parametrize('spec', WIDE_SHAPES, ids=lambda s: '-'.join(map(str, s)))
+def test_wide_matches_oracle(device, spec, m):
+    fmt, n, k, group = spec
+    announce('wide', spec, m)
+    rng = np.random.default_rng(n + 7 * k + group + 1000 * m)
+    p = problem(rng, fmt, m, n, k, group)
+    check(p, run(p, device, WIDE), f'wide {spec} M={m}')
+
+
+@pytest.mark.parametrize('spec', [('int4', 4096, 4096, 128), ('int4', 20000, 1024, 128), ('int8', 2048, 2048, 2048)],
+                         ids=lambda s: '-'.join(map(str, s)))
+def test_wide_with_bias(device, spec):
+    fmt, n, k, group = spec
+    announce('wide bias', spec)
+    rng = np.random.default_rng(3 * n + k)
+    p = problem(rng, fmt, 24, n, k, group, bias=True)
+    check(p, run(p, device, WIDE), f'wide bias {spec}')
+
+
+def test_wide_strided_rows(device):
+    """x and y as views with row strides beyond K and N (q|k|v-style slices); the rest of each
+    output row is untouched."""
+    announce('wide strided')
+    rng = np.random.default_rng(11)
+    m, n, k, group = 20, 2000, 2048, 128
+    p = problem(rng, 'int4', m, n, k, group)
+    xb = to_dev(np.zeros((m, k + 40), np.float16), device)
+    xb[:, 8:8 + k] = to_dev(p['x'], device)
+    yb = torch.full((m, n + 24), 7.0, dtype=torch.float16, device=device)
+    codes = to_dev(np.frombuffer(p['data'], np.uint8), device)
+    scales = to_dev(np.frombuffer(p['scales'], np.float16), device)
+    lowbit_hip.linear(xb[:, 8:8 + k], codes, scales, format='int4', N=n, K=k, group_size=group, flags=WIDE,
+                      out=yb[:, 16:16 + n])
+    torch.cuda.synchronize()
+    got = yb.cpu().numpy()
+    check(p, got[:, 16:16 + n], 'wide strided')
+    assert (got[:, :16] == 7.0).all() and (got[:, 16 + n:] == 7.0).all()
+
+
+@pytest.mark.parametrize('fmt,group,n,k', [('int4', 128, 4096, 4096), ('int4', 64, 1024, 1024),
+                                           ('int8', 4096, 2048, 4096), ('int8', 32, 1000, 512)])
+def test_wide_identity_is_bit_exact(device, fmt, group, n, k):
+    """One-hot activation rows and power-of-two scales: row i of y is the dequantized column of its
+    hot index, bit for bit, in every K slice and row position."""
+    announce('wide identity', fmt, group, n, k)
+    rng = np.random.default_rng(group + n)
+    codes = rng.integers(0, 16, n * k).astype(np.uint8) if fmt == 'int4' else rng.integers(-128, 128, n * k)
+    data = o.pack(codes) if fmt == 'int4' else codes.astype(np.int8).tobytes()
+    g = k // group
+    scales = (2.0 ** rng.integers(-12, 3, n * g)).astype(np.float16)
+    w = o.dequantize(fmt, (n, k), group, data, scales.tobytes())
+    cols = [0, 1, 31, 32, 33, 127, 128, 255, 256, k // 2 + 5, k - 129, k - 1]
+    x = np.zeros((32, k), np.float16)
+    for i in range(32):
+        x[i, cols[i % len(cols)]] = 1.0
+    y = lowbit_hip.linear(to_dev(x, device), to_dev(np.frombuffer(data, np.uint8), device), to_dev(scales, device),
+                          format=fmt, N=n, K=k, group_size=group, flags=WIDE)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for i in range(32):
+        np.testing.assert_array_equal(got[i], w[:, cols[i % len(cols)]], err_msg=f'row {i}')
+
+
+def test_wide_is_the_default_for_17_to_32_rows(device):
+    """14336x4096 INT4 g128 at M = 24 (config-5 shape): the default dispatch gives the forced
+    kernel's result bit for bit, and the oracle's values."""
+    announce('wide default dispatch')
+    rng = np.random.default_rng(5)
+    p = problem(rng, 'int4', 24, 14336, 4096, 128)
+    default = run(p, device)
+    np.testing.assert_array_equal(default, run(p, device, WIDE))
+    check(p, default, 'wide default')
+
+
+@pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=32), dict(fmt='nf4'), dict(M=33)])
+def test_wide_refuses_shapes_it_does_not_take(device, over):
+    announce('wide refuses', over)
+    fmt, m, n, k, group = over.get('fmt', 'int4'), over.get('M', 4), 256, over.get('K', 4096), over.get('group', 128)
+    x = torch.zeros(m, k, dtype=torch.float16, device=device)
+    codes = torch.zeros(n * k // 2, dtype=torch.uint8, device=device)
+    scales = torch.ones(n * (k // group), dtype=torch.float16, device=device)
+    with pytest.raises(RuntimeError, match='LB_FLAG_FORCE_WIDE'):
+        lowbit_hip.linear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, flags=WIDE)

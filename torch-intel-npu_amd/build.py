@@ -12,10 +12,10 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / 'csrc'
 LIBRARY = HERE / 'liblowbit_hip.so'
-SOURCES = [CSRC / 'lowbit_abi.hip', CSRC / 'decode_abi.hip']
+SOURCES = [CSRC / 'lowbit_abi.hip', CSRC / 'decode_abi.hip', CSRC / 'wide_abi.hip']
 HEADERS = [CSRC / 'lb_common.h', CSRC / 'lb_kernels.h', CSRC / 'lb_decode.h', CSRC / 'abi_util.h',
            CSRC / 'lb_gemm.h', CSRC / 'lb_variants.h', CSRC / 'fused_launch.h', CSRC / 'lb_stream.h', CSRC / 'lb_layer.h',
-           CSRC / 'lb_line.h',
+           CSRC / 'lb_line.h', CSRC / 'lb_wide.h',
            HERE.parent / 'include' / 'lowbit_hip.h', HERE.parent / 'include' / 'lowbit_decode_hip.h']
 ARCH = 'gfx950'
 

@@ -1,0 +1,276 @@
+// gfx950 several-row GEMV for 2 .. 32 activation rows over INT4 / INT8 weights:
+// y[M, N] = x[M, K] . (q * s)[N, K]^T with every weight code decoded once per launch.
+//
+// The product runs on v_mfma_f32_32x32x16_f16 with the activation rows as the A operand (32 rows:
+// rows past M read a zero row, so M <= 32 costs one MFMA tile) and the decoded weights as the B
+// operand (32 weight rows per wave).  A wave owns 32 consecutive weight rows; lane (col, half)
+// holds weight row col and reads, per 16-byte load, the half-th 16 bytes of each 32-byte piece of
+// the row, so one wave-wide load covers 32 rows x 32 bytes and four consecutive loads a 128-byte
+// "position" of every row (256 INT4 / 128 INT8 codes).
+//
+// Decode to the exact integer q as fp16, without a scale: the nibble / byte sits under a magic
+// exponent and one subtraction removes the bias (every value involved is a small integer, so the
+// fp16 arithmetic is exact):
+//   INT4 even codes  0x6400 | (c ^ 8)         = 1024 + (c ^ 8)  - 1032 = q
+//   INT4 odd codes   0x5400 | ((c ^ 8) << 4)  =   64 + (c ^ 8)  -   72 = q   (decoded where it sits)
+//   INT8             0x6400 | (b ^ 0x80)      = 1024 + (b ^ 0x80) - 1152 = b
+// Eight codes become the MFMA's eight k slots in the order (0,4,1,5,2,6,3,7) (INT4) or
+// (0,2,1,3,4,6,5,7) (INT8); the activations are staged in LDS with the same permutation of every
+// 8-element block, so both operands agree on k.
+//
+// Scales: a group's integer sums accumulate in their own MFMA accumulator (a group is one or more
+// whole loads: 64+ INT4 / 32+ INT8 codes), then acc += s * group_sum in fp32 -- the exact
+// x . (q * s) product up to fp32 rounding, whose distance to the reference's fp16(q * s) weights
+// the reference's rounding-budget gate bounds (torch_npu_lowbit_demo.py:97-106), as for the other
+// exact-q kernels.  Per-row INT8 accumulates all of K and multiplies once (the reference's W8
+// value, torch_npu_smollm.py:153-157).
+//
+// Workgroups of four waves own 128 weight rows and one K slice (grid y), walked in chunks of PC
+// positions: the chunk's activations of all M rows are staged once per workgroup in one of two
+// LDS stages and serve the four waves; the next chunk's weights (registers) and activations are
+// loaded while the current one is computed, one barrier per chunk.  With one slice the workgroup
+// writes y; with several it writes fp32 partial sums [slice, M, N] that splitk_reduce_kernel adds
+// in slice order.
+#pragma once
+#include "lb_common.h"
+
+namespace lb {
+
+struct WideParams {
+  const f16 *x;           // [M, ldx]
+  const uint8_t *codes;   // [N, K * bits / 8]
+  const f16 *scales;      // [N, G]
+  f16 *y;                 // [M, ldy] (one slice)
+  float *partial;         // [slices, M, N] (several slices)
+  const f16 *bias;        // [N] or null (one slice)
+  int M, N, K, G, group_shift;
+  int ldx, ldy;
+  int kslice;             // codes per slice, a multiple of the chunk
+  int per_row;            // INT8 with one scale per row: the scale multiplies the whole sum
+};
+
+template <int FMT> struct WideTraits;
+template <> struct WideTraits<FMT_INT4> { static constexpr int CPL = 32, BITS = 4; };
+template <> struct WideTraits<FMT_INT8> { static constexpr int CPL = 16, BITS = 8; };
+
+constexpr int kWideWaves = 4;
+constexpr int kWideRows = 32 * kWideWaves;  // weight rows per workgroup
+constexpr int kWideLoads = 4;               // 16-byte loads per lane per position (128 bytes of a row)
+
+template <int FMT> constexpr int wide_position() { return kWideLoads * 2 * WideTraits<FMT>::CPL; }
+
+// B operand of one 32x32x16 MFMA: the exact codes q of 8 k slots from the 16-byte load w (INT4:
+// dword t; INT8: dwords 2t, 2t + 1).
+template <int FMT>
+__device__ __forceinline__ h8 wide_decode(const u4 &w, int t) {
+  uint32_t r[4];
+  h2 bias_even, bias_odd;
+  if constexpr (FMT == FMT_INT4) {
+    const uint32_t a = w[t] ^ 0x88888888u, b = a >> 8;
+    r[0] = (a & 0x000F000Fu) | 0x64006400u;  // c0, c4: 1024 + c'
+    r[1] = (a & 0x00F000F0u) | 0x54005400u;  // c1, c5:   64 + c'
+    r[2] = (b & 0x000F000Fu) | 0x64006400u;  // c2, c6
+    r[3] = (b & 0x00F000F0u) | 0x54005400u;  // c3, c7
+    bias_even = h2{(f16)-1032.0f, (f16)-1032.0f};
+    bias_odd = h2{(f16)-72.0f, (f16)-72.0f};
+  } else {
+    const uint32_t a = w[2 * t] ^ 0x80808080u, b = w[2 * t + 1] ^ 0x80808080u;
+    r[0] = (a & 0x00FF00FFu) | 0x64006400u;         // b0, b2: 1024 + b'
+    r[1] = ((a >> 8) & 0x00FF00FFu) | 0x64006400u;  // b1, b3
+    r[2] = (b & 0x00FF00FFu) | 0x64006400u;         // b4, b6
+    r[3] = ((b >> 8) & 0x00FF00FFu) | 0x64006400u;  // b5, b7
+    bias_even = bias_odd = h2{(f16)-1152.0f, (f16)-1152.0f};
+  }
+  const h2 p0 = as_h2(r[0]) + bias_even, p1 = as_h2(r[1]) + bias_odd;
+  const h2 p2 = as_h2(r[2]) + bias_even, p3 = as_h2(r[3]) + bias_odd;
+  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Activation block permutation matching wide_decode: slot e holds element perm[e].
+template <int FMT>
+__device__ __forceinline__ h8 wide_permute(h8 v) {
+  if constexpr (FMT == FMT_INT4) return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
+  else return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
+}
+
+// GL: loads per scale group (1, 2, 4, ... ; 0 for per-row INT8).  PC: positions per chunk.
+template <int FMT, int GL, int PC>
+__global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p) {
+  constexpr int CPL = WideTraits<FMT>::CPL, BITS = WideTraits<FMT>::BITS;
+  constexpr int POS = wide_position<FMT>();  // codes per position
+  constexpr int KC = PC * POS;                // codes per chunk
+  constexpr int NL = PC * kWideLoads;         // loads per lane per chunk
+  constexpr int T8 = CPL / 8;                 // MFMAs per load
+  constexpr int LD = KC + 8;                  // staged row stride in halves (+16 bytes: rows spread over banks)
+  constexpr int NT = 64 * kWideWaves;
+  constexpr int XPIECES = 32 * KC / 8;        // 16-byte activation pieces of a chunk (32 rows)
+  constexpr int XP = (XPIECES + NT - 1) / NT; // per thread
+  constexpr bool GROUPED = GL > 0;
+  constexpr int GPC = GROUPED ? NL / GL : 1;  // scale groups per chunk
+  constexpr int kOutOfRange = (int)0x80000000u;
+  static_assert(!GROUPED || (NL % GL == 0), "a chunk holds whole groups");
+  __shared__ __align__(16) f16 xs[2 * 32 * LD + LD];  // two stages, then a zero row
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int row0 = blockIdx.x * kWideRows + wave * 32;  // this wave's first weight row
+  const int rows = __builtin_amdgcn_readfirstlane(max(0, min(32, p.N - row0)));  // scalar: the descriptors stay uniform
+  const int kbeg = blockIdx.y * p.kslice;
+  const int chunks = min(p.kslice, p.K - kbeg) / KC;
+  const int row_bytes = p.K * BITS / 8;
+  const __amdgpu_buffer_rsrc_t wb =
+      buffer_rsrc(p.codes + (size_t)(rows > 0 ? row0 : 0) * row_bytes, (size_t)rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t sb =
+      buffer_rsrc(p.scales + (size_t)(rows > 0 ? row0 : 0) * p.G, GROUPED ? (size_t)rows * p.G * 2 : 0);
+  // Lane's byte offset of load l of a chunk at k: row col, piece 32 * l + 16 * half of the chunk.
+  const int lane_off = col * row_bytes + 16 * half;
+
+  struct Buf {
+    u4 w[NL];
+    uint32_t s[GPC];
+  };
+  auto issue = [&](Buf &b, int c) {
+    const int kb = (kbeg + c * KC) * BITS / 8;
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+      b.w[l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, lane_off + kb + 32 * l, 0, 0));
+    if constexpr (GROUPED) {
+      const int g0 = (kbeg + c * KC) >> p.group_shift;
+#pragma unroll
+      for (int q = 0; q < GPC; ++q)
+        b.s[q] = __builtin_amdgcn_raw_buffer_load_b16(sb, (col * p.G + g0 + q) * 2, 0, 0);
+    }
+  };
+  // Activation pieces of chunk c: piece i = (row m, 8-element block); rows past M are not staged.
+  const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(p.x, ((size_t)(p.M - 1) * p.ldx + p.K) * 2);
+  auto load_x = [&](u4 (&xv)[XP], int c) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int idx = i * NT + t;
+      const int m = idx / (KC / 8), blk = idx % (KC / 8);
+      const bool live = idx < XPIECES && m < p.M;
+      xv[i] = __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (m * p.ldx + kbeg + c * KC + 8 * blk) * 2 : kOutOfRange,
+                                                    0, 0));
+    }
+  };
+  auto store_x = [&](const u4 (&xv)[XP], int st) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int idx = i * NT + t;
+      const int m = idx / (KC / 8), blk = idx % (KC / 8);
+      if (idx < XPIECES && m < p.M)
+        *reinterpret_cast<h8 *>(xs + st * 32 * LD + m * LD + 8 * blk) = wide_permute<FMT>(__builtin_bit_cast(h8, xv[i]));
+    }
+  };
+
+  Buf buf[2];
+  u4 xv[XP];
+  if (chunks > 0) {
+    issue(buf[0], 0);
+    load_x(xv, 0);
+  }
+  for (int i = t; i < LD / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * LD + 8 * i) = h8{};
+  if (chunks > 0) store_x(xv, 0);
+  __syncthreads();
+
+  // A operand of lane (col, half): activation row col (or the zero row), k piece half.
+  const bool arow = col < p.M;
+  const int a_base = (arow ? col * LD : 2 * 32 * LD) + half * CPL;
+  f16x acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+  auto step = [&](auto stage) {
+    constexpr int ST = decltype(stage)::value;
+    Buf &b = buf[ST];
+    const f16 *xa = xs + a_base + (arow ? ST * 32 * LD : 0);
+    f16x part;
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      asm volatile("" : "+v"(b.w[l]));  // decode here, not at the load
+#pragma unroll
+      for (int q = 0; q < T8; ++q) {
+        const h8 bw = wide_decode<FMT>(b.w[l], q);
+        const h8 xa8 = *reinterpret_cast<const h8 *>(xa + 2 * CPL * l + 8 * q);
+        if constexpr (GROUPED) {
+          if (l % GL == 0 && q == 0) {
+            f16x zero;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+            part = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, zero, 0, 0, 0);
+          } else {
+            part = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, part, 0, 0, 0);
+          }
+        } else {
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, acc, 0, 0, 0);
+        }
+      }
+      if constexpr (GROUPED) {
+        if (l % GL == GL - 1) {
+          const float s = (float)__builtin_bit_cast(f16, (unsigned short)b.s[l / GL]);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, part[r], acc[r]);
+        }
+      }
+    }
+  };
+  // Chunk c uses stage c % 2; chunk c + 1 is loaded meanwhile and stored into the other stage.
+  for (int c = 0; c < chunks; c += 2) {
+    if (c + 1 < chunks) {
+      issue(buf[1], c + 1);
+      load_x(xv, c + 1);
+    }
+    step(std::integral_constant<int, 0>{});
+    if (c + 1 < chunks) store_x(xv, 1);
+    __syncthreads();
+    if (c + 1 >= chunks) break;
+    if (c + 2 < chunks) {
+      issue(buf[0], c + 2);
+      load_x(xv, c + 2);
+    }
+    step(std::integral_constant<int, 1>{});
+    if (c + 2 < chunks) store_x(xv, 0);
+    __syncthreads();
+  }
+
+  // Lane (col, half) holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col.
+  const int n = row0 + col;
+  if (col >= rows) return;
+  if (gridDim.y > 1) {
+    float *part = p.partial + (size_t)blockIdx.y * p.M * p.N + n;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+      if (m < p.M) part[(size_t)m * p.N] = acc[r];
+    }
+    return;
+  }
+  const float rs = p.per_row ? (float)p.scales[n] : 1.0f;
+  const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+    if (m >= p.M) continue;
+    f16 h = (f16)(p.per_row ? acc[r] * rs : acc[r]);
+    if (p.bias) h = (f16)((float)h + bias);
+    p.y[(size_t)m * p.ldy + n] = h;
+  }
+}
+
+}  // namespace lb
+
+namespace lb {
+
+// Positions per chunk of the launched kernels.
+constexpr int kWidePC = 2;
+template <int FMT> constexpr int wide_chunk() { return kWidePC * wide_position<FMT>(); }
+inline int wide_chunk_codes(int fmt) { return fmt == FMT_INT4 ? wide_chunk<FMT_INT4>() : wide_chunk<FMT_INT8>(); }
+
+// Launches wide_rows_kernel over ceil(N / 128) x `slices` workgroups; gl: loads per scale group
+// (0: per-row INT8).  Defined in wide_abi.hip.
+void launch_wide(const WideParams &p, int format, int gl, int slices, hipStream_t stream);
+
+}  // namespace lb

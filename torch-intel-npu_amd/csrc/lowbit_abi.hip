@@ -16,6 +16,7 @@
 #include "lb_gemm.h"
 #include "lb_kernels.h"
 #include "lb_variants.h"
+#include "lb_wide.h"
 
 using namespace lb;
 using namespace lb::abi;
@@ -25,7 +26,7 @@ namespace {
 #ifndef LB_GEMM_FROM_M
 #define LB_GEMM_FROM_M 17  // from this many rows, calls with K >= N that no streaming GEMV takes run
 #endif                     // on the split-K GEMM (measured faster there up to 32 rows; K < N stays on gemv_kernel)
-enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4, PATH_TILE = 5 };
+enum Path { PATH_GEMV = 0, PATH_GEMM = 1, PATH_GENERIC = 2, PATH_ROW = 3, PATH_STREAM = 4, PATH_TILE = 5, PATH_WIDE = 6 };
 enum Variant { VAR_PLAIN = 0, VAR_COMPACT = 1, VAR_W8A8 = 2 };
 constexpr int kCompactMaxGroups = 32;
 constexpr int64_t kW8A8MaxK = 131072;  // |sum| <= K * 128 * 127 stays inside int32
@@ -323,6 +324,57 @@ bool tile_rows_eligible(const lb_linear_args *a) {
   return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
 }
 
+#ifndef LB_WIDE_MIN_M
+#define LB_WIDE_MIN_M 17  // wide_rows_kernel from this many activation rows (up to 32)
+#endif
+#ifndef LB_WIDE_MIN_BYTES
+#define LB_WIDE_MIN_BYTES (4ll << 20)  // ... over weights of at least this many bytes
+#endif
+#ifndef LB_WIDE_TARGET_WGS
+#define LB_WIDE_TARGET_WGS 200  // K slices: the fewest that give this many workgroups
+#endif
+#ifndef LB_WIDE_MAX_SLICES
+#define LB_WIDE_MAX_SLICES 16
+#endif
+
+// Loads per scale group of wide_rows_kernel (0: per-row INT8), or -1 where its groups do not fit:
+// a group is whole 32-byte pieces of a row (INT4 >= 64 codes, INT8 >= 32) and a chunk whole groups.
+int wide_group_loads(int fmt, int64_t K, int64_t group) {
+  if (fmt == FMT_INT8 && group == K) return 0;
+  const int bits = fmt == FMT_INT8 ? 8 : 4;
+  if (!is_pow2(group) || group * bits / 8 < 32 || wide_chunk_codes(fmt) % group != 0) return -1;
+  return (int)(group * bits / 8 / 32);
+}
+
+// Whether wide_rows_kernel takes the shape (force flag: this only; the default dispatch adds the
+// row count and weight size it is chosen for).
+bool wide_shape_ok(const lb_linear_args *a) {
+  const int fmt = (int)a->format;
+  if ((fmt != FMT_INT4 && fmt != FMT_INT8) || a->rank > 0 || a->M < 1 || a->M > 32) return false;
+  if (a->K % wide_chunk_codes(fmt) != 0 || a->K > 65536) return false;
+  if (wide_group_loads(fmt, a->K, a->group_size) < 0) return false;
+  return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
+}
+
+bool wide_eligible(const lb_linear_args *a) {
+  if (a->M < LB_WIDE_MIN_M || !wide_shape_ok(a)) return false;
+  const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
+  return bytes >= LB_WIDE_MIN_BYTES;
+}
+
+// K slices of wide_rows_kernel: the fewest dividing the chunk count that give LB_WIDE_TARGET_WGS
+// workgroups (row blocks of 128 rows x slices), at most LB_WIDE_MAX_SLICES.
+int wide_slices(int fmt, int64_t N, int64_t K) {
+  const int64_t blocks = (N + kWideRows - 1) / kWideRows, chunks = K / wide_chunk_codes(fmt);
+  int best = 1;
+  for (int s = 1; s <= LB_WIDE_MAX_SLICES && s <= chunks; ++s) {
+    if (chunks % s) continue;
+    best = s;
+    if (blocks * s >= LB_WIDE_TARGET_WGS) break;
+  }
+  return best;
+}
+
 // Workspace and kernel path of the compact_groups and W8A8 variants.
 Plan make_variant_plan(const lb_linear_args *a, int variant) {
   Plan pl;
@@ -364,10 +416,14 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
   const int fmt = (int)a->format;
   if (a->flags & LB_FLAG_FORCE_STREAM) {  // validated: the stream kernel takes the shape
     pl.path = a->M == 1 ? PATH_ROW : PATH_STREAM;
+  } else if (a->flags & LB_FLAG_FORCE_WIDE) {  // validated: the wide kernel takes the shape
+    pl.path = PATH_WIDE;
   } else if ((a->flags & LB_FLAG_FORCE_GENERIC) || !eligible) {
     pl.path = PATH_GENERIC;
   } else if (a->flags & LB_FLAG_FORCE_GEMM) {
     pl.path = PATH_GEMM;
+  } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && wide_eligible(a)) {
+    pl.path = PATH_WIDE;
   } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && row_eligible(a)) {
     pl.path = PATH_ROW;
   } else if (!(a->flags & LB_FLAG_FORCE_GEMV) && stream_rows_eligible(a)) {
@@ -394,6 +450,15 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     const GemmShape gs = gemm_shape(a->M, a->N, a->K, 1, true);
     pl.splits = gs.splits;
     pl.kslice = gs.kslice;
+    if (pl.splits > 1) {
+      pl.part_off = off;
+      pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
+      off = round_up(off + pl.part_bytes, 256);
+    }
+  }
+  if (pl.path == PATH_WIDE) {
+    pl.splits = wide_slices(fmt, a->N, a->K);
+    pl.kslice = (int)(a->K / pl.splits);
     if (pl.splits > 1) {
       pl.part_off = off;
       pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
@@ -464,7 +529,8 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
     if (overlaps(inputs[6], inputs[i]))
       return fail(LB_INVALID_ARGUMENT, "lb_linear: workspace overlaps %s", inputs[i].name);
 
-  constexpr uint32_t kForce = LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_FORCE_STREAM;
+  constexpr uint32_t kForce =
+      LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_FORCE_STREAM | LB_FLAG_FORCE_WIDE;
   if (a->flags & ~(kForce | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8))
     return fail(LB_INVALID_ARGUMENT, "lb_linear: unknown flags 0x%x", a->flags);
   if ((a->flags & LB_FLAG_FORCE_GEMV) && a->M > kGemvMaxM)
@@ -481,6 +547,12 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
                   "codes/x rows, and M == 1 or 17 <= M <= 32 with K <= 16384 (a multiple of 32 / 16) and groups "
                   "spanning whole 128 / 64-code pieces, or 2 <= M <= 16 with K <= 4096 and longer groups as M grows");
   }
+  if ((a->flags & LB_FLAG_FORCE_WIDE) && ((a->flags & (LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8)) || !wide_shape_ok(a)))
+    return fail(LB_UNSUPPORTED,
+                "lb_linear: LB_FLAG_FORCE_WIDE needs int4/int8 codes, no correction or variant, M <= 32, 16-byte "
+                "aligned codes/x rows, K a multiple of %d (int4) / %d (int8) up to 65536, and per-row int8 or "
+                "power-of-two groups of at least 64 (int4) / 32 (int8) codes dividing that",
+                wide_chunk_codes(FMT_INT4), wide_chunk_codes(FMT_INT8));
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {
     // reference _activation_scale (torch_npu_lowbit.py:155-166)
@@ -842,6 +914,33 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     }
     for (FusedProblem &r : fp.prob) r.tiles_end = tiles;
     launch_fused(fp, fmt, scaled, a->rank > 0, tiles, s);
+    return launch_status("lb_linear");
+  }
+  if (plan.path == PATH_WIDE) {
+    WideParams wp{};
+    wp.x = p.x;
+    wp.codes = p.codes;
+    wp.scales = p.scales;
+    wp.y = p.y;
+    wp.bias = p.bias;
+    wp.M = p.M;
+    wp.N = p.N;
+    wp.K = p.K;
+    wp.G = p.G;
+    wp.group_shift = p.group_shift;
+    wp.ldx = p.ldx;
+    wp.ldy = p.ldy;
+    wp.kslice = plan.kslice;
+    wp.per_row = p.per_row;
+    wp.partial = plan.splits > 1 ? reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) + plan.part_off)
+                                 : nullptr;
+    launch_wide(wp, fmt, wide_group_loads(fmt, a->K, a->group_size), plan.splits, s);
+    if (plan.splits > 1) {  // partials [slice, M, N] -> y in slice order (per-row scale, bias)
+      p.partial = wp.partial;
+      p.splits = plan.splits;
+      const size_t count = (size_t)p.M * p.N;
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p);
+    }
     return launch_status("lb_linear");
   }
   if (plan.path == PATH_STREAM || plan.path == PATH_TILE) {

@@ -19,7 +19,7 @@ LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve(
 ABI_VERSION = 5
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
-FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM = 0x1, 0x2, 0x4, 0x20
+FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM, FLAG_FORCE_WIDE = 0x1, 0x2, 0x4, 0x20, 0x40
 FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')

@@ -296,7 +296,7 @@ def test_force_stream_argument_errors(over, status, needle):
 
 @pytest.mark.parametrize('over,needle', [
     (dict(K=4096 + 256, ldx=4352), 'LB_FLAG_FORCE_WIDE'),
-    (dict(K=4096, ldx=4096, group_size=32), 'LB_FLAG_FORCE_WIDE'),
+    (dict(K=4096, ldx=4096, group_size=64), 'LB_FLAG_FORCE_WIDE'),
     (dict(K=4096, ldx=4096, format=2), 'LB_FLAG_FORCE_WIDE'),
     (dict(K=4096, ldx=4096, M=33), 'LB_FLAG_FORCE_WIDE'),
     (dict(K=4096, ldx=4096, rank=8, down=0x50000, up=0x60000, up_ld=8), 'LB_FLAG_FORCE_WIDE'),

@@ -7,7 +7,7 @@ is the exact x . (q s) product: the bars are those of every linear path, rel-L2 
 the oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), and bit
 for bit on one-hot inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes
 cover one K slice and several (fp32 partials added in slice order), partial 32-row blocks, every
-group span (1, 2, 4, 8 loads per group, and per row), bias, and strided activation / output rows.
+group span (2, 4, 8 loads per group, and per row), bias, and strided activation / output rows.
 """
 import numpy as np
 import pytest
@@ -26,12 +26,12 @@ WIDE_SHAPES = [
     ('int4', 300, 1024, 128),      # 3 blocks (the last partial), K split in 2
     ('int4', 4096, 4096, 128),     # 32 blocks, split into 8 one-chunk slices
     ('int4', 14336, 1024, 128),    # 112 blocks, 2 slices
-    ('int4', 28000, 512, 64),      # one load per group, one slice, a partial block
+    ('int4', 28000, 512, 128),     # one chunk, one slice, a partial block
     ('int4', 1000, 2048, 256),     # four loads per group
     ('int4', 520, 1536, 512),      # eight loads per group, 3 chunks
     ('int8', 4096, 4096, 4096),    # per-row int8, split
     ('int8', 26000, 256, 256),     # per-row int8, one chunk, one slice, partial block
-    ('int8', 2048, 2048, 32),      # one load per group
+    ('int8', 2048, 2048, 128),     # four loads per group
     ('int8', 1030, 1024, 64),      # two loads per group
     ('int8', 777, 768, 256),       # eight loads per group
 ]
@@ -78,8 +78,8 @@ def test_wide_strided_rows(device):
     assert (got[:, :16] == 7.0).all() and (got[:, 16 + n:] == 7.0).all()
 
 
-@pytest.mark.parametrize('fmt,group,n,k', [('int4', 128, 4096, 4096), ('int4', 64, 1024, 1024),
-                                           ('int8', 4096, 2048, 4096), ('int8', 32, 1000, 512)])
+@pytest.mark.parametrize('fmt,group,n,k', [('int4', 128, 4096, 4096), ('int4', 256, 1024, 1024),
+                                           ('int8', 4096, 2048, 4096), ('int8', 64, 1000, 512)])
 def test_wide_identity_is_bit_exact(device, fmt, group, n, k):
     """One-hot activation rows and power-of-two scales: row i of y is the dequantized column of its
     hot index, bit for bit, in every K slice and row position."""
@@ -113,7 +113,7 @@ def test_wide_is_the_default_for_17_to_32_rows(device):
     check(p, default, 'wide default')
 
 
-@pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=32), dict(fmt='nf4'), dict(M=33)])
+@pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=64), dict(fmt='nf4'), dict(M=33)])
 def test_wide_refuses_shapes_it_does_not_take(device, over):
     announce('wide refuses', over)
     fmt, m, n, k, group = over.get('fmt', 'int4'), over.get('M', 4), 256, over.get('K', 4096), over.get('group', 128)

@@ -18,14 +18,14 @@
 // (0,2,1,3,4,6,5,7) (INT8); the activations are staged in LDS with the same permutation of every
 // 8-element block, so both operands agree on k.
 //
-// Scales: a group's integer sums accumulate in their own MFMA accumulator (a group is one or more
-// whole loads: 64+ INT4 / 32+ INT8 codes), then acc += s * group_sum in fp32 -- the exact
+// Scales: a group's integer sums accumulate in their own MFMA accumulator (a group is two or more
+// whole loads: 128+ INT4 / 64+ INT8 codes), then acc += s * group_sum in fp32 -- the exact
 // x . (q * s) product up to fp32 rounding, whose distance to the reference's fp16(q * s) weights
 // the reference's rounding-budget gate bounds (torch_npu_lowbit_demo.py:97-106), as for the other
 // exact-q kernels.  Per-row INT8 accumulates all of K and multiplies once (the reference's W8
 // value, torch_npu_smollm.py:153-157).
 //
-// Workgroups of four waves own 128 weight rows and one K slice (grid y), walked in chunks of PC
+// Workgroups of kWideWaves waves own 32 weight rows each and one K slice (grid y), walked in chunks of PC
 // positions: the chunk's activations of all M rows are staged once per workgroup in one of two
 // LDS stages and serve the four waves; the next chunk's weights (registers) and activations are
 // loaded while the current one is computed, one barrier per chunk.  With one slice the workgroup
@@ -53,7 +53,10 @@ template <int FMT> struct WideTraits;
 template <> struct WideTraits<FMT_INT4> { static constexpr int CPL = 32, BITS = 4; };
 template <> struct WideTraits<FMT_INT8> { static constexpr int CPL = 16, BITS = 8; };
 
-constexpr int kWideWaves = 4;
+#ifndef LB_WIDE_WAVES
+#define LB_WIDE_WAVES 8
+#endif
+constexpr int kWideWaves = LB_WIDE_WAVES;
 constexpr int kWideRows = 32 * kWideWaves;  // weight rows per workgroup
 constexpr int kWideLoads = 4;               // 16-byte loads per lane per position (128 bytes of a row)
 
@@ -94,8 +97,9 @@ __device__ __forceinline__ h8 wide_permute(h8 v) {
   else return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
 }
 
-// GL: loads per scale group (1, 2, 4, ... ; 0 for per-row INT8).  PC: positions per chunk.
-template <int FMT, int GL, int PC>
+// GL: loads per scale group (2, 4, 8; 0 for per-row INT8).  PC: positions per chunk.  PD:
+// chunks of weights in flight (register buffers; chunk c + PD - 1 is requested while chunk c runs).
+template <int FMT, int GL, int PC, int PD>
 __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p) {
   constexpr int CPL = WideTraits<FMT>::CPL, BITS = WideTraits<FMT>::BITS;
   constexpr int POS = wide_position<FMT>();  // codes per position
@@ -110,6 +114,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
   constexpr int GPC = GROUPED ? NL / GL : 1;  // scale groups per chunk
   constexpr int kOutOfRange = (int)0x80000000u;
   static_assert(!GROUPED || (NL % GL == 0), "a chunk holds whole groups");
+  static_assert(PD >= 2, "at least the next chunk in flight");
   __shared__ __align__(16) f16 xs[2 * 32 * LD + LD];  // two stages, then a zero row
 
   const int t = threadIdx.x, lane = t & 63;
@@ -166,12 +171,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
     }
   };
 
-  Buf buf[2];
+  Buf buf[PD];
   u4 xv[XP];
-  if (chunks > 0) {
-    issue(buf[0], 0);
-    load_x(xv, 0);
-  }
+#pragma unroll
+  for (int u = 0; u < PD - 1; ++u)
+    if (u < chunks) issue(buf[u], u);
+  if (chunks > 0) load_x(xv, 0);
   for (int i = t; i < LD / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * LD + 8 * i) = h8{};
   if (chunks > 0) store_x(xv, 0);
   __syncthreads();
@@ -183,10 +188,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 
-  auto step = [&](auto stage) {
-    constexpr int ST = decltype(stage)::value;
-    Buf &b = buf[ST];
-    const f16 *xa = xs + a_base + (arow ? ST * 32 * LD : 0);
+  auto step = [&](Buf &b, int stage) {
+    const f16 *xa = xs + a_base + (arow ? stage * 32 * LD : 0);
     f16x part;
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
@@ -213,27 +216,25 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
           const float s = (float)__builtin_bit_cast(f16, (unsigned short)b.s[l / GL]);
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, part[r], acc[r]);
+          __builtin_amdgcn_sched_barrier(0);  // one group's accumulator at a time
         }
       }
     }
   };
-  // Chunk c uses stage c % 2; chunk c + 1 is loaded meanwhile and stored into the other stage.
-  for (int c = 0; c < chunks; c += 2) {
-    if (c + 1 < chunks) {
-      issue(buf[1], c + 1);
-      load_x(xv, c + 1);
+  // Chunk c runs from buffer c % PD and stage c % 2; chunk c + PD - 1's weights and chunk c + 1's
+  // activations are requested before it, the activations stored into the other stage after it.
+  for (int c = 0; c < chunks; c += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      const int cc = c + u;
+      if (cc < chunks) {
+        if (cc + PD - 1 < chunks) issue(buf[(u + PD - 1) % PD], cc + PD - 1);
+        if (cc + 1 < chunks) load_x(xv, cc + 1);
+        step(buf[u], cc & 1);
+        if (cc + 1 < chunks) store_x(xv, (cc + 1) & 1);
+        __syncthreads();
+      }
     }
-    step(std::integral_constant<int, 0>{});
-    if (c + 1 < chunks) store_x(xv, 1);
-    __syncthreads();
-    if (c + 1 >= chunks) break;
-    if (c + 2 < chunks) {
-      issue(buf[0], c + 2);
-      load_x(xv, c + 2);
-    }
-    step(std::integral_constant<int, 1>{});
-    if (c + 2 < chunks) store_x(xv, 0);
-    __syncthreads();
   }
 
   // Lane (col, half) holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col.
@@ -264,8 +265,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
 
 namespace lb {
 
-// Positions per chunk of the launched kernels.
-constexpr int kWidePC = 2;
+// Positions per chunk and chunks of weights in flight of the launched kernels.
+#ifndef LB_WIDE_PD
+#define LB_WIDE_PD 3
+#endif
+constexpr int kWidePC = 2, kWidePD = LB_WIDE_PD;
 template <int FMT> constexpr int wide_chunk() { return kWidePC * wide_position<FMT>(); }
 inline int wide_chunk_codes(int fmt) { return fmt == FMT_INT4 ? wide_chunk<FMT_INT4>() : wide_chunk<FMT_INT8>(); }
 

@@ -338,11 +338,12 @@ bool tile_rows_eligible(const lb_linear_args *a) {
 #endif
 
 // Loads per scale group of wide_rows_kernel (0: per-row INT8), or -1 where its groups do not fit:
-// a group is whole 32-byte pieces of a row (INT4 >= 64 codes, INT8 >= 32) and a chunk whole groups.
+// a group is at least two 32-byte pieces of a row (INT4 >= 128 codes, INT8 >= 64) and a chunk
+// whole groups.
 int wide_group_loads(int fmt, int64_t K, int64_t group) {
   if (fmt == FMT_INT8 && group == K) return 0;
   const int bits = fmt == FMT_INT8 ? 8 : 4;
-  if (!is_pow2(group) || group * bits / 8 < 32 || wide_chunk_codes(fmt) % group != 0) return -1;
+  if (!is_pow2(group) || group * bits / 8 < 64 || wide_chunk_codes(fmt) % group != 0) return -1;
   return (int)(group * bits / 8 / 32);
 }
 
@@ -551,7 +552,7 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
     return fail(LB_UNSUPPORTED,
                 "lb_linear: LB_FLAG_FORCE_WIDE needs int4/int8 codes, no correction or variant, M <= 32, 16-byte "
                 "aligned codes/x rows, K a multiple of %d (int4) / %d (int8) up to 65536, and per-row int8 or "
-                "power-of-two groups of at least 64 (int4) / 32 (int8) codes dividing that",
+                "power-of-two groups of at least 128 (int4) / 64 (int8) codes dividing that",
                 wide_chunk_codes(FMT_INT4), wide_chunk_codes(FMT_INT8));
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {

@@ -9,13 +9,12 @@ namespace lb {
 template <int FMT, int GL>
 void launch_wide_t(const WideParams &p, int slices, hipStream_t s) {
   const dim3 grid((unsigned)((p.N + kWideRows - 1) / kWideRows), (unsigned)slices);
-  hipLaunchKernelGGL((wide_rows_kernel<FMT, GL, kWidePC>), grid, dim3(64 * kWideWaves), 0, s, p);
+  hipLaunchKernelGGL((wide_rows_kernel<FMT, GL, kWidePC, kWidePD>), grid, dim3(64 * kWideWaves), 0, s, p);
 }
 
 template <int FMT>
 void launch_wide_f(const WideParams &p, int gl, int slices, hipStream_t s) {
   switch (gl) {
-    case 1: launch_wide_t<FMT, 1>(p, slices, s); break;
     case 2: launch_wide_t<FMT, 2>(p, slices, s); break;
     case 4: launch_wide_t<FMT, 4>(p, slices, s); break;
     case 8: launch_wide_t<FMT, 8>(p, slices, s); break;

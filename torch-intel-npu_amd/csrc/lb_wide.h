@@ -171,12 +171,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
     }
   };
 
+  // Loads complete in issue order, so every activation load is issued before the weight loads
+  // that may still be in flight when its staging waits for it.
   Buf buf[PD];
   u4 xv[XP];
+  if (chunks > 0) load_x(xv, 0);
 #pragma unroll
   for (int u = 0; u < PD - 1; ++u)
     if (u < chunks) issue(buf[u], u);
-  if (chunks > 0) load_x(xv, 0);
   for (int i = t; i < LD / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * LD + 8 * i) = h8{};
   if (chunks > 0) store_x(xv, 0);
   __syncthreads();
@@ -221,15 +223,15 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
       }
     }
   };
-  // Chunk c runs from buffer c % PD and stage c % 2; chunk c + PD - 1's weights and chunk c + 1's
-  // activations are requested before it, the activations stored into the other stage after it.
+  // Chunk c runs from buffer c % PD and stage c % 2; chunk c + 1's activations and chunk c + PD - 1's
+  // weights are requested before it, the activations stored into the other stage after it.
   for (int c = 0; c < chunks; c += PD) {
 #pragma unroll
     for (int u = 0; u < PD; ++u) {
       const int cc = c + u;
       if (cc < chunks) {
-        if (cc + PD - 1 < chunks) issue(buf[(u + PD - 1) % PD], cc + PD - 1);
         if (cc + 1 < chunks) load_x(xv, cc + 1);
+        if (cc + PD - 1 < chunks) issue(buf[(u + PD - 1) % PD], cc + PD - 1);
         step(buf[u], cc & 1);
         if (cc + 1 < chunks) store_x(xv, (cc + 1) & 1);
         __syncthreads();

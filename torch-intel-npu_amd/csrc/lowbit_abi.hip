@@ -325,10 +325,16 @@ bool tile_rows_eligible(const lb_linear_args *a) {
 }
 
 #ifndef LB_WIDE_MIN_M
-#define LB_WIDE_MIN_M 17  // wide_rows_kernel from this many activation rows (up to 32)
+#define LB_WIDE_MIN_M 17  // wide_rows_kernel from this many activation rows (up to 32) ...
 #endif
 #ifndef LB_WIDE_MIN_BYTES
 #define LB_WIDE_MIN_BYTES (4ll << 20)  // ... over weights of at least this many bytes
+#endif
+#ifndef LB_WIDE_MID_M
+#define LB_WIDE_MID_M 9  // and from this many rows over weights of LB_WIDE_MID_BYTES up to the streaming sizes
+#endif
+#ifndef LB_WIDE_MID_BYTES
+#define LB_WIDE_MID_BYTES (16ll << 20)
 #endif
 #ifndef LB_WIDE_TARGET_WGS
 #define LB_WIDE_TARGET_WGS 200  // K slices: the fewest that give this many workgroups
@@ -357,10 +363,13 @@ bool wide_shape_ok(const lb_linear_args *a) {
   return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
 }
 
+// 17..32 rows over >= 4 MB; 9..16 rows over 16..64 MB (the streaming kernels keep larger weights,
+// where they measured faster at these rows, and the one-tile kernels smaller ones).
 bool wide_eligible(const lb_linear_args *a) {
-  if (a->M < LB_WIDE_MIN_M || !wide_shape_ok(a)) return false;
+  if (a->M < LB_WIDE_MID_M || !wide_shape_ok(a)) return false;
   const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
-  return bytes >= LB_WIDE_MIN_BYTES;
+  if (a->M >= LB_WIDE_MIN_M) return bytes >= LB_WIDE_MIN_BYTES;
+  return bytes >= LB_WIDE_MID_BYTES && bytes < LB_STREAM_ROWS_MIN_BYTES;
 }
 
 // K slices of wide_rows_kernel: the fewest dividing the chunk count that give LB_WIDE_TARGET_WGS

@@ -211,6 +211,21 @@ GEMM_SPECS = ([('nf4', m, n, k, 64, name) for m in (128, 512, 2048)
               + [('int4', m, n, k, g, name) for m in (256, 1024) for name, n, k, g in LLAMA_SHAPES]
               + [('int4', 512, 14336, 4096, 128, '14336x4096'), ('nf4', 512, 14336, 4096, 128, '14336x4096'),
                  ('int8', 256, 576, 576, 576, 'smol135m_q_prefill')])
+# The cells the reference publishes (1024 x 1024; NPU times in ms, context only: its calls are bound by
+# one synchronous graph submission each), as (fmt, M, N, K, group, name, reference ms, source).
+REF_SPECS = [
+    ('int4', 1, 1024, 1024, 1024, 'ref_1024sq_per_channel', 0.530, 'research/results/lowbit/REPORT.md:56'),
+    ('nf4', 1, 1024, 1024, 1024, 'ref_1024sq_per_channel', 0.428, 'research/results/lowbit/REPORT.md:56'),
+    ('int4', 1, 1024, 1024, 128, 'ref_1024sq_g128', 0.369, 'research/results/lowbit-group/REPORT.md:54'),
+    ('nf4', 1, 1024, 1024, 128, 'ref_1024sq_g128', 0.349, 'research/results/lowbit-group/REPORT.md:57'),
+    ('int4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'CPU only: research/results/lowbit/REPORT.md:58'),
+    ('nf4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'CPU only: research/results/lowbit/REPORT.md:58'),
+    ('int4', 128, 1024, 1024, 128, 'ref_1024sq_g128', 0.547, 'research/results/lowbit-group/REPORT.md:55'),
+    ('nf4', 128, 1024, 1024, 128, 'ref_1024sq_g128', 0.485, 'research/results/lowbit-group/REPORT.md:58'),
+    ('int8', 1, 1024, 1024, 1024, 'ref_w8a16_1024sq', 0.2119, 'research/results/throughput-20261005/REPORT.md:24'),
+    ('int8', 512, 1024, 1024, 1024, 'ref_w8a16_1024sq', 0.4436, 'research/results/throughput-20261005/REPORT.md:27'),
+    ('int8', 1024, 1024, 1024, 1024, 'ref_w8a16_1024sq', 0.6308, 'research/results/throughput-20261005/REPORT.md:28'),
+]
 # hipBLASLt fp16 (torch.matmul, no dequantization) on the M = 512 cells: the vendor rate on these shapes.
 VENDOR_SPECS = [(512, 2560, 960, 'smol360m_gate'), (512, 960, 2560, 'smol360m_down'),
                 (512, 14336, 4096, '14336x4096'), (1024, 14336, 4096, '14336x4096')]
@@ -227,11 +242,18 @@ def sweep_row(lin, stream, fmt, m, n, k, g, name):
 
 
 def sweep(device, stream, quick):
-    """Config-5 GEMVs (INT4 at M = 1, 8, 32; W8 per-row at M = 1), the prefill cells of configs 3 and
-    5, and hipBLASLt fp16 on the M = 512 cells.  One packed weight per (format, shape) serves every M."""
+    """Config-5 GEMVs (INT4 and NF4 at M = 1, 8, 32; W8 per-row at M = 1), the prefill cells of configs 3
+    and 5, the 1024 x 1024 cells the reference publishes (with its NPU time beside ours), and hipBLASLt
+    fp16 on the M = 512 cells.  One packed weight per (format, shape) serves every M."""
     specs = [('int4', m, n, k, g, name) for m in ((1, 32) if quick else (1, 8, 32)) for name, n, k, g in LLAMA_SHAPES]
     specs += [('int8', 1, n, k, k, name) for name, n, k, _ in LLAMA_SHAPES]
+    if not quick:
+        specs += [('nf4', m, n, k, g, name) for m in (1, 8, 32) for name, n, k, g in LLAMA_SHAPES]
     specs += GEMM_SPECS[:4] if quick else GEMM_SPECS
+    reference = {}
+    for fmt, m, n, k, g, name, ms, src in ([] if quick else REF_SPECS):
+        reference[len(specs)] = dict(reference_npu_ms=ms, reference_source='/root/reference/npunlock-probe/' + src)
+        specs.append((fmt, m, n, k, g, name))
     order = sorted(range(len(specs)), key=lambda i: (specs[i][0], specs[i][2], specs[i][3]))
     rows, packed = [None] * len(specs), {}
     for i in order:
@@ -244,6 +266,10 @@ def sweep(device, stream, quick):
         bytes_w = algorithmic_bytes(fmt, 0, n, k, g)
         lin = Linear(packed[key], m, copies_for(bytes_w, cap=32), device, 400 + i)
         rows[i] = sweep_row(lin, stream, fmt, m, n, k, g, name)
+        if i in reference:
+            rows[i].update(reference[i])
+            if reference[i]['reference_npu_ms']:
+                rows[i]['speedup_vs_reference_npu'] = round(1e3 * reference[i]['reference_npu_ms'] / rows[i]['us'], 1)
         del lin
         torch.cuda.empty_cache()
     for m, n, k, name in ([] if quick else VENDOR_SPECS):

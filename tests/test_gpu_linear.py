@@ -212,6 +212,23 @@ SHAPES = [
 ]
 
 
+# Config 2: every SmolLM-135M linear shape at M = 1, 4, 16 on the default dispatch, with the
+# config's groups (64 at K = 576, 128 at K = 1536) and with the SmolLM default group 32.
+CONFIG2 = [(n, k) for n, k in ((576, 576), (192, 576), (1536, 576), (576, 1536), (49152, 576))]
+
+
+@pytest.mark.parametrize('group', ['config', 32])
+@pytest.mark.parametrize('m', [1, 4, 16])
+@pytest.mark.parametrize('shape', CONFIG2, ids=lambda s: f'{s[0]}x{s[1]}')
+def test_config2_cell_matches_oracle(device, shape, m, group):
+    n, k = shape
+    g = (64 if k == 576 else 128) if group == 'config' else group
+    announce('config2 cell', n, k, m, g)
+    rng = np.random.default_rng(100 + 7 * n + k + m)
+    p = problem(rng, 'int4', m, n, k, g)
+    check(p, run(p, device), f'config2 {n}x{k} M={m} g{g}')
+
+
 @pytest.mark.parametrize('spec', SHAPES, ids=lambda s: '-'.join(map(str, s)))
 def test_linear_matches_oracle(device, spec):
     fmt, m, n, k, group = spec

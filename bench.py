@@ -218,8 +218,8 @@ REF_SPECS = [
     ('nf4', 1, 1024, 1024, 1024, 'ref_1024sq_per_channel', 0.428, 'research/results/lowbit/REPORT.md:56'),
     ('int4', 1, 1024, 1024, 128, 'ref_1024sq_g128', 0.369, 'research/results/lowbit-group/REPORT.md:54'),
     ('nf4', 1, 1024, 1024, 128, 'ref_1024sq_g128', 0.349, 'research/results/lowbit-group/REPORT.md:57'),
-    ('int4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'CPU only: research/results/lowbit/REPORT.md:58'),
-    ('nf4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'CPU only: research/results/lowbit/REPORT.md:58'),
+    ('int4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'research/results/lowbit/REPORT.md:58 (CPU only)'),
+    ('nf4', 128, 1024, 1024, 1024, 'ref_1024sq_per_channel', None, 'research/results/lowbit/REPORT.md:58 (CPU only)'),
     ('int4', 128, 1024, 1024, 128, 'ref_1024sq_g128', 0.547, 'research/results/lowbit-group/REPORT.md:55'),
     ('nf4', 128, 1024, 1024, 128, 'ref_1024sq_g128', 0.485, 'research/results/lowbit-group/REPORT.md:58'),
     ('int8', 1, 1024, 1024, 1024, 'ref_w8a16_1024sq', 0.2119, 'research/results/throughput-20261005/REPORT.md:24'),

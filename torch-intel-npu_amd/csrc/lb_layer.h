@@ -360,21 +360,6 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
 }
 
 // ---------------------------------------------------------------- GEMV tiles
-// d = z.U[row] over the rank (zs and U both fp16, zero past the rank), 8 ranks per step on dot2.
-__device__ __forceinline__ float correction_dot_h(const f16 *zs, const f16 *urow, int rank) {
-  float d = 0.0f;
-#pragma unroll
-  for (int r8 = 0; r8 < kFusedMaxRank / 8; ++r8) {
-    if (8 * r8 < rank) {
-      const h8 u = *reinterpret_cast<const h8 *>(urow + 8 * r8);
-      const h8 z = *reinterpret_cast<const h8 *>(zs + 8 * r8);
-      d = dot2(pair_of(z, 3), pair_of(u, 3), dot2(pair_of(z, 2), pair_of(u, 2),
-              dot2(pair_of(z, 1), pair_of(u, 1), dot2(pair_of(z, 0), pair_of(u, 0), d))));
-    }
-  }
-  return d;
-}
-
 // Rows [n0, n0 + 16) of problem pi, with the fused decode kernel's product and epilogue.  Output:
 // q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
 // residual h1).
@@ -395,6 +380,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
   constexpr int VB = OWN_Z ? (KMAX / 8 + 7) / 8 : 0;  // V blocks per thread (8 threads per rank row)
   static_assert(!OWN_Z || (RANKED && VB * 64 <= KMAX + 4 * CPL + 8), "own z: staged row too short");
+  static_assert(kFusedMaxRank == 32, "the correction is one 32-deep product");
   constexpr int kOutOfRange = (int)0x80000000u;
   f16 *xs = reinterpret_cast<f16 *>(smem);                                  // [XLD]
   f16 *ss = xs + XLD;                                                       // [16 GMAX + 8]
@@ -576,7 +562,11 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   if (p.per_row) sum *= (float)rscale;
   f16 hv = (f16)sum;
   if (RANKED && rank > 0) {
-    const float d = correction_dot_h(zs, us + j * kFusedMaxRank, rank);
+    // d = z.U[row]^T as one 32-deep product: lane (g, j) brings ranks [8g, 8g + 8) of z (the A
+    // rows, all alike) and of U row j; both are zero from the rank on.  Lane (0, j) gets row j.
+    const h8 zfr = *reinterpret_cast<const h8 *>(zs + 8 * g);
+    const h8 ufr = *reinterpret_cast<const h8 *>(us + j * kFusedMaxRank + 8 * g);
+    const float d = __builtin_amdgcn_mfma_f32_16x16x32_f16(zfr, ufr, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0)[0];
     hv = (f16)((float)hv + (float)(f16)d);
   }
   if (pi == P_O || pi == P_DOWN) hv = (f16)((float)residual + (float)hv);

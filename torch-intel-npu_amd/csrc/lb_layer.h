@@ -491,21 +491,19 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   // Own z = fp16(x'.V^T) into zs (zero from the rank on), read by the epilogue after the barrier
   // that follows the product.  x' and V are both in the format's slot order within a block.
   if constexpr (OWN_Z) {
-    if (rank > 0) {
-      h8 xx[VB];
+    h8 xx[VB];
 #pragma unroll
-      for (int i = 0; i < VB; ++i) xx[i] = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
-      float za = 0.0f, zb = 0.0f;
+    for (int i = 0; i < VB; ++i) xx[i] = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
+    float za = 0.0f, zb = 0.0f;
 #pragma unroll
-      for (int i = 0; i < VB; ++i) {
-        asm volatile("" : "+v"(vreg[i]));
-        const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
-        za = dot2(pair_of(xx[i], 0), pair_of(vv, 0), dot2(pair_of(xx[i], 2), pair_of(vv, 2), za));
-        zb = dot2(pair_of(xx[i], 1), pair_of(vv, 1), dot2(pair_of(xx[i], 3), pair_of(vv, 3), zb));
-      }
-      za = sum8(za + zb);
-      if (vpart == 0) zs[vr] = vr < rank ? (f16)za : (f16)0.0f;
+    for (int i = 0; i < VB; ++i) {
+      asm volatile("" : "+v"(vreg[i]));
+      const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
+      za = dot2(pair_of(xx[i], 0), pair_of(vv, 0), dot2(pair_of(xx[i], 2), pair_of(vv, 2), za));
+      zb = dot2(pair_of(xx[i], 1), pair_of(vv, 1), dot2(pair_of(xx[i], 3), pair_of(vv, 3), zb));
     }
+    za = sum8(za + zb);
+    if (vpart == 0) zs[vr] = vr < rank ? (f16)za : (f16)0.0f;
   }
 
   f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -527,7 +525,6 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
-    if (kb >= K) break;
     asm volatile("" : "+v"(w[u]));
     const h2 s2 = {gsc[u], gsc[u]};
 #pragma unroll

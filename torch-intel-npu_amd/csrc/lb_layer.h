@@ -276,16 +276,19 @@ __device__ __forceinline__ h8 layer_prologue_apply(int prologue, const h8 &x, co
   return v;
 }
 
-// The source, prologue and K of each GEMV role.
+// The source, prologue and K of each GEMV role, by its source (a template argument, so every
+// role body is compiled for its own source and prologue): q|k|v read h, o the attention output,
+// gate|up h1, down (and its z) the gate|up words.
 struct RoleShape {
   int src, prologue, K;
   const f16 *gamma;
 };
-__device__ __forceinline__ RoleShape role_shape(const LayerParams &p, const LayerWeights &W, int pi) {
-  if (pi <= P_V) return {SRC_H, PRO_RMSNORM, p.hidden, W.norm1};
-  if (pi == P_O) return {SRC_ATT, PRO_NONE, p.hidden, nullptr};
-  if (pi <= P_UP) return {SRC_H1, PRO_RMSNORM, p.hidden, W.norm2};
-  return {SRC_GU, PRO_SILU_MUL, p.inter, nullptr};
+template <int SRC>
+__device__ __forceinline__ RoleShape role_shape(const LayerParams &p, const LayerWeights &W) {
+  if constexpr (SRC == SRC_H) return {SRC_H, PRO_RMSNORM, p.hidden, W.norm1};
+  else if constexpr (SRC == SRC_ATT) return {SRC_ATT, PRO_NONE, p.hidden, nullptr};
+  else if constexpr (SRC == SRC_H1) return {SRC_H1, PRO_RMSNORM, p.hidden, W.norm2};
+  else return {SRC_GU, PRO_SILU_MUL, p.inter, nullptr};
 }
 
 // Loads the plain source row (the layer input h) and the prologue's gamma row, straight-line.
@@ -309,14 +312,14 @@ __device__ __forceinline__ void layer_plain_loads(const LayerParams &p, const La
 // Rank r of problem pi: z = fp16(x'.V[r]^T), published as one tagged word (z in bits 16..31).
 // Thread t holds block t of the source row and of V[r] (K <= 2048), so no staging is needed:
 // each thread adds its eight products, the waves reduce on DPP and thread 0 adds the four waves.
-template <int KMAX>
+template <int KMAX, int SRC>
 __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W, int pi,
                                              int r, uint64_t passed, float *wsum) {
   constexpr int XB = (KMAX / 8 + 255) / 256;
   static_assert(XB == 1, "one source block per thread");
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const RoleShape rs = role_shape(p, W, pi);
+  const RoleShape rs = role_shape<SRC>(p, W);
   const int K = rs.K, blocks = K >> 3;
   const int zrank = pick(p.rank, pi);
   h8 xv[XB], av[XB];
@@ -363,7 +366,7 @@ __device__ __forceinline__ void layer_z_role(const LayerParams &p, const LayerCt
 // Rows [n0, n0 + 16) of problem pi, with the fused decode kernel's product and epilogue.  Output:
 // q|k|v and gate|up as words, o as the h1 words (after the residual h), down into h (after the
 // residual h1).
-template <int FMT, bool SCALED, int KMAX, bool RANKED, bool OWN_Z>
+template <int FMT, bool SCALED, int KMAX, bool RANKED, bool OWN_Z, int SRC>
 __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W, int pi,
                                                 int n0, uint64_t passed, uint8_t *smem) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
@@ -393,7 +396,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const RoleShape rs = role_shape(p, W, pi);
+  const RoleShape rs = role_shape<SRC>(p, W);
   const int K = rs.K, N = pick(p.N, pi), up_ld = pick(p.up_ld, pi);
   const int G = K == p.hidden ? p.G1 : p.G2;
   const int group_shift = K == p.hidden ? p.shift1 : p.shift2;
@@ -795,7 +798,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p, const 
     case R_TQKV:
       tile_of(P_Q, 3, pi, n0);
       each_layer([&](const LayerCtx &c, const LayerWeights &W) {
-        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, pi, n0, passed, smem);
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED, SRC_H>(p, c, W, pi, n0, passed, smem);
       });
       break;
     case R_ATTN:
@@ -803,21 +806,21 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerParams p, const 
       break;
     case R_TO:
       each_layer([&](const LayerCtx &c, const LayerWeights &W) {
-        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, P_O, i * 16, passed, smem);
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED, SRC_ATT>(p, c, W, P_O, i * 16, passed, smem);
       });
       break;
     case R_TGU:
       tile_of(P_GATE, 2, pi, n0);
       each_layer([&](const LayerCtx &c, const LayerWeights &W) {
-        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED>(p, c, W, pi, n0, passed, smem);
+        layer_tile_role<FMT, SCALED, 640, RANKED, RANKED, SRC_H1>(p, c, W, pi, n0, passed, smem);
       });
       break;
     case R_ZD:
-      each_layer([&](const LayerCtx &c, const LayerWeights &W) { layer_z_role<kFusedMaxK>(p, c, W, P_DOWN, i, passed, wsum); });
+      each_layer([&](const LayerCtx &c, const LayerWeights &W) { layer_z_role<kFusedMaxK, SRC_GU>(p, c, W, P_DOWN, i, passed, wsum); });
       break;
     default:
       each_layer([&](const LayerCtx &c, const LayerWeights &W) {
-        layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED, false>(p, c, W, P_DOWN, i * 16, passed, smem);
+        layer_tile_role<FMT, SCALED, kFusedMaxK, RANKED, false, SRC_GU>(p, c, W, P_DOWN, i * 16, passed, smem);
       });
       break;
   }

@@ -1114,7 +1114,6 @@ __global__ __launch_bounds__(1024) void argmax_next_kernel(const f16 *logits, in
                                                            int64_t *position, int limit) {
   __shared__ float bv[16];
   __shared__ int bi[16];
-  __shared__ int chosen;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   constexpr int kOutOfRange = (int)0x80000000u;
   constexpr int kLoads = 6;  // 16-byte loads per thread per round: 49152 logits per round
@@ -1141,21 +1140,33 @@ __global__ __launch_bounds__(1024) void argmax_next_kernel(const f16 *logits, in
   for (int i = full * 8 + t; i < vocab; i += 1024)
     if ((float)logits[i] > best) { best = (float)logits[i]; idx = i; }
   if (idx == 0x7fffffff) idx = vocab;  // a thread with no element (or only -inf) loses every tie below
+  // (value, index) pairs reduced by the larger value, then the smaller index: a total order, so the
+  // result does not depend on the order of the steps.  Within each row of 16 lanes on DPP moves,
+  // then over the four rows and the sixteen waves.
+  auto take = [](float &bv_, int &bi_, float ov, int oi) {
+    if (ov > bv_ || (ov == bv_ && oi < bi_)) { bv_ = ov; bi_ = oi; }
+  };
+  auto row_best = [&](float &bv_, int &bi_) {
+    take(bv_, bi_, dpp_move<kDppXor1>(bv_), dpp_move<kDppXor1>(bi_));
+    take(bv_, bi_, dpp_move<kDppXor2>(bv_), dpp_move<kDppXor2>(bi_));
+    take(bv_, bi_, dpp_move<kDppHalfMirror>(bv_), dpp_move<kDppHalfMirror>(bi_));
+    take(bv_, bi_, dpp_move<kDppMirror>(bv_), dpp_move<kDppMirror>(bi_));
+  };
+  row_best(best, idx);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ob = __shfl_xor(best, off, 64);
-    const int oi = __shfl_xor(idx, off, 64);
-    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-  }
+  for (int r = 16; r < 64; r += 16)
+    take(best, idx, lane_value(best, r), __builtin_amdgcn_readlane(idx, r));
   if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
   __syncthreads();
-  if (t == 0) {
-    float b0 = bv[0];
-    int i0 = bi[0];
-    for (int w = 1; w < 16; ++w)
-      if (bv[w] > b0 || (bv[w] == b0 && bi[w] < i0)) { b0 = bv[w]; i0 = bi[w]; }
-    if (i0 >= vocab) i0 = 0;  // every logit -inf: torch.argmax returns 0
-    chosen = i0;
+  if (wave != 0) return;
+  // Wave 0: the sixteen wave results (lanes 16..63 hold copies that lose every comparison), the
+  // token's bookkeeping, then the next input embedding.
+  best = lane < 16 ? bv[lane] : -INFINITY;
+  idx = lane < 16 ? bi[lane] : 0x7fffffff;
+  row_best(best, idx);
+  int i0 = __builtin_amdgcn_readfirstlane(idx);
+  if (i0 >= vocab) i0 = 0;  // every logit -inf: torch.argmax returns 0
+  if (lane == 0) {
     const int64_t pos = position[0];
     if (pos >= 0 && pos < limit) {
       tokens[pos] = i0;
@@ -1163,10 +1174,8 @@ __global__ __launch_bounds__(1024) void argmax_next_kernel(const f16 *logits, in
     }
     token[0] = i0;
   }
-  __syncthreads();
-  const int tok = chosen;
-  for (int b = t; b * 8 < hidden; b += 1024)
-    *reinterpret_cast<h8 *>(h + b * 8) = *reinterpret_cast<const h8 *>(embedding + (size_t)tok * hidden + b * 8);
+  for (int b = lane; b * 8 < hidden; b += 64)
+    *reinterpret_cast<h8 *>(h + b * 8) = *reinterpret_cast<const h8 *>(embedding + (size_t)i0 * hidden + b * 8);
 }
 
 }  // namespace lb

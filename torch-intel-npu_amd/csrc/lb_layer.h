@@ -601,8 +601,8 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
   f16 *kn = qs + kHeadDim;                               // [64]
   f16 *vn = kn + kHeadDim;                               // [64]
   f16 *raw = vn + kHeadDim;                              // [128] raw q and k rows
-  float *wred = reinterpret_cast<float *>(raw + 2 * kHeadDim);  // [4]
-  float *pv = wred + 4;                                  // [kPvPartials * kSliceDims]
+  float *wred = reinterpret_cast<float *>(raw + 2 * kHeadDim);  // [8] wave maxima, then wave sums
+  float *pv = wred + 8;                                  // [kPvPartials * kSliceDims]
   float *sc = pv + kPvPartials * kSliceDims;             // [capacity]
   constexpr int kOutOfRange = (int)0x80000000u;
   const int t = threadIdx.x, lane = t & 63;
@@ -688,6 +688,10 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
   h8 qreg[kHeadDim / 8];
 #pragma unroll
   for (int b = 0; b < kHeadDim / 8; ++b) qreg[b] = *reinterpret_cast<const h8 *>(qs + 8 * b);
+  // Scores of the first round's slots (t + 256 i) stay in registers; later rounds go through sc.
+  // The new key (slot pos, written to the cache by this launch) is read from LDS by the one lane
+  // that owns it, after the cached ones.
+  float scv[kScoreSlots];
   float lmax = -INFINITY;
   for (int base = 0; base <= pos; base += 256 * kScoreSlots) {
     if (base > 0) load_keys(base);
@@ -700,36 +704,57 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
       for (int b = 0; b < kHeadDim / 8; ++b) {
         asm volatile("" : "+v"(kreg[i][b]));
         const h8 qq = qreg[b];
-        const h8 kk = s == pos ? *reinterpret_cast<const h8 *>(kn + 8 * b) : __builtin_bit_cast(h8, kreg[i][b]);
+        const h8 kk = __builtin_bit_cast(h8, kreg[i][b]);
         acc0 = dot2(pair_of(qq, 0), pair_of(kk, 0), dot2(pair_of(qq, 2), pair_of(kk, 2), acc0));
         acc1 = dot2(pair_of(qq, 1), pair_of(kk, 1), dot2(pair_of(qq, 3), pair_of(kk, 3), acc1));
       }
-      if (s <= pos) {
-        const float v = (float)(f16)((float)(f16)(acc0 + acc1) * p.scale);
-        sc[s] = v;
-        lmax = fmaxf(lmax, v);
+      if (s == pos) {
+        acc0 = acc1 = 0.0f;
+#pragma unroll
+        for (int b = 0; b < kHeadDim / 8; ++b) {
+          const h8 qq = qreg[b];
+          const h8 kk = *reinterpret_cast<const h8 *>(kn + 8 * b);
+          acc0 = dot2(pair_of(qq, 0), pair_of(kk, 0), dot2(pair_of(qq, 2), pair_of(kk, 2), acc0));
+          acc1 = dot2(pair_of(qq, 1), pair_of(kk, 1), dot2(pair_of(qq, 3), pair_of(kk, 3), acc1));
+        }
       }
+      const float v = (float)(f16)((float)(f16)(acc0 + acc1) * p.scale);
+      if (base == 0) scv[i] = v;
+      else if (s <= pos) sc[s] = v;
+      if (s <= pos) lmax = fmaxf(lmax, v);
     }
   }
   lmax = wave_max(lmax);
   if (lane == 0) wred[wave] = lmax;
   __syncthreads();
   const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float ev[kScoreSlots];
   float lsum = 0.0f;
-  for (int s = t; s <= pos; s += 256) {
+#pragma unroll
+  for (int i = 0; i < kScoreSlots; ++i) {
+    ev[i] = 0.0f;
+    if (t + 256 * i <= pos) {
+      ev[i] = expf(scv[i] - m);
+      lsum += ev[i];
+    }
+  }
+  for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) {
     const float e = expf(sc[s] - m);
     sc[s] = e;
     lsum += e;
   }
   lsum = wave_sum(lsum);
+  if (lane == 0) wred[4 + wave] = lsum;
   __syncthreads();
-  if (lane == 0) wred[wave] = lsum;
-  __syncthreads();
-  const float total = ((wred[0] + wred[1]) + wred[2]) + wred[3];
-  for (int s = t; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
+  const float total = ((wred[4] + wred[5]) + wred[6]) + wred[7];
+#pragma unroll
+  for (int i = 0; i < kScoreSlots; ++i)
+    if (t + 256 * i <= pos) sc[t + 256 * i] = (float)(f16)(ev[i] / total);
+  for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
   __syncthreads();
 
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const h8 vnew = *reinterpret_cast<const h8 *>(vn + d0 + 8 * blk);  // the new value row's block
   for (int base = 0; base <= pos; base += kAttnParts * kValueSlots) {
     if (base > 0) load_values(base);
 #pragma unroll
@@ -737,7 +762,7 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
       const int s = base + part + kAttnParts * i;
       if (base + kAttnParts * i > pos) break;
       asm volatile("" : "+v"(vreg[i]));
-      const h8 vv = s == pos ? *reinterpret_cast<const h8 *>(vn + d0 + 8 * blk) : __builtin_bit_cast(h8, vreg[i]);
+      const h8 vv = s == pos ? vnew : __builtin_bit_cast(h8, vreg[i]);
       const float pr = s <= pos ? sc[min(s, pos)] : 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += pr * (float)vv[e];

@@ -679,12 +679,6 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
     }
     return;
   }
-  if (h % group == 0 && idx % kAttnDimSlices == 0 && t < 2 * kHeadDim) {
-    const int dd = t & 63;
-    f16 *dst = (t < kHeadDim ? W.keys : W.values) + head_base + (size_t)pos * kHeadDim + dd;
-    *dst = t < kHeadDim ? kn[dd] : vn[dd];
-  }
-
   h8 qreg[kHeadDim / 8];
 #pragma unroll
   for (int b = 0; b < kHeadDim / 8; ++b) qreg[b] = *reinterpret_cast<const h8 *>(qs + 8 * b);
@@ -773,6 +767,15 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
   if (t < kSliceDims && (t & 1) == 0) {
     const f16 a = (f16)pv_total(pv, t), b = (f16)pv_total(pv, t + 1);
     sys_store(p.ws + c.lw + p.w_att + (h * kHeadDim + d0 + t) / 2, pair_word(tag, a, b));
+  }
+  // The KV append (the first dim slice of the first query head of each KV group) comes last: the
+  // load counter also counts stores, so a store issued before the scores would make their wait
+  // for the cached rows wait for the store's round trip as well.  No workgroup of this launch
+  // reads the slot (each uses its own copy of the new row).
+  if (h % group == 0 && idx % kAttnDimSlices == 0 && t < 2 * kHeadDim) {
+    const int dd = t & 63;
+    f16 *dst = (t < kHeadDim ? W.keys : W.values) + head_base + (size_t)pos * kHeadDim + dd;
+    *dst = t < kHeadDim ? kn[dd] : vn[dd];
   }
 }
 

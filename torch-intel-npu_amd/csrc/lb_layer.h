@@ -718,33 +718,40 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
       if (s <= pos) lmax = fmaxf(lmax, v);
     }
   }
+  // Softmax with one exchange between the waves: each wave takes its exponentials against its own
+  // maximum and sums them; after one barrier every thread rescales by exp(wave max - max) (0 for a
+  // wave without keys) and divides by the rescaled total, added in wave order.
   lmax = wave_max(lmax);
-  if (lane == 0) wred[wave] = lmax;
-  __syncthreads();
-  const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
   float ev[kScoreSlots];
   float lsum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kScoreSlots; ++i) {
     ev[i] = 0.0f;
     if (t + 256 * i <= pos) {
-      ev[i] = expf(scv[i] - m);
+      ev[i] = expf(scv[i] - lmax);
       lsum += ev[i];
     }
   }
   for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) {
-    const float e = expf(sc[s] - m);
+    const float e = expf(sc[s] - lmax);
     sc[s] = e;
     lsum += e;
   }
   lsum = wave_sum(lsum);
-  if (lane == 0) wred[4 + wave] = lsum;
+  if (lane == 0) {
+    wred[wave] = lmax;
+    wred[4 + wave] = lsum;
+  }
   __syncthreads();
-  const float total = ((wred[4] + wred[5]) + wred[6]) + wred[7];
+  const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) total += wred[4 + w] * expf(wred[w] - m);
+  const float f = expf(lmax - m) / total;
 #pragma unroll
   for (int i = 0; i < kScoreSlots; ++i)
-    if (t + 256 * i <= pos) sc[t + 256 * i] = (float)(f16)(ev[i] / total);
-  for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] / total);
+    if (t + 256 * i <= pos) sc[t + 256 * i] = (float)(f16)(ev[i] * f);
+  for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) sc[s] = (float)(f16)(sc[s] * f);
   __syncthreads();
 
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};

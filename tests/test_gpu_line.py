@@ -8,8 +8,8 @@ lane's activations once; the sum is the exact x . (q s) product (magic-bias code
 v_dot2_f32_f16 with the bias removed per lane; group scales per lane, or per lane quad once two
 reduction levels have summed it; per-row scales on the row total).  The bars are those of every linear path: rel-L2 <= 1e-3 against the
 oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), bit-exact for
-identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes cover 1..8
-INT4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,
+identity inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  NF4 codes enter as the
+fp16 literals of an LDS pair table (no bias).  Shapes cover 1..8 INT4 / NF4 and 1..16 INT8 segments, a partly filled last segment, row groups and workgroups past N,
 groups of one lane pair, one quad and longer, per-row scales, bias and residual.  Rows shorter
 than a segment take pack_gemv_kernel, which packs whole rows across a wave's lanes: four loads per
 wave over at least 16384 rows (the SmolLM tied head), one load per wave for INT4 below that (the
@@ -44,6 +44,11 @@ LINE_SHAPES = [
     ('int8', 2048, 4096, 64),      # groups of one lane quad
     ('int8', 2048, 1536, 32),      # groups of two lanes
     ('int8', 3000, 1024, 1024),    # exactly one segment
+    ('nf4', 4096, 4096, 128),      # NF4: literals from the LDS pair table, quad scales
+    ('nf4', 37, 2176, 128),        # one quad in the second segment
+    ('nf4', 1000, 14336, 128),     # seven segments
+    ('nf4', 2056, 4096, 64),       # groups of two lanes
+    ('nf4', 4104, 4096, 4096),     # one scale per row (per-channel NF4)
 ]
 
 
@@ -66,15 +71,17 @@ def test_line_with_bias(device, spec):
     check(p, run(p, device), f'line bias {spec}')
 
 
-@pytest.mark.parametrize('fmt,group', [('int4', 128), ('int4', 64), ('int4', 4096), ('int8', 4096), ('int8', 64)])
+@pytest.mark.parametrize('fmt,group', [('int4', 128), ('int4', 64), ('int4', 4096), ('int8', 4096), ('int8', 64),
+                                       ('nf4', 128), ('nf4', 4096)])
 def test_line_identity_is_bit_exact(device, fmt, group):
     """One-hot activations and power-of-two scales: y is the dequantized column, bit for bit, for
     columns in every slot of a 16-byte load (even and odd INT4 nibbles) and in both segments."""
     n, k = 1000, 4096
     announce('line identity', fmt, group)
     rng = np.random.default_rng(group + (fmt == 'int8'))
-    codes = rng.integers(0, 16, n * k).astype(np.uint8) if fmt == 'int4' else rng.integers(-128, 128, n * k)
-    data = o.pack(codes) if fmt == 'int4' else codes.astype(np.int8).tobytes()
+    nibbles = fmt in ('int4', 'nf4')
+    codes = rng.integers(0, 16, n * k).astype(np.uint8) if nibbles else rng.integers(-128, 128, n * k)
+    data = o.pack(codes) if nibbles else codes.astype(np.int8).tobytes()
     g = k // group
     scales = (2.0 ** rng.integers(-12, 3, n * g)).astype(np.float16)
     w = o.dequantize(fmt, (n, k), group, data, scales.tobytes())

@@ -350,3 +350,18 @@ def test_host_or_mismatched_operands_raise_before_launch(device):
         lowbit_hip.linear(x, codes, wide[::2], **kw)
     y = lowbit_hip.linear(x, codes, scales, **kw, **good)
     assert o.rel_l2(y.cpu().numpy(), expected(p)) <= REL_L2
+
+
+@pytest.mark.parametrize('m,n,k,group', [(1, 20000, 4096, 128), (64, 4096, 1024, 64), (512, 2560, 960, 64)])
+def test_nf4_gemm_repeated_launches(device, m, n, k, group):
+    """NF4 GEMM tiles decode their weights through an LDS table that the workgroup's threads build
+    together; the first decode waits for the whole table.  Twelve launches of the forced GEMM path
+    each match the oracle and give the same bits."""
+    announce('nf4 gemm repeated', m, n, k, group)
+    rng = np.random.default_rng(m + n + k)
+    p = problem(rng, 'nf4', m, n, k, group)
+    first = run(p, device, lowbit_hip.FLAG_FORCE_GEMM)
+    check(p, first, f'nf4 gemm {m}x{n}x{k}')
+    for i in range(11):
+        again = run(p, device, lowbit_hip.FLAG_FORCE_GEMM)
+        np.testing.assert_array_equal(again.view(np.uint16), first.view(np.uint16), err_msg=f'launch {i + 2}')

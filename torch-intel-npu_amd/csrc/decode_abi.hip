@@ -335,21 +335,22 @@ bool try_stream(const FusedParams &p, int tiles, hipStream_t s) {
 #define LB_LINE_FEW_SEGMENTS 4  // rows of at most this many segments: 4 rows per wave (more waves), else 8
 #endif
 
-// One problem, one activation row, no prologue or correction, INT4 / INT8 codes whose 16-byte lane
+// One problem, one activation row, no prologue or correction, INT4 / INT8 / NF4 codes whose 16-byte lane
 // loads each lie in one group (one group per row, or power-of-two groups of at least CPL codes),
 // rows of at least one segment (64 lanes x CPL codes) and at most 16: launched in line_gemv_kernel,
 // which measured faster than the single-tile, multi-tile and streaming kernels on every such
 // shape (MI355X, one-row INT4 g128 and INT8 per-row GEMVs of 1024-128256 rows, K = 2048-14336).
 template <int FMT, bool SCALED>
 bool try_line(const FusedParams &p, hipStream_t s) {
-  if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8) {
+  if constexpr (FMT != FMT_INT4 && FMT != FMT_INT8 && FMT != FMT_NF4) {
     return false;
   } else {
     constexpr int CPL = LineTraits<FMT>::CPL, SEG = 64 * CPL;
     const FusedProblem &q = p.prob[0];
     if (p.force_stream || p.prologue != PRO_NONE || q.rank > 0 || p.G <= 0 || p.K % p.G != 0) return false;
     const int group = p.K / p.G;
-    if (p.K < SEG || p.K > kLineMaxWaves * SEG || stream_group_span(FMT, p.K, group) == 0 ||
+    // NF4 lanes hold the INT4 lane's 32 codes, so the same group spans apply.
+    if (p.K < SEG || p.K > kLineMaxWaves * SEG || stream_group_span(FMT == FMT_NF4 ? FMT_INT4 : FMT, p.K, group) == 0 ||
         (group != p.K && group < CPL) || !aligned(q.codes, 16) || !aligned(p.x, 16))
       return false;
     const int nseg = (p.K + SEG - 1) / SEG;

@@ -208,6 +208,8 @@ __global__ __launch_bounds__(256) void gemm2_kernel(LinearParams p) {
   Stage r0, r1;
   load(r0, kbeg);
   load(r1, min(kbeg + BK, klast));
+  // Every entry of the NF4 table (each written by one thread) before the first decode reads it.
+  if constexpr (FMT == FMT_NF4) __syncthreads();
   store(r0, 0);
   load(r0, min(kbeg + 2 * BK, klast));
   __syncthreads();
@@ -446,12 +448,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemm4_kernel(LinearParams p) {
   dma_a(std::integral_constant<int, 0>{}, kbeg);
   __builtin_amdgcn_sched_barrier(0);
   load(kbeg);
+  // Every entry of the NF4 table (each written by one thread) before the first decode reads it.
+  if constexpr (FMT == FMT_NF4) __syncthreads();
   store_b(0);
   load(kbeg + min(1, steps - 1) * BK);
   wait_vm(std::integral_constant<int, 0>{});
 #else
   load(kbeg);
   store_a(std::integral_constant<int, 0>{});
+  if constexpr (FMT == FMT_NF4) __syncthreads();  // the NF4 table before the first decode
   store_b(0);
   if (steps > 1) load(kbeg + BK);
 #endif

@@ -1,4 +1,4 @@
-// gfx950 one-row GEMV over INT4 / INT8 weights with lane-linear weight loads:
+// gfx950 one-row GEMV over INT4 / INT8 / NF4 weights with lane-linear weight loads:
 // y[n] = x . (q * s)[n] (+ bias) (+ residual), the exact-product sums of stream_gemv_kernel.
 //
 // Layout of the work.  A segment of a row is what one wave-wide 16-byte load covers: 64 lanes x
@@ -16,7 +16,9 @@
 //   INT8             0x6400 | (b ^ 0x80)      = 1152 + q
 // so a row's chain sums x (bias + q) over the lane's codes.  The chain starts at -B, B being the
 // lane's activations dotted with the biases (computed once, the same for all R rows), which leaves
-// sum x q up to fp32 rounding; the lane's CPL codes lie in one group, whose scale multiplies the
+// sum x q up to fp32 rounding.  NF4 codes enter as the fp16 literals of their byte's two codes
+// (the low nibble the even code) from a 256-pair table each workgroup builds in LDS, with no
+// bias (line_gemv_kernel only); the lane's CPL codes lie in one group, whose scale multiplies the
 // lane's sum (per-row scales multiply the row's total).  The reference's rounding-budget gate
 // (torch_npu_lowbit_demo.py:97-106) bounds the distance to its fp16(q * s) weights.
 #pragma once
@@ -28,6 +30,7 @@ namespace lb {
 template <int FMT> struct LineTraits;
 template <> struct LineTraits<FMT_INT4> { static constexpr int CPL = 32, BITS = 4, XL = 4; };
 template <> struct LineTraits<FMT_INT8> { static constexpr int CPL = 16, BITS = 8, XL = 2; };
+template <> struct LineTraits<FMT_NF4> { static constexpr int CPL = 32, BITS = 4, XL = 4; };
 
 constexpr int kLineMaxWaves = 16;  // waves per workgroup (segments x row groups)
 
@@ -51,6 +54,13 @@ __device__ __forceinline__ float line_pairs(const u4 *xv, h2 *xp) {
       b = dot2(xp[4 * i + 2], even, b);
       b = dot2(xp[4 * i + 3], odd, b);
     }
+  } else if constexpr (FMT == FMT_NF4) {  // natural pairs (codes 2e, 2e + 1 of a byte), no bias
+#pragma unroll
+    for (int i = 0; i < TR::XL; ++i) {
+      const h8 v = __builtin_bit_cast(h8, xv[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xp[4 * i + e] = h2{v[2 * e], v[2 * e + 1]};
+    }
   } else {
     const h2 bias = {(f16)1152.0f, (f16)1152.0f};
 #pragma unroll
@@ -67,9 +77,21 @@ __device__ __forceinline__ float line_pairs(const u4 *xv, h2 *xp) {
   return b;
 }
 
-// Chain of one 16-byte weight load against the lane's activation pairs, starting at acc.
+// Chain of one 16-byte weight load against the lane's activation pairs, starting at acc.  NF4:
+// each code byte's pair of fp16 literals from the workgroup's LDS table (all 16 reads issued
+// before the chain).
 template <int FMT>
-__device__ __forceinline__ float line_dot(const u4 &w, const h2 *xp, float acc) {
+__device__ __forceinline__ float line_dot(const u4 &w, const h2 *xp, float acc, const uint32_t *nf4_table) {
+  if constexpr (FMT == FMT_NF4) {
+    h2 pr[16];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pr[4 * d + e] = __builtin_bit_cast(h2, nf4_table[(w[d] >> (8 * e)) & 0xFFu]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2(xp[i], pr[i], acc);
+    return acc;
+  }
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     if constexpr (FMT == FMT_INT4) {  // (nibble ^ 8) under 0x6400: one three-input bit operation each
@@ -129,6 +151,7 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
   constexpr int kOutOfRange = (int)0x80000000u;
   static_assert(R == 4 || R == 8 || R == 16, "rows per wave");
   __shared__ float part[kLineMaxWaves * R];
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -188,6 +211,10 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
       SCALED ? (f16)1.0f
              : __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(pre_scales, ebytes), eoff, 0, 0));
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first wait
+  if constexpr (FMT == FMT_NF4) {
+    build_nf4_pair_table(nf4_table);
+    __syncthreads();
+  }
 
   // ---- arithmetic: R chains from -B ----
   h2 xp[4 * XL];
@@ -195,7 +222,7 @@ __global__ __launch_bounds__(64 * kLineMaxWaves) void line_gemv_kernel(const f16
   float v[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float a = line_dot<FMT>(w[r], xp, -bsum);
+    const float a = line_dot<FMT>(w[r], xp, -bsum, nf4_table);
     if constexpr (SCALED && !QS) v[r] = (float)sc[r] * a;
     else v[r] = a;
   }
@@ -348,7 +375,7 @@ __global__ __launch_bounds__(256) void pack_gemv_kernel(const f16 *pre_x, const 
   const int lg = S % 4 == 0 ? 2 : S % 2 == 0 ? 1 : 0;  // log2 of the slots per LDS sum
 #pragma unroll
   for (int u = 0; u < R; ++u) {
-    const float a = line_dot<FMT>(w[u], xp, -bsum);
+    const float a = line_dot<FMT>(w[u], xp, -bsum, nullptr);
     float v = SCALED ? (float)sc[u] * a : a;
     // Both moves under the full wave, then uniform selects.
     const float o1 = dpp_move<kDppXor1>(v);

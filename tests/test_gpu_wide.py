@@ -1,6 +1,6 @@
 """GPU parity of the several-row GEMV on 32x32 MFMA tiles (wide_rows_kernel) against the CPU oracle.
 
-INT4 / INT8 calls of 17..32 rows over >= 4 MB of weights run there by default; the tests force it
+INT4 / NF4 / INT8 calls of 17..32 rows over >= 4 MB of weights run there by default; the tests force it
 (LB_FLAG_FORCE_WIDE) on other shapes and row counts.  Every code is decoded to its exact integer q
 and a group's (or, for per-row INT8, the whole row's) integer sum is scaled in fp32, so its value
 is the exact x . (q s) product: the bars are those of every linear path, rel-L2 <= 1e-3 against
@@ -34,6 +34,9 @@ WIDE_SHAPES = [
     ('int8', 2048, 2048, 128),     # four loads per group
     ('int8', 1030, 1024, 64),      # two loads per group
     ('int8', 777, 768, 256),       # eight loads per group
+    ('nf4', 4096, 4096, 128),      # NF4 literals from the LDS table, split
+    ('nf4', 300, 1024, 256),       # NF4, a partial block, four loads per group
+    ('nf4', 28000, 512, 512),      # NF4, one chunk, one slice, eight loads per group
 ]
 ROWS = [1, 2, 5, 16, 17, 31, 32]
 
@@ -79,14 +82,16 @@ def test_wide_strided_rows(device):
 
 
 @pytest.mark.parametrize('fmt,group,n,k', [('int4', 128, 4096, 4096), ('int4', 256, 1024, 1024),
-                                           ('int8', 4096, 2048, 4096), ('int8', 64, 1000, 512)])
+                                           ('int8', 4096, 2048, 4096), ('int8', 64, 1000, 512),
+                                           ('nf4', 128, 2048, 2048)])
 def test_wide_identity_is_bit_exact(device, fmt, group, n, k):
     """One-hot activation rows and power-of-two scales: row i of y is the dequantized column of its
     hot index, bit for bit, in every K slice and row position."""
     announce('wide identity', fmt, group, n, k)
     rng = np.random.default_rng(group + n)
-    codes = rng.integers(0, 16, n * k).astype(np.uint8) if fmt == 'int4' else rng.integers(-128, 128, n * k)
-    data = o.pack(codes) if fmt == 'int4' else codes.astype(np.int8).tobytes()
+    nibbles = fmt in ('int4', 'nf4')
+    codes = rng.integers(0, 16, n * k).astype(np.uint8) if nibbles else rng.integers(-128, 128, n * k)
+    data = o.pack(codes) if nibbles else codes.astype(np.int8).tobytes()
     g = k // group
     scales = (2.0 ** rng.integers(-12, 3, n * g)).astype(np.float16)
     w = o.dequantize(fmt, (n, k), group, data, scales.tobytes())
@@ -113,7 +118,7 @@ def test_wide_is_the_default_for_17_to_32_rows(device):
     check(p, default, 'wide default')
 
 
-@pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=64), dict(fmt='nf4'), dict(M=33)])
+@pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=64), dict(fmt='nf4', group=64), dict(M=33)])
 def test_wide_refuses_shapes_it_does_not_take(device, over):
     announce('wide refuses', over)
     fmt, m, n, k, group = over.get('fmt', 'int4'), over.get('M', 4), 256, over.get('K', 4096), over.get('group', 128)

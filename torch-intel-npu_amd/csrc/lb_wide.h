@@ -52,6 +52,7 @@ struct WideParams {
 template <int FMT> struct WideTraits;
 template <> struct WideTraits<FMT_INT4> { static constexpr int CPL = 32, BITS = 4; };
 template <> struct WideTraits<FMT_INT8> { static constexpr int CPL = 16, BITS = 8; };
+template <> struct WideTraits<FMT_NF4> { static constexpr int CPL = 32, BITS = 4; };
 
 #ifndef LB_WIDE_WAVES
 #define LB_WIDE_WAVES 8
@@ -65,7 +66,14 @@ template <int FMT> constexpr int wide_position() { return kWideLoads * 2 * WideT
 // B operand of one 32x32x16 MFMA: the exact codes q of 8 k slots from the 16-byte load w (INT4:
 // dword t; INT8: dwords 2t, 2t + 1).
 template <int FMT>
-__device__ __forceinline__ h8 wide_decode(const u4 &w, int t) {
+__device__ __forceinline__ h8 wide_decode(const u4 &w, int t, const uint32_t *nf4_table) {
+  if constexpr (FMT == FMT_NF4) {  // each byte's two fp16 literals from the LDS table, natural order
+    const uint32_t v = w[t];
+    const h2 p0 = as_h2(nf4_table[v & 0xFFu]), p1 = as_h2(nf4_table[(v >> 8) & 0xFFu]);
+    const h2 p2 = as_h2(nf4_table[(v >> 16) & 0xFFu]), p3 = as_h2(nf4_table[v >> 24]);
+    return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+  }
   uint32_t r[4];
   h2 bias_even, bias_odd;
   if constexpr (FMT == FMT_INT4) {
@@ -94,6 +102,7 @@ __device__ __forceinline__ h8 wide_decode(const u4 &w, int t) {
 template <int FMT>
 __device__ __forceinline__ h8 wide_permute(h8 v) {
   if constexpr (FMT == FMT_INT4) return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
+  else if constexpr (FMT == FMT_NF4) return v;
   else return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
 }
 
@@ -116,6 +125,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
   static_assert(!GROUPED || (NL % GL == 0), "a chunk holds whole groups");
   static_assert(PD >= 2, "at least the next chunk in flight");
   __shared__ __align__(16) f16 xs[2 * 32 * LD + LD];  // two stages, then a zero row
+  __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -181,6 +191,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
     if (u < chunks) issue(buf[u], u);
   for (int i = t; i < LD / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * LD + 8 * i) = h8{};
   if (chunks > 0) store_x(xv, 0);
+  if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);  // complete at the barrier below
   __syncthreads();
 
   // A operand of lane (col, half): activation row col (or the zero row), k piece half.
@@ -198,7 +209,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
       asm volatile("" : "+v"(b.w[l]));  // decode here, not at the load
 #pragma unroll
       for (int q = 0; q < T8; ++q) {
-        const h8 bw = wide_decode<FMT>(b.w[l], q);
+        const h8 bw = wide_decode<FMT>(b.w[l], q, nf4_table);
         const h8 xa8 = *reinterpret_cast<const h8 *>(xa + 2 * CPL * l + 8 * q);
         if constexpr (GROUPED) {
           if (l % GL == 0 && q == 0) {
@@ -273,7 +284,7 @@ namespace lb {
 #endif
 constexpr int kWidePC = 2, kWidePD = LB_WIDE_PD;
 template <int FMT> constexpr int wide_chunk() { return kWidePC * wide_position<FMT>(); }
-inline int wide_chunk_codes(int fmt) { return fmt == FMT_INT4 ? wide_chunk<FMT_INT4>() : wide_chunk<FMT_INT8>(); }
+inline int wide_chunk_codes(int fmt) { return fmt == FMT_INT8 ? wide_chunk<FMT_INT8>() : wide_chunk<FMT_INT4>(); }
 
 // Launches wide_rows_kernel over ceil(N / 128) x `slices` workgroups; gl: loads per scale group
 // (0: per-row INT8).  Defined in wide_abi.hip.

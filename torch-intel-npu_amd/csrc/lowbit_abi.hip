@@ -344,7 +344,7 @@ bool tile_rows_eligible(const lb_linear_args *a) {
 #endif
 
 // Loads per scale group of wide_rows_kernel (0: per-row INT8), or -1 where its groups do not fit:
-// a group is at least two 32-byte pieces of a row (INT4 >= 128 codes, INT8 >= 64) and a chunk
+// a group is at least two 32-byte pieces of a row (INT4 / NF4 >= 128 codes, INT8 >= 64) and a chunk
 // whole groups.
 int wide_group_loads(int fmt, int64_t K, int64_t group) {
   if (fmt == FMT_INT8 && group == K) return 0;
@@ -357,7 +357,7 @@ int wide_group_loads(int fmt, int64_t K, int64_t group) {
 // row count and weight size it is chosen for).
 bool wide_shape_ok(const lb_linear_args *a) {
   const int fmt = (int)a->format;
-  if ((fmt != FMT_INT4 && fmt != FMT_INT8) || a->rank > 0 || a->M < 1 || a->M > 32) return false;
+  if ((fmt != FMT_INT4 && fmt != FMT_INT8 && fmt != FMT_NF4) || a->rank > 0 || a->M < 1 || a->M > 32) return false;
   if (a->K % wide_chunk_codes(fmt) != 0 || a->K > 65536) return false;
   if (wide_group_loads(fmt, a->K, a->group_size) < 0) return false;
   return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
@@ -559,9 +559,9 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
   }
   if ((a->flags & LB_FLAG_FORCE_WIDE) && ((a->flags & (LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8)) || !wide_shape_ok(a)))
     return fail(LB_UNSUPPORTED,
-                "lb_linear: LB_FLAG_FORCE_WIDE needs int4/int8 codes, no correction or variant, M <= 32, 16-byte "
-                "aligned codes/x rows, K a multiple of %d (int4) / %d (int8) up to 65536, and per-row int8 or "
-                "power-of-two groups of at least 128 (int4) / 64 (int8) codes dividing that",
+                "lb_linear: LB_FLAG_FORCE_WIDE needs int4/nf4/int8 codes, no correction or variant, M <= 32, "
+                "16-byte aligned codes/x rows, K a multiple of %d (int4, nf4) / %d (int8) up to 65536, and per-row "
+                "int8 or power-of-two groups of at least 128 (int4, nf4) / 64 (int8) codes dividing that",
                 wide_chunk_codes(FMT_INT4), wide_chunk_codes(FMT_INT8));
   int variant = VAR_PLAIN;
   if (a->flags & LB_FLAG_W8A8) {

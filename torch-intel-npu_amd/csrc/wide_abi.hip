@@ -26,6 +26,7 @@ void launch_wide_f(const WideParams &p, int gl, int slices, hipStream_t s) {
 
 void launch_wide(const WideParams &p, int format, int gl, int slices, hipStream_t s) {
   if (format == FMT_INT4) launch_wide_f<FMT_INT4>(p, gl, slices, s);
+  else if (format == FMT_NF4) launch_wide_f<FMT_NF4>(p, gl, slices, s);
   else launch_wide_f<FMT_INT8>(p, gl, slices, s);
 }
 

@@ -267,6 +267,31 @@ lb_status lb_decode_check(const void *workspace, size_t timeout_offset, void *st
 lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embedding, int64_t hidden, void *h_next,
                          int64_t *tokens, int64_t *token, int64_t *position, int64_t limit, void *stream);
 
+/* Workspace of lb_head_next for a head of `vocab` rows: a 64-bit maximum word and a 64-bit
+ * counter per group of 32 workgroups (64 rows each), and one pair for the total. */
+#define LB_HEAD_NEXT_WORKGROUPS(vocab) (((size_t)(vocab) + 63u) / 64u)
+#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 31u) / 32u + 1u))
+
+/*
+ * Final RMSNorm -> lm_head -> greedy step in one launch: lb_fused_linear(head) followed by
+ * lb_argmax_next(head->problems[0].y, vocab = N, embedding, hidden = K, h_next, tokens, token,
+ * position, limit), without the second launch: every workgroup reduces its 64 logits to one
+ * candidate and the last workgroup to finish picks the token (no workgroup waits for another).
+ * The logits are written as lb_fused_linear writes them (the same products and fp32 sums; for
+ * heads of fewer than 32768 rows lb_fused_linear may add a row's K slices in another order) and
+ * the token is the one lb_argmax_next picks from them.  Replaces the final RMSNorm and tied head
+ * (torch_npu_smollm_io.py:52-61) and the host argmax and embedding lookup of the reference
+ * generation loop (torch_npu_smollm_kv_demo.py:229-245, torch_npu_smollm_io.py:45-50).
+ *   head: one problem (the vocab rows), prologue LB_PROLOGUE_RMSNORM, no correction, bias or
+ *         residual; format LB_FORMAT_FP16 with K <= 640 or LB_FORMAT_INT4 (LB_UNSUPPORTED
+ *         otherwise: run the two calls).  head->workspace: LB_HEAD_NEXT_WORKSPACE_BYTES(N) bytes,
+ *         256-byte aligned, zero before its first use (every call leaves it zero again);
+ *         calls sharing it must be ordered (one stream).
+ *   h_next may be head->x itself (every workgroup has read x before the token is written).
+ */
+lb_status lb_head_next(const lb_fused_linear_args *head, const void *embedding, void *h_next, int64_t *tokens,
+                       int64_t *token, int64_t *position, int64_t limit, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

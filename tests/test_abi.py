@@ -238,6 +238,62 @@ def test_argmax_next_argument_errors():
         assert lib.lb_argmax_next(*bad, None) == lowbit_hip.INVALID_ARGUMENT, (index, value)
 
 
+def head_next_args(**over):
+    """A valid lb_head_next head: fp16 [1000, 64] tied rows, RMSNorm, its workspace."""
+    a = lowbit_hip.FusedLinearArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.format, a.K, a.group_size, a.prologue, a.count = 3, 64, 64, 1, 1
+    a.x, a.gamma, a.eps = 0x10000, 0x11000, 1e-5
+    q = a.problems[0]
+    q.codes, q.N, q.y = 0x100000, 1000, 0x20000
+    a.workspace, a.workspace_bytes = 0x40000, lowbit_hip.head_next_workspace_bytes(1000)
+    for key, value in over.items():
+        target = q if key in ('codes', 'scales', 'N', 'y', 'bias', 'residual', 'rank') else a
+        setattr(target, key, value)
+    return a
+
+
+HEAD_NEXT_OK = dict(embedding=0x100000, h_next=0x12000, tokens=0x30000, token=0x31000, position=0x32000, limit=8)
+
+
+@pytest.mark.parametrize('over,call_over,needle,status', [
+    (dict(count=2), {}, 'one problem', lowbit_hip.INVALID_ARGUMENT),
+    (dict(prologue=0), {}, 'RMSNorm', lowbit_hip.INVALID_ARGUMENT),
+    (dict(bias=0x50000), {}, 'no correction, bias or residual', lowbit_hip.INVALID_ARGUMENT),
+    (dict(format=0, scales=0x60000), {}, 'fp16 or int4', lowbit_hip.UNSUPPORTED),
+    (dict(K=1024, group_size=1024, x=0x200000, gamma=0x210000), dict(embedding=0x1000000, h_next=0x220000),
+     'K <= 640', lowbit_hip.UNSUPPORTED),
+    (dict(workspace_bytes=16), {}, 'workspace', lowbit_hip.INVALID_ARGUMENT),
+    (dict(workspace=0x40008), {}, 'workspace', lowbit_hip.INVALID_ARGUMENT),
+    (dict(struct_size=ctypes.sizeof(lowbit_hip.FusedLinearArgs) - 16), {}, 'struct_size', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(embedding=0), 'NULL', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(h_next=0x12008), 'alignment', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(limit=-1), 'limit', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(h_next=0x20000), 'h_next overlaps', lowbit_hip.INVALID_ARGUMENT),      # the logits
+    ({}, dict(h_next=0x11000), 'h_next overlaps gamma', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(token=0x30008), 'tokens overlaps token', lowbit_hip.INVALID_ARGUMENT),
+    ({}, dict(position=0x40010), 'overlaps workspace', lowbit_hip.INVALID_ARGUMENT),
+])
+def test_head_next_argument_errors(over, call_over, needle, status):
+    lib = lowbit_hip.library()
+    call = dict(HEAD_NEXT_OK, **call_over)
+    got = lib.lb_head_next(ctypes.byref(head_next_args(**over)), call['embedding'], call['h_next'], call['tokens'],
+                           call['token'], call['position'], call['limit'], None)
+    assert got == status, lib.lb_last_error().decode()
+    assert needle in lib.lb_last_error().decode()
+
+
+def test_head_next_workspace_size_matches_header():
+    """LB_HEAD_NEXT_WORKSPACE_BYTES as the Python helper computes it (the header macro is the ABI)."""
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parents[1] / 'include' / 'lowbit_decode_hip.h').read_text()
+    assert re.search(r'#define LB_HEAD_NEXT_WORKGROUPS\(vocab\) \(\(\(size_t\)\(vocab\) \+ 63u\) / 64u\)', text)
+    assert '#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 31u) / 32u + 1u))' in text
+    for vocab, want in ((1, 32), (2048, 32), (2049, 48), (49152, 16 * 25), (70001, 16 * 36)):
+        assert lowbit_hip.head_next_workspace_bytes(vocab) == want, vocab
+
+
 W8 = dict(format=0, group_size=128, K=128, flags=lowbit_hip.FLAG_W8A8, activation_scale=1 / 128)
 
 
@@ -456,7 +512,9 @@ calls = [('lb_linear', lambda: lib.lb_linear(ctypes.byref(a), None)),
          ('lb_dequantize', lambda: lib.lb_dequantize(1, 64, 128, 32, 0x10000, 0x20000, 0x50000, None)),
          ('lb_fused_linear', lambda: lib.lb_fused_linear(ctypes.byref(lowbit_hip.FusedLinearArgs()), None)),
          ('lb_decode_attention', lambda: lib.lb_decode_attention(ctypes.byref(lowbit_hip.DecodeAttentionArgs()), None)),
-         ('lb_argmax_next', lambda: lib.lb_argmax_next(0x1, 16, 0x2, 8, 0x3, 0x4, 0x5, 0x6, 4, None))]
+         ('lb_argmax_next', lambda: lib.lb_argmax_next(0x1, 16, 0x2, 8, 0x3, 0x4, 0x5, 0x6, 4, None)),
+         ('lb_head_next', lambda: lib.lb_head_next(ctypes.byref(lowbit_hip.FusedLinearArgs()), 0x1, 0x2, 0x3, 0x4, 0x5,
+                                                   4, None))]
 for name, call in calls:
     assert call() == lowbit_hip.DEVICE_FAILED, name
     message = lib.lb_last_error().decode()

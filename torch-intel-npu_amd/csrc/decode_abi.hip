@@ -120,6 +120,43 @@ lb_status check_fused(const lb_fused_linear_args *a) {
   return ok();
 }
 
+// The kernel parameters of a checked lb_fused_linear call (no shared-z workspace) and its tiles.
+FusedParams fused_params(const lb_fused_linear_args *a, int *tiles_out) {
+  FusedParams p{};
+  const bool dense = a->format == LB_FORMAT_FP16;
+  p.x = static_cast<const f16 *>(a->x);
+  p.x2 = static_cast<const f16 *>(a->x2);
+  p.gamma = static_cast<const f16 *>(a->gamma);
+  p.eps = a->eps;
+  p.K = (int)a->K;
+  const int64_t group = dense ? a->K : a->group_size;
+  p.G = (int)(a->K / group);
+  p.group_shift = shift_of(group, a->K);
+  p.per_row = a->format == LB_FORMAT_INT8 && group == a->K;
+  p.prologue = (int)a->prologue;
+  int tiles = 0;
+  for (int i = 0; i < LB_FUSED_MAX_PROBLEMS; ++i) {
+    FusedProblem &q = p.prob[i];
+    if (i < (int)a->count) {
+      const lb_fused_problem &s = a->problems[i];
+      q.codes = static_cast<const uint8_t *>(s.codes);
+      q.scales = static_cast<const f16 *>(s.scales);
+      q.y = static_cast<f16 *>(s.y);
+      q.bias = static_cast<const f16 *>(s.bias);
+      q.residual = static_cast<const f16 *>(s.residual);
+      q.rank = (int)s.rank;
+      q.down = s.rank ? static_cast<const f16 *>(s.down) : nullptr;
+      q.up = s.rank ? static_cast<const f16 *>(s.up) : nullptr;
+      q.up_ld = (int)s.up_ld;
+      q.N = (int)s.N;
+      tiles += (int)((s.N + 15) / 16);
+    }
+    q.tiles_end = tiles;  // absent problems own no tiles
+  }
+  *tiles_out = tiles;
+  return p;
+}
+
 template <int FMT, bool SCALED, int KMAX, bool RANKED>
 void launch_fused_k(const FusedParams &p, int tiles, hipStream_t s) {
   if constexpr (RANKED) {
@@ -157,8 +194,28 @@ bool launch_rows_k(const FusedParams &p, int tiles, hipStream_t s) {
   constexpr int WSTEP = (4 / RG) * 4 * FormatTraits<FMT>::CPL;
   if constexpr ((KMAX + WSTEP - 1) / WSTEP <= 32) {  // all of a lane's loads fit in registers
     const f16 *aux = p.prologue == PRO_SILU_MUL ? p.x2 : p.gamma;
-    hipLaunchKernelGGL((rows_gemv_kernel<FMT, SCALED, KMAX, RG>), dim3((tiles + RG - 1) / RG), dim3(256), 0, s,
-                       p.prob[0].codes, p.x, p.prob[0].scales, aux, p.prob[0].N, p.K, p.G, p.prologue, p.group_shift, p);
+    hipLaunchKernelGGL((rows_gemv_kernel<FMT, SCALED, KMAX, RG, false>), dim3((tiles + RG - 1) / RG), dim3(256), 0, s,
+                       p.prob[0].codes, p.x, p.prob[0].scales, aux, p.prob[0].N, p.K, p.G, p.prologue, p.group_shift, p,
+                       HeadNextParams{});
+    return true;
+  }
+  return false;
+}
+
+// lb_head_next: rows_gemv_kernel with four tiles per workgroup and the greedy tail (fp16 rows of
+// up to 640, INT4 rows of up to 1536; false: not available).
+template <int FMT, bool SCALED>
+bool launch_head_next_f(const FusedParams &p, const HeadNextParams &hn, int wgs, hipStream_t s) {
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(wgs), dim3(256), 0, s, p.prob[0].codes, p.x, p.prob[0].scales, p.gamma,
+                       p.prob[0].N, p.K, p.G, p.prologue, p.group_shift, p, hn);
+  };
+  if (p.K <= 640) {
+    go(rows_gemv_kernel<FMT, SCALED, 640, 4, true>);
+    return true;
+  }
+  if constexpr (FMT == FMT_INT4) {
+    go(rows_gemv_kernel<FMT, SCALED, 1536, 4, true>);
     return true;
   }
   return false;
@@ -612,37 +669,9 @@ lb_status lb_fused_linear(const lb_fused_linear_args *a, void *stream) {
   if (const lb_status bad = refuse_if_failed("lb_fused_linear"); bad != LB_OK) return bad;
   const lb_status st = check_fused(a);
   if (st != LB_OK) return st;
-  FusedParams p{};
-  const bool dense = a->format == LB_FORMAT_FP16;
-  p.x = static_cast<const f16 *>(a->x);
-  p.x2 = static_cast<const f16 *>(a->x2);
-  p.gamma = static_cast<const f16 *>(a->gamma);
-  p.eps = a->eps;
-  p.K = (int)a->K;
-  const int64_t group = dense ? a->K : a->group_size;
-  p.G = (int)(a->K / group);
-  p.group_shift = shift_of(group, a->K);
-  p.per_row = a->format == LB_FORMAT_INT8 && group == a->K;
-  p.prologue = (int)a->prologue;
   int tiles = 0;
-  for (int i = 0; i < LB_FUSED_MAX_PROBLEMS; ++i) {
-    FusedProblem &q = p.prob[i];
-    if (i < (int)a->count) {
-      const lb_fused_problem &s = a->problems[i];
-      q.codes = static_cast<const uint8_t *>(s.codes);
-      q.scales = static_cast<const f16 *>(s.scales);
-      q.y = static_cast<f16 *>(s.y);
-      q.bias = static_cast<const f16 *>(s.bias);
-      q.residual = static_cast<const f16 *>(s.residual);
-      q.rank = (int)s.rank;
-      q.down = s.rank ? static_cast<const f16 *>(s.down) : nullptr;
-      q.up = s.rank ? static_cast<const f16 *>(s.up) : nullptr;
-      q.up_ld = (int)s.up_ld;
-      q.N = (int)s.N;
-      tiles += (int)((s.N + 15) / 16);
-    }
-    q.tiles_end = tiles;  // absent problems own no tiles
-  }
+  FusedParams p = fused_params(a, &tiles);
+  const bool dense = a->format == LB_FORMAT_FP16;
   bool ranked = false;
   for (uint32_t i = 0; i < a->count; ++i) ranked = ranked || a->problems[i].rank > 0;
   void *ws = fused_workspace(a);
@@ -756,6 +785,75 @@ lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embeddin
                      static_cast<const f16 *>(logits), (int)vocab, static_cast<const f16 *>(embedding), (int)hidden,
                      static_cast<f16 *>(h_next), tokens, token, position, (int)limit);
   return launch_status("lb_argmax_next");
+}
+
+lb_status lb_head_next(const lb_fused_linear_args *a, const void *embedding, void *h_next, int64_t *tokens,
+                       int64_t *token, int64_t *position, int64_t limit, void *stream) {
+  if (const lb_status bad = refuse_if_failed("lb_head_next"); bad != LB_OK) return bad;
+  if (!a) return fail(LB_INVALID_ARGUMENT, "lb_head_next: args is NULL");
+  if (a->struct_size < sizeof(lb_fused_linear_args))
+    return fail(LB_INVALID_ARGUMENT, "lb_head_next: struct_size %u < %zu (the workspace fields are required)",
+                a->struct_size, sizeof(lb_fused_linear_args));
+  const lb_fused_problem &q = a->problems[0];
+  if (a->count != 1 || a->prologue != LB_PROLOGUE_RMSNORM || q.rank != 0 || q.bias || q.residual)
+    return fail(LB_INVALID_ARGUMENT, "lb_head_next: one problem with the RMSNorm prologue, no correction, bias or residual");
+  // The head itself is an lb_fused_linear call; its workspace belongs to the greedy tail here.
+  lb_fused_linear_args head = *a;
+  head.workspace = nullptr;
+  head.workspace_bytes = 0;
+  if (const lb_status st = check_fused(&head); st != LB_OK) return st;
+  if (a->format != LB_FORMAT_FP16 && a->format != LB_FORMAT_INT4)
+    return fail(LB_UNSUPPORTED, "lb_head_next: fp16 or int4 heads only (use lb_fused_linear + lb_argmax_next)");
+  if (a->format == LB_FORMAT_FP16 && a->K > 640)
+    return fail(LB_UNSUPPORTED, "lb_head_next: fp16 heads of K <= 640 only (use lb_fused_linear + lb_argmax_next)");
+  if (!embedding || !h_next || !tokens || !token || !position)
+    return fail(LB_INVALID_ARGUMENT, "lb_head_next: NULL pointer");
+  if (!aligned(embedding, 16) || !aligned(h_next, 16) || !aligned(tokens, 8) || !aligned(token, 8) ||
+      !aligned(position, 8))
+    return fail(LB_INVALID_ARGUMENT, "lb_head_next: embedding/h_next need 16-byte, indices 8-byte alignment");
+  if (limit < 0 || limit > INT32_MAX) return fail(LB_INVALID_ARGUMENT, "lb_head_next: limit outside 0..2^31-1");
+  const int64_t vocab = q.N, hidden = a->K;
+  const size_t ws_bytes = LB_HEAD_NEXT_WORKSPACE_BYTES(vocab);
+  static_assert(kHeadNextGroup == 32 && LB_HEAD_NEXT_WORKSPACE_BYTES(64 * 32 * 3) == 16u * 4u,
+                "the workspace macro's group size is the kernel's");
+  if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < ws_bytes)
+    return fail(LB_INVALID_ARGUMENT, "lb_head_next: workspace must be 256-byte aligned with %zu bytes", ws_bytes);
+  const Range ins[] = {range_of(a->x, (size_t)hidden * 2, "x"), range_of(a->gamma, (size_t)hidden * 2, "gamma"),
+                       range_of(q.codes, code_bytes(a->format, vocab, hidden), "codes"),
+                       range_of(q.scales, a->format == LB_FORMAT_FP16 ? 0 : (size_t)(vocab * (hidden / a->group_size) * 2),
+                                "scales"),
+                       range_of(embedding, (size_t)(vocab * hidden * 2), "embedding")};
+  const Range outs[] = {range_of(h_next, (size_t)hidden * 2, "h_next"), range_of(tokens, (size_t)limit * 8, "tokens"),
+                        range_of(token, 8, "token"), range_of(position, 8, "position"),
+                        range_of(q.y, (size_t)vocab * 2, "logits"), range_of(a->workspace, ws_bytes, "workspace")};
+  constexpr int kOuts = sizeof(outs) / sizeof(outs[0]);
+  for (int i = 0; i < kOuts; ++i) {
+    for (const Range &r : ins)  // h_next may be x itself: every workgroup reads x before the token is known
+      if (overlaps(outs[i], r) && !(i == 0 && h_next == a->x && &r == &ins[0]))
+        return fail(LB_INVALID_ARGUMENT, "lb_head_next: %s overlaps %s", outs[i].name, r.name);
+    for (int k = i + 1; k < kOuts; ++k)
+      if (overlaps(outs[i], outs[k]))
+        return fail(LB_INVALID_ARGUMENT, "lb_head_next: %s overlaps %s", outs[i].name, outs[k].name);
+  }
+  int tiles = 0;
+  const FusedParams p = fused_params(&head, &tiles);
+  const int wgs = (tiles + 3) / 4;
+  HeadNextParams hn{};
+  hn.ws = static_cast<uint64_t *>(a->workspace);
+  hn.embedding = static_cast<const f16 *>(embedding);
+  hn.h_next = static_cast<f16 *>(h_next);
+  hn.tokens = tokens;
+  hn.token = token;
+  hn.position = position;
+  hn.limit = (int)limit;
+  hn.hidden = (int)hidden;
+  hn.groups = (wgs + kHeadNextGroup - 1) / kHeadNextGroup;
+  hn.vocab = (int)vocab;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool launched = a->format == LB_FORMAT_FP16 ? launch_head_next_f<FMT_FP16, false>(p, hn, wgs, s)
+                                                    : launch_head_next_f<FMT_INT4, true>(p, hn, wgs, s);
+  if (!launched) return fail(LB_UNSUPPORTED, "lb_head_next: no kernel for this shape");
+  return launch_status("lb_head_next");
 }
 
 }  // extern "C"

@@ -69,6 +69,31 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// 64-bit keys across lanes: the two halves move on DPP / readlane separately.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_move64(uint64_t v) {
+  const uint32_t lo = (uint32_t)dpp_move<CTRL>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)dpp_move<CTRL>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t lane_value64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// Largest key of each row of 16 lanes, in every lane of the row; of the whole wave, wave-uniform.
+__device__ __forceinline__ uint64_t row_max64(uint64_t v) {
+  v = max64(v, dpp_move64<kDppXor1>(v));
+  v = max64(v, dpp_move64<kDppXor2>(v));
+  v = max64(v, dpp_move64<kDppHalfMirror>(v));
+  return max64(v, dpp_move64<kDppMirror>(v));
+}
+__device__ __forceinline__ uint64_t wave_max64(uint64_t v) {
+  v = row_max64(v);
+  return max64(max64(lane_value64(v, 0), lane_value64(v, 16)), max64(lane_value64(v, 32), lane_value64(v, 48)));
+}
+
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // SiLU from the hardware exp2 and reciprocal (about 1 fp32 ulp each; the result is rounded to
@@ -505,6 +530,80 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
   P.y[n0 + j] = h;
 }
 
+// Greedy token folded into the head GEMV (lb_head_next).  A logit v of row n becomes the 64-bit
+// key (order(v) << 32) | (2^32 - 1 - n), so the largest key is the largest value at its first row
+// (torch.argmax order; -0 ranks with +0); NaN and -inf take key 0, which every other key beats, and
+// a result of 0 means token 0, as in argmax_next_kernel.  The workgroups form groups of
+// kHeadNextGroup: each raises its group's maximum word to its own largest key, then counts itself
+// on the group's counter; the workgroup that completes a group takes the group's maximum (leaving
+// 0), raises the total's maximum word and counts itself on the top counter; the one that completes
+// that takes the total and writes the token, the position and the next embedding.  Every step is a
+// returning system-scope atomic (performed at the memory side, past the per-XCD L2s) issued only
+// after the previous one has returned, so a workgroup that sees a counter complete sees every
+// maximum raised before it; no workgroup waits for another and no cache is written back or
+// invalidated.  Maximum words and counters are set back to zero by the workgroup that completes
+// them, so a zeroed workspace is zero again after every call.
+constexpr int kHeadNextGroup = 32;  // LB_HEAD_NEXT_WORKSPACE_BYTES counts groups of 32
+struct HeadNextParams {
+  uint64_t *ws;              // maximum words [groups + 1] (the last one the total's), counters [groups + 1]
+  const f16 *embedding;      // [vocab, hidden]
+  f16 *h_next;               // [hidden]
+  int64_t *tokens, *token, *position;
+  int limit, hidden, groups, vocab;
+};
+
+__device__ __forceinline__ uint64_t logit_key(float v, int n) {
+  if (!(v > -INFINITY)) return 0;
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if (b == 0x80000000u) b = 0u;
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (0xFFFFFFFFu - (uint32_t)n);
+}
+
+// Lane 0: raise *max_word to key, then count on *counter; returns the counter's previous value.
+__device__ __forceinline__ uint64_t head_next_arrive(uint64_t *max_word, uint64_t *counter, uint64_t key) {
+  const uint64_t prev = __hip_atomic_fetch_max(max_word, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  asm volatile("" : : "v"(prev) : "memory");  // the maximum has returned before the count is issued
+  return __hip_atomic_fetch_add(counter, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Wave 0 of workgroup `wg` of `wgs`, with the workgroup's largest key `best` (wave-uniform).
+__device__ __forceinline__ void head_next_tail(const HeadNextParams &hn, uint64_t best, int lane, int wg, int wgs) {
+  uint64_t *maxima = hn.ws, *counters = hn.ws + hn.groups + 1;
+  const int grp = wg / kHeadNextGroup;
+  const int members = min(kHeadNextGroup, wgs - grp * kHeadNextGroup);
+  uint64_t seen = 0, v = 0;
+  if (lane == 0) seen = head_next_arrive(maxima + grp, counters + grp, best);
+  if ((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)seen) != (uint32_t)(members - 1)) return;
+  if (lane == 0) {
+    v = __hip_atomic_exchange(maxima + grp, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(counters + grp, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (hn.groups > 1) {  // a single group's maximum is already the total
+    if (lane == 0) seen = head_next_arrive(maxima + hn.groups, counters + hn.groups, v);
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)seen) != (uint32_t)(hn.groups - 1)) return;
+    if (lane == 0) {
+      v = __hip_atomic_exchange(maxima + hn.groups, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(counters + hn.groups, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+  v = lane_value64(v, 0);
+  // A key names a row below vocab; the bound only matters for a workspace that was not zeroed.
+  const uint32_t row = 0xFFFFFFFFu - (uint32_t)v;
+  const int t = (v == 0 || row >= (uint32_t)hn.vocab) ? 0 : (int)row;
+  if (lane == 0) {
+    const int64_t pos = hn.position[0];
+    if (pos >= 0 && pos < hn.limit) {
+      hn.tokens[pos] = t;
+      hn.position[0] = pos + 1;
+    }
+    hn.token[0] = t;
+  }
+  for (int b = lane; b * 8 < hn.hidden; b += 64)
+    *reinterpret_cast<h8 *>(hn.h_next + b * 8) =
+        *reinterpret_cast<const h8 *>(hn.embedding + (size_t)t * hn.hidden + b * 8);
+}
+
 // One activation row, one problem, no correction, many rows (the long-N one-row linears: a tied
 // head, the Llama-shaped projections).  A workgroup holds RG 16-row tiles; wave (rg, kg) computes
 // tile rg over the k-steps kg, kg + KG, ... with KG = 4 / RG, so the staged activation row serves
@@ -514,11 +613,13 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
 // registers at wave launch (-amdgpu-kernarg-preload-count): workgroups dispatched while earlier ones
 // flood the memory system with weight requests would otherwise wait microseconds for their
 // argument block before issuing a single load.  The epilogue operands (residual, bias, per-row
-// scale) are loaded after the weights and staged behind a second barrier.
-template <int FMT, bool SCALED, int KMAX, int RG>
+// scale) are loaded after the weights and staged behind a second barrier.  With NEXT the
+// workgroups also pick the greedy token of the row they compute (head_next_tail above).
+template <int FMT, bool SCALED, int KMAX, int RG, bool NEXT>
 __global__ __launch_bounds__(256) void rows_gemv_kernel(const uint8_t *pre_codes, const f16 *pre_x, const f16 *pre_scales,
                                                         const f16 *pre_aux, int pre_N, int pre_K, int pre_G,
-                                                        int pre_prologue, int pre_shift, FusedParams p) {
+                                                        int pre_prologue, int pre_shift, FusedParams p,
+                                                        HeadNextParams hn) {
   constexpr int CPL = FormatTraits<FMT>::CPL;
   constexpr int BITS = FormatTraits<FMT>::BITS;
   constexpr int KSTEP = 4 * CPL;
@@ -539,6 +640,8 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(const uint8_t *pre_codes
   __shared__ float red[KG > 1 ? (KG - 1) * ROWS : 1];
   __shared__ float wsum[4];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
+  __shared__ uint64_t wkey[NEXT ? 4 : 1];
+  static_assert(!NEXT || RG == 4, "the greedy tail needs every wave to own a whole tile");
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -639,15 +742,29 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(const uint8_t *pre_codes
 #pragma unroll
     for (int q = 0; q < KG - 1; ++q) sum += red[q * ROWS + rg * 16 + j];
   }
-  if (g != 0 || j >= rows) return;
-
   // ---- epilogue (reference torch_npu_lowbit.py:262-266, torch_npu_smollm.py:160-163) ----
-  const int r = rg * 16 + j;
-  if (p.per_row) sum *= (float)es[2 * ROWS + r];
-  f16 h = (f16)sum;
-  if (P.bias) h = (f16)((float)h + (float)es[ROWS + r]);
-  if (P.residual) h = (f16)((float)es[r] + (float)h);
-  P.y[n0 + j] = h;
+  auto finish = [&]() {
+    const int r = rg * 16 + j;
+    if (p.per_row) sum *= (float)es[2 * ROWS + r];
+    f16 h = (f16)sum;
+    if (P.bias) h = (f16)((float)h + (float)es[ROWS + r]);
+    if (P.residual) h = (f16)((float)es[r] + (float)h);
+    P.y[n0 + j] = h;
+    return h;
+  };
+  if constexpr (NEXT) {
+    // Lanes 0..15 hold the tile's rows: the wave's largest key, then the workgroup's.
+    const uint64_t key = (g == 0 && j < rows) ? logit_key((float)finish(), n0 + j) : 0;
+    const uint64_t tile_best = row_max64(key);  // every lane active: the DPP moves read lanes 0..15
+    if (lane == 0) wkey[wave] = tile_best;
+    __syncthreads();
+    if (wave != 0) return;
+    head_next_tail(hn, max64(max64(wkey[0], wkey[1]), max64(wkey[2], wkey[3])), lane, (int)blockIdx.x,
+                   (int)gridDim.x);
+  } else {
+    if (g != 0 || j >= rows) return;
+    finish();
+  }
 }
 
 struct AttnParams {

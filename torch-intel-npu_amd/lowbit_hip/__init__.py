@@ -24,7 +24,7 @@ FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
-DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_decode_layer',
+DECODE_EXPORTS = ('lb_fused_linear', 'lb_decode_attention', 'lb_argmax_next', 'lb_head_next', 'lb_decode_layer',
                   'lb_decode_stack_prepare', 'lb_decode_stack', 'lb_decode_stack_release', 'lb_decode_check')
 PROLOGUES = {'none': 0, 'rmsnorm': 1, 'silu_mul': 2}
 MAX_PROBLEMS, MAX_RANK, MAX_FUSED_K = 3, 32, 1536
@@ -36,6 +36,13 @@ def attention_workspace_bytes(heads, capacity):
 FUSED_WORKSPACE_BYTES = 512  # LB_FUSED_WORKSPACE_BYTES: tagged z words [3][12] u64, launch count u64, timeout u32
 FUSED_TIMEOUT_OFFSET = 392   # LB_FUSED_TIMEOUT_OFFSET
 DECODE_TIMEOUT_OFFSET = 8    # LB_DECODE_TIMEOUT_OFFSET (lb_decode_layer / lb_decode_stack workspaces)
+
+
+def head_next_workspace_bytes(vocab):
+    """LB_HEAD_NEXT_WORKSPACE_BYTES: a maximum word and a counter (u64) per group of 32 workgroups
+    of 64 rows, and one pair for the total."""
+    wgs = (vocab + 63) // 64
+    return 16 * ((wgs + 31) // 32 + 1)
 
 
 def attention_timeout_offset(heads, capacity):
@@ -195,6 +202,10 @@ def library():
         lib.lb_argmax_next.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int64, ctypes.c_void_p]
+        lib.lb_head_next.restype = ctypes.c_int
+        lib.lb_head_next.argtypes = [ctypes.POINTER(FusedLinearArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                     ctypes.c_void_p]
         if lib.lb_abi_version() != ABI_VERSION:
             raise RuntimeError(f'liblowbit_hip ABI {lib.lb_abi_version()} != expected {ABI_VERSION}')
         _lib = lib
@@ -630,6 +641,43 @@ class PreparedArgmax:
         status = self._fn(*self._call, ctypes.c_void_p(handle))
         if status != OK:
             _check(status, 'lb_argmax_next')
+
+
+class PreparedHeadNext:
+    """lb_head_next: final RMSNorm -> head -> greedy token in one launch, the result of
+    PreparedFused(h, [head], prologue='rmsnorm') followed by PreparedArgmax on its logits, with
+    h_next = h.  head: dict(codes, scales (None for fp16), N = vocab, y = logits); format 'fp16'
+    (K <= 640) or 'int4'.  Owns a zeroed workspace (every run leaves it zero again)."""
+
+    FORMATS = ('fp16', 'int4')
+
+    def __init__(self, h, head, embedding, tokens, token, position, *, format, K, group_size, gamma, eps=1e-5,
+                 limit):
+        if format not in self.FORMATS or (format == 'fp16' and K > 640):
+            raise ValueError('lb_head_next takes fp16 heads of K <= 640 and int4 heads')
+        vocab = head['N']
+        if embedding.shape != (vocab, K):
+            raise ValueError('embedding must be [N, K]')
+        for t, name in ((tokens, 'tokens'), (token, 'token'), (position, 'position')):
+            _row(t, name, 1, torch.int64)
+        if tokens.numel() < limit:
+            raise ValueError('tokens must hold `limit` entries')
+        _row(embedding, 'embedding', vocab * K)
+        self._fused = PreparedFused(h, [head], format=format, K=K, group_size=group_size, prologue='rmsnorm',
+                                    gamma=gamma, eps=eps, shared_z=False)
+        size = head_next_workspace_bytes(vocab)
+        self.workspace = torch.zeros(size, dtype=torch.uint8, device=h.device)
+        self._fused.args.workspace, self._fused.args.workspace_bytes = _ptr(self.workspace), size
+        self._keep = [embedding, tokens, token, position, self.workspace]
+        self._call = (_ptr(embedding), _ptr(h), _ptr(tokens), _ptr(token), _ptr(position), limit)
+        self._fn = library().lb_head_next
+        self._device = h.device
+
+    def run(self, stream=None):
+        handle = torch.cuda.current_stream(self._device).cuda_stream if stream is None else stream
+        status = self._fn(self._fused._ref, *self._call, ctypes.c_void_p(handle))
+        if status != OK:
+            _check(status, 'lb_head_next')
 
 
 def _fill_projections(proj, projections, keep):

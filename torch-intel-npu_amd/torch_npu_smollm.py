@@ -556,8 +556,9 @@ class GraphDecoder:
       3. o projection (+ correction) + residual                     lb_fused_linear
       4. RMSNorm -> gate | up projections (+ corrections)           lb_fused_linear
       5. SiLU(gate) * up -> down projection (+ correction) + residual  lb_fused_linear
-    then RMSNorm -> tied fp16 lm_head (lb_fused_linear) and the greedy token with the next
-    embedding (lb_argmax_next).  Projections of different formats (fp16-protected ones)
+    then RMSNorm -> tied fp16 lm_head and the greedy token with the next embedding, as one
+    lb_head_next launch (head_next=True, the default, where it takes the head's format) or as
+    lb_fused_linear + lb_argmax_next.  Projections of different formats (fp16-protected ones)
     get separate launches.  layer=True (default) runs those five steps of a layer as one
     lb_decode_layer launch whenever its seven projections share one format and group (the
     reference's one graph per layer); the fused launches remain for other layers.  stack=True
@@ -568,11 +569,13 @@ class GraphDecoder:
     corrections its own workspace, so each correction's z is computed once per launch.
     """
 
-    def __init__(self, stack, io, *, fused=True, shared_z=True, layer=True, stack_kernel=True):
+    def __init__(self, stack, io, *, fused=True, shared_z=True, layer=True, stack_kernel=True, head_next=True):
         self.device = io.embedding.device
         if self.device.type != 'cuda':
             raise ValueError('GraphDecoder needs FrozenSmolIO moved to a ROCm device')
         self.stack, self.io, self.fused, self.shared_z = stack, io, fused, shared_z
+        self.use_head_next = head_next
+        self.head_next = None
         dev = self.device
         cap = stack.layers[0].capacity
         self.capacity = cap
@@ -656,17 +659,24 @@ class GraphDecoder:
         self._build_head(io)
 
     def _build_head(self, io):
-        """Final RMSNorm -> tied lm_head (one fused launch) and the greedy token with the next embedding."""
+        """Final RMSNorm -> tied lm_head and the greedy token with the next embedding: one
+        lb_head_next launch where it takes the head (fp16, int4), else one fused launch for the head
+        and lb_argmax_next."""
         import lowbit_hip as lb
         if io.head is None:
             head, head_format, head_group = dict(codes=io.embedding, scales=None), 'fp16', HIDDEN
         else:
             codes, scales = io.head_tensors(self.device)
             head, head_format, head_group = dict(codes=codes, scales=scales), io.head.format, io.head.group_size
-        self.head = lb.PreparedFused(self.h, [dict(head, N=io.vocab_size, y=self.logits)], format=head_format,
-                                     K=HIDDEN, group_size=head_group, prologue='rmsnorm', gamma=io.norm, eps=1e-5)
+        problem = dict(head, N=io.vocab_size, y=self.logits)
+        self.head = lb.PreparedFused(self.h, [problem], format=head_format, K=HIDDEN, group_size=head_group,
+                                     prologue='rmsnorm', gamma=io.norm, eps=1e-5)
         self.argmax = lb.PreparedArgmax(self.logits, io.embedding, self.h, self.tokens, self.token, self.pos,
                                         limit=self.capacity)
+        if self.use_head_next and head_format in lb.PreparedHeadNext.FORMATS:
+            self.head_next = lb.PreparedHeadNext(self.h, problem, io.embedding, self.tokens, self.token, self.pos,
+                                                 format=head_format, K=HIDDEN, group_size=head_group, gamma=io.norm,
+                                                 eps=1e-5, limit=self.capacity)
 
     # ---------------------------------------------------------------- one launch per layer
     _ORDER = ('self_attn.q_proj.weight', 'self_attn.k_proj.weight', 'self_attn.v_proj.weight',
@@ -850,8 +860,11 @@ class GraphDecoder:
         for seq in self.calls:
             for call in seq:
                 call.run()
-        self.head.run()
-        self.argmax.run()
+        if self.head_next is not None:
+            self.head_next.run()
+        else:
+            self.head.run()
+            self.argmax.run()
 
     def capture(self, tokens=1):
         """Record `tokens` consecutive step()s into one HIP graph (warm-up runs first on a side

@@ -1026,7 +1026,7 @@ void finish_params(LayerParams *p, uint32_t format, int64_t group_size, int *fmt
 
 // Dynamic LDS: the largest role (a 1536-long tile: staged row, scales, U rows, reductions, NF4
 // table) or the attention (its rows, the P.V partials and one float per cache slot).
-size_t layer_smem(const LayerParams &p) { return std::max<size_t>(9216, 2048 + (size_t)4 * p.capacity); }
+size_t layer_smem(const LayerParams &p) { return std::max<size_t>(kLayerTileSmem, 2048 + (size_t)4 * p.capacity); }
 
 template <int FMT, bool SCALED, bool RANKED, bool STACK>
 const void *layer_kernel_fn() {

@@ -88,6 +88,7 @@ struct LayerCtx {
 
 constexpr int kLayerSpinLimit = 1 << 18;
 constexpr int kLayerZWords = 32;  // z words per problem: one rank per z workgroup and word
+constexpr int kLayerTileSmem = 9216;  // dynamic LDS bytes a tile role may use (the launch gives at least this)
 
 __device__ __forceinline__ uint64_t sys_load(const uint64_t *a) {
   return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -382,7 +383,11 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   constexpr int GMAX = KMAX / FusedGroupMin<KMAX>::value;
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
   constexpr int VB = OWN_Z ? (KMAX / 8 + 7) / 8 : 0;  // V blocks per thread (8 threads per rank row)
-  static_assert(!OWN_Z || (RANKED && VB * 64 <= KMAX + 4 * CPL + 8), "own z: staged row too short");
+  static_assert(!OWN_Z || RANKED, "own z needs the correction");
+  static_assert(XLD * 2 + (SCALED ? 16 * GMAX + 8 : 8) * 2 + 16 * kFusedMaxRank * 2 + 2 * kFusedMaxRank * 2 +
+                        ((KG - 1) * 16 + 4) * 4 + 256 * 4 + (OWN_Z ? VB * 64 * 2 : 0) <=
+                    kLayerTileSmem,
+                "the tile role's LDS exceeds the launch's dynamic LDS");
   static_assert(kFusedMaxRank == 32, "the correction is one 32-deep product");
   constexpr int kOutOfRange = (int)0x80000000u;
   f16 *xs = reinterpret_cast<f16 *>(smem);                                  // [XLD]
@@ -392,6 +397,7 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
   float *red = reinterpret_cast<float *>(zs + 2 * kFusedMaxRank);           // [48]
   float *wsum = red + (KG - 1) * 16;                                        // [4]
   uint32_t *nf4_table = reinterpret_cast<uint32_t *>(wsum + 4);             // [256]
+  f16 *xn = reinterpret_cast<f16 *>(nf4_table + 256);                       // [VB * 64] x' in natural order (own z)
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -484,24 +490,30 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
     const int b = t + 256 * i;
-    if (b < blocks) *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(layer_prologue_apply(rs.prologue, xv[i], av[i], inv));
+    if (b < blocks) {
+      const h8 v = layer_prologue_apply(rs.prologue, xv[i], av[i], inv);
+      *reinterpret_cast<h8 *>(xs + b * 8) = permute_block<FMT>(v);
+      if constexpr (OWN_Z) *reinterpret_cast<h8 *>(xn + b * 8) = v;
+    }
   }
   // Zeros past K: MFMA lanes read up to KSTEP beyond it, the own z product up to VB * 64.
-  const int zero_end = OWN_Z ? XLD : min(XLD, K + KSTEP + 8);
-  for (int b = blocks + t; b * 8 < zero_end; b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  for (int b = blocks + t; b * 8 < min(XLD, K + KSTEP + 8); b += 256) *reinterpret_cast<h8 *>(xs + b * 8) = h8{};
+  if constexpr (OWN_Z) {
+    for (int b = blocks + t; b < VB * 8; b += 256) *reinterpret_cast<h8 *>(xn + b * 8) = h8{};
+  }
   __syncthreads();
 
   // Own z = fp16(x'.V^T) into zs (zero from the rank on), read by the epilogue after the barrier
-  // that follows the product.  x' and V are both in the format's slot order within a block.
+  // that follows the product: V rows as loaded against the natural-order copy of x'.
   if constexpr (OWN_Z) {
     h8 xx[VB];
 #pragma unroll
-    for (int i = 0; i < VB; ++i) xx[i] = *reinterpret_cast<const h8 *>(xs + (vpart + 8 * i) * 8);
+    for (int i = 0; i < VB; ++i) xx[i] = *reinterpret_cast<const h8 *>(xn + (vpart + 8 * i) * 8);
     float za = 0.0f, zb = 0.0f;
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       asm volatile("" : "+v"(vreg[i]));
-      const h8 vv = permute_block<FMT>(__builtin_bit_cast(h8, vreg[i]));
+      const h8 vv = __builtin_bit_cast(h8, vreg[i]);
       za = dot2(pair_of(xx[i], 0), pair_of(vv, 0), dot2(pair_of(xx[i], 2), pair_of(vv, 2), za));
       zb = dot2(pair_of(xx[i], 1), pair_of(vv, 1), dot2(pair_of(xx[i], 3), pair_of(vv, 3), zb));
     }

@@ -108,8 +108,14 @@ __device__ __forceinline__ h8 wide_permute(h8 v) {
 
 // GL: loads per scale group (2, 4, 8; 0 for per-row INT8).  PC: positions per chunk.  PD:
 // chunks of weights in flight (register buffers; chunk c + PD - 1 is requested while chunk c runs).
+// The operands of the first loads come as leading scalar arguments (pre_*, the same values as in
+// p), which the build preloads into registers at wave launch: a workgroup dispatched while earlier
+// ones flood the memory system would otherwise wait for its argument block before its first load.
 template <int FMT, int GL, int PC, int PD>
-__global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p) {
+__global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_t *pre_codes, const f16 *pre_x,
+                                                                    const f16 *pre_scales, int pre_M, int pre_N,
+                                                                    int pre_K, int pre_G, int pre_shift, int pre_ldx,
+                                                                    int pre_kslice, WideParams p) {
   constexpr int CPL = WideTraits<FMT>::CPL, BITS = WideTraits<FMT>::BITS;
   constexpr int POS = wide_position<FMT>();  // codes per position
   constexpr int KC = PC * POS;                // codes per chunk
@@ -131,14 +137,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int row0 = blockIdx.x * kWideRows + wave * 32;  // this wave's first weight row
-  const int rows = __builtin_amdgcn_readfirstlane(max(0, min(32, p.N - row0)));  // scalar: the descriptors stay uniform
-  const int kbeg = blockIdx.y * p.kslice;
-  const int chunks = min(p.kslice, p.K - kbeg) / KC;
-  const int row_bytes = p.K * BITS / 8;
+  const int rows = __builtin_amdgcn_readfirstlane(max(0, min(32, pre_N - row0)));  // scalar: the descriptors stay uniform
+  const int kbeg = blockIdx.y * pre_kslice;
+  const int chunks = min(pre_kslice, pre_K - kbeg) / KC;
+  const int row_bytes = pre_K * BITS / 8;
   const __amdgpu_buffer_rsrc_t wb =
-      buffer_rsrc(p.codes + (size_t)(rows > 0 ? row0 : 0) * row_bytes, (size_t)rows * row_bytes);
+      buffer_rsrc(pre_codes + (size_t)(rows > 0 ? row0 : 0) * row_bytes, (size_t)rows * row_bytes);
   const __amdgpu_buffer_rsrc_t sb =
-      buffer_rsrc(p.scales + (size_t)(rows > 0 ? row0 : 0) * p.G, GROUPED ? (size_t)rows * p.G * 2 : 0);
+      buffer_rsrc(pre_scales + (size_t)(rows > 0 ? row0 : 0) * pre_G, GROUPED ? (size_t)rows * pre_G * 2 : 0);
   // Lane's byte offset of load l of a chunk at k: row col, piece 32 * l + 16 * half of the chunk.
   const int lane_off = col * row_bytes + 16 * half;
 
@@ -152,22 +158,22 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
     for (int l = 0; l < NL; ++l)
       b.w[l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, lane_off + kb + 32 * l, 0, 0));
     if constexpr (GROUPED) {
-      const int g0 = (kbeg + c * KC) >> p.group_shift;
+      const int g0 = (kbeg + c * KC) >> pre_shift;
 #pragma unroll
       for (int q = 0; q < GPC; ++q)
-        b.s[q] = __builtin_amdgcn_raw_buffer_load_b16(sb, (col * p.G + g0 + q) * 2, 0, 0);
+        b.s[q] = __builtin_amdgcn_raw_buffer_load_b16(sb, (col * pre_G + g0 + q) * 2, 0, 0);
     }
   };
   // Activation pieces of chunk c: piece i = (row m, 8-element block); rows past M are not staged.
-  const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(p.x, ((size_t)(p.M - 1) * p.ldx + p.K) * 2);
+  const __amdgpu_buffer_rsrc_t xb = buffer_rsrc(pre_x, ((size_t)(pre_M - 1) * pre_ldx + pre_K) * 2);
   auto load_x = [&](u4 (&xv)[XP], int c) {
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
       const int idx = i * NT + t;
       const int m = idx / (KC / 8), blk = idx % (KC / 8);
-      const bool live = idx < XPIECES && m < p.M;
+      const bool live = idx < XPIECES && m < pre_M;
       xv[i] = __builtin_bit_cast(
-          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (m * p.ldx + kbeg + c * KC + 8 * blk) * 2 : kOutOfRange,
+          u4, __builtin_amdgcn_raw_buffer_load_b128(xb, live ? (m * pre_ldx + kbeg + c * KC + 8 * blk) * 2 : kOutOfRange,
                                                     0, 0));
     }
   };
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
     for (int i = 0; i < XP; ++i) {
       const int idx = i * NT + t;
       const int m = idx / (KC / 8), blk = idx % (KC / 8);
-      if (idx < XPIECES && m < p.M)
+      if (idx < XPIECES && m < pre_M)
         *reinterpret_cast<h8 *>(xs + st * 32 * LD + m * LD + 8 * blk) = wide_permute<FMT>(__builtin_bit_cast(h8, xv[i]));
     }
   };
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(WideParams p
   __syncthreads();
 
   // A operand of lane (col, half): activation row col (or the zero row), k piece half.
-  const bool arow = col < p.M;
+  const bool arow = col < pre_M;
   const int a_base = (arow ? col * LD : 2 * 32 * LD) + half * CPL;
   f16x acc;
 #pragma unroll

@@ -9,7 +9,8 @@ namespace lb {
 template <int FMT, int GL>
 void launch_wide_t(const WideParams &p, int slices, hipStream_t s) {
   const dim3 grid((unsigned)((p.N + kWideRows - 1) / kWideRows), (unsigned)slices);
-  hipLaunchKernelGGL((wide_rows_kernel<FMT, GL, kWidePC, kWidePD>), grid, dim3(64 * kWideWaves), 0, s, p);
+  hipLaunchKernelGGL((wide_rows_kernel<FMT, GL, kWidePC, kWidePD>), grid, dim3(64 * kWideWaves), 0, s, p.codes, p.x,
+                     p.scales, p.M, p.N, p.K, p.G, p.group_shift, p.ldx, p.kslice, p);
 }
 
 template <int FMT>

@@ -8,15 +8,18 @@
 // the row, so one wave-wide load covers 32 rows x 32 bytes and four consecutive loads a 128-byte
 // "position" of every row (256 INT4 / 128 INT8 codes).
 //
-// Decode to the exact integer q as fp16, without a scale: the nibble / byte sits under a magic
-// exponent and one subtraction removes the bias (every value involved is a small integer, so the
-// fp16 arithmetic is exact):
-//   INT4 even codes  0x6400 | (c ^ 8)         = 1024 + (c ^ 8)  - 1032 = q
-//   INT4 odd codes   0x5400 | ((c ^ 8) << 4)  =   64 + (c ^ 8)  -   72 = q   (decoded where it sits)
-//   INT8             0x6400 | (b ^ 0x80)      = 1024 + (b ^ 0x80) - 1152 = b
+// INT4 codes enter the MFMA as the fp16 value of a "magic" half-word, the sign-flipped nibble
+// under the exponent of 1024 (one three-input bit operation per pair):
+//   even codes  (c ^ 8) | 0x6400         = 1032 + q   (activation x)
+//   odd codes   ((c ^ 8) << 4) | 0x6400  = 1152 + 16 q (activation x / 16, nibble in place)
+// so the product sums x (bias + q).  The bias part, B = the staged activations dotted with the
+// biases, is the same for every weight row: the staging computes it per activation row and scale
+// group, and the group's MFMA accumulator starts at -B, which leaves sum x q up to fp32 rounding.
+// INT8 bytes become the exact q in registers: (b ^ 0x80) | 0x6400 = 1152 + q, then - 1152 (exact
+// fp16 arithmetic on small integers).
 // Eight codes become the MFMA's eight k slots in the order (0,4,1,5,2,6,3,7) (INT4) or
 // (0,2,1,3,4,6,5,7) (INT8); the activations are staged in LDS with the same permutation of every
-// 8-element block, so both operands agree on k.
+// 8-element block, so both operands agree on k.  NF4 codes enter as their fp16 literals (no bias).
 //
 // Scales: a group's integer sums accumulate in their own MFMA accumulator (a group is two or more
 // whole loads: 128+ INT4 / 64+ INT8 codes), then acc += s * group_sum in fp32 -- the exact
@@ -75,35 +78,67 @@ __device__ __forceinline__ h8 wide_decode(const u4 &w, int t, const uint32_t *nf
                                    0, 1, 2, 3, 4, 5, 6, 7);
   }
   uint32_t r[4];
-  h2 bias_even, bias_odd;
   if constexpr (FMT == FMT_INT4) {
-    const uint32_t a = w[t] ^ 0x88888888u, b = a >> 8;
-    r[0] = (a & 0x000F000Fu) | 0x64006400u;  // c0, c4: 1024 + c'
-    r[1] = (a & 0x00F000F0u) | 0x54005400u;  // c1, c5:   64 + c'
-    r[2] = (b & 0x000F000Fu) | 0x64006400u;  // c2, c6
-    r[3] = (b & 0x00F000F0u) | 0x54005400u;  // c3, c7
-    bias_even = h2{(f16)-1032.0f, (f16)-1032.0f};
-    bias_odd = h2{(f16)-72.0f, (f16)-72.0f};
-  } else {
+    const uint32_t a = w[t], b = a >> 8;
+    r[0] = (a & 0x000F000Fu) ^ 0x64086408u;  // c0, c4: 1032 + q
+    r[1] = (a & 0x00F000F0u) ^ 0x64806480u;  // c1, c5: 1152 + 16 q
+    r[2] = (b & 0x000F000Fu) ^ 0x64086408u;  // c2, c6
+    r[3] = (b & 0x00F000F0u) ^ 0x64806480u;  // c3, c7
+  } else {  // INT8: the exact q (the bias removed here; it measured faster than a staged bias)
     const uint32_t a = w[2 * t] ^ 0x80808080u, b = w[2 * t + 1] ^ 0x80808080u;
-    r[0] = (a & 0x00FF00FFu) | 0x64006400u;         // b0, b2: 1024 + b'
+    r[0] = (a & 0x00FF00FFu) | 0x64006400u;         // b0, b2: 1152 + q
     r[1] = ((a >> 8) & 0x00FF00FFu) | 0x64006400u;  // b1, b3
     r[2] = (b & 0x00FF00FFu) | 0x64006400u;         // b4, b6
     r[3] = ((b >> 8) & 0x00FF00FFu) | 0x64006400u;  // b5, b7
-    bias_even = bias_odd = h2{(f16)-1152.0f, (f16)-1152.0f};
+    const h2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+    const h2 p0 = as_h2(r[0]) + bias, p1 = as_h2(r[1]) + bias, p2 = as_h2(r[2]) + bias, p3 = as_h2(r[3]) + bias;
+    return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
   }
-  const h2 p0 = as_h2(r[0]) + bias_even, p1 = as_h2(r[1]) + bias_odd;
-  const h2 p2 = as_h2(r[2]) + bias_even, p3 = as_h2(r[3]) + bias_odd;
-  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
-                                 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(h8, u4{r[0], r[1], r[2], r[3]});
+}
+
+// Bias part of one staged INT4 block (slot order) against the magic codes: 1032 for the even
+// codes' slots, 1152 for the odd ones (which hold x / 16).
+__device__ __forceinline__ float wide_block_bias(const h8 &v) {
+  const float even = ((float)v[0] + (float)v[1]) + ((float)v[4] + (float)v[5]);
+  const float odd = ((float)v[2] + (float)v[3]) + ((float)v[6] + (float)v[7]);
+  return 1032.0f * even + 1152.0f * odd;
+}
+
+// Sum over aligned groups of N consecutive lanes (4 .. 64), in every lane of the group; every lane
+// active.  DPP: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror; then lane swaps.
+template <int CTRL>
+__device__ __forceinline__ float wide_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int N>
+__device__ __forceinline__ float wide_group_sum(float v) {
+  static_assert(N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group of 4 .. 64 lanes");
+  v += wide_dpp<0xB1>(v);
+  v += wide_dpp<0x4E>(v);
+  if constexpr (N >= 8) v += wide_dpp<0x141>(v);
+  if constexpr (N >= 16) v += wide_dpp<0x140>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
 }
 
 // Activation block permutation matching wide_decode: slot e holds element perm[e].
+// INT4: the odd codes' slots (2, 3, 6, 7) hold x / 16 (exact: a power of two).
 template <int FMT>
 __device__ __forceinline__ h8 wide_permute(h8 v) {
-  if constexpr (FMT == FMT_INT4) return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
-  else if constexpr (FMT == FMT_NF4) return v;
-  else return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
+  if constexpr (FMT == FMT_INT4) {
+    h8 p = __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
+    const h2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const h2 o0 = h2{p[2], p[3]} * sixteenth, o1 = h2{p[6], p[7]} * sixteenth;
+    p[2] = o0[0]; p[3] = o0[1]; p[6] = o1[0]; p[7] = o1[1];
+    return p;
+  } else if constexpr (FMT == FMT_NF4) {
+    return v;
+  } else {
+    return __builtin_shufflevector(v, v, 0, 2, 1, 3, 4, 6, 5, 7);
+  }
 }
 
 // GL: loads per scale group (2, 4, 8; 0 for per-row INT8).  PC: positions per chunk.  PD:
@@ -130,7 +165,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
   constexpr int kOutOfRange = (int)0x80000000u;
   static_assert(!GROUPED || (NL % GL == 0), "a chunk holds whole groups");
   static_assert(PD >= 2, "at least the next chunk in flight");
+  // Staged pieces of one activation row per scale group (INT4, where the bias is staged):
+  // consecutive threads hold consecutive pieces of a row, a group aligned to PPG lanes.
+  constexpr bool BIASED = FMT == FMT_INT4;
+  constexpr int PPG = GROUPED ? GL * 2 * CPL / 8 : KC / 8;  // a load covers 2 CPL codes of a row
+  static_assert(!BIASED || GROUPED, "INT4 weights have scale groups");
+  static_assert(!BIASED || (PPG <= 64 && NT % (KC / 8) == 0 && (KC / 8) % PPG == 0), "bias groups within a wave");
   __shared__ __align__(16) f16 xs[2 * 32 * LD + LD];  // two stages, then a zero row
+  __shared__ __align__(16) float nbs[BIASED ? 2 * GPC * 32 : 4];  // -B per stage, group of the chunk, activation row
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -177,13 +219,20 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
                                                     0, 0));
     }
   };
+  // Staged pieces, and each (row, group) bias sum B negated into nbs (every lane takes part in the
+  // group sums: pieces past M or the chunk were loaded as zeros).
   auto store_x = [&](const u4 (&xv)[XP], int st) {
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
       const int idx = i * NT + t;
       const int m = idx / (KC / 8), blk = idx % (KC / 8);
-      if (idx < XPIECES && m < pre_M)
-        *reinterpret_cast<h8 *>(xs + st * 32 * LD + m * LD + 8 * blk) = wide_permute<FMT>(__builtin_bit_cast(h8, xv[i]));
+      const bool live = idx < XPIECES && m < pre_M;
+      const h8 v = wide_permute<FMT>(__builtin_bit_cast(h8, xv[i]));
+      if (live) *reinterpret_cast<h8 *>(xs + st * 32 * LD + m * LD + 8 * blk) = v;
+      if constexpr (BIASED) {
+        const float b = wide_group_sum<PPG>(wide_block_bias(v));
+        if (live && blk % PPG == 0) nbs[(st * GPC + blk / PPG) * 32 + m] = -b;
+      }
     }
   };
 
@@ -196,6 +245,10 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
   for (int u = 0; u < PD - 1; ++u)
     if (u < chunks) issue(buf[u], u);
   for (int i = t; i < LD / 8; i += NT) *reinterpret_cast<h8 *>(xs + 2 * 32 * LD + 8 * i) = h8{};
+  if constexpr (BIASED) {  // rows past M (never staged) start their groups at 0
+    for (int i = t; i < 2 * GPC * 32; i += NT)
+      if ((i & 31) >= pre_M) nbs[i] = 0.0f;
+  }
   if (chunks > 0) store_x(xv, 0);
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);  // complete at the barrier below
   __syncthreads();
@@ -207,6 +260,18 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 
+  // The lane's 16 accumulator rows m = 8 (r / 4) + 4 half + r % 4: four runs of 4 consecutive rows.
+  auto bias_start = [&](int stage, int grp) {
+    f16x c0;
+    const float *nb = nbs + (stage * GPC + grp) * 32 + 4 * half;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f4 v = *reinterpret_cast<const f4 *>(nb + 8 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c0[4 * q + e] = v[e];
+    }
+    return c0;
+  };
   auto step = [&](Buf &b, int stage) {
     const f16 *xa = xs + a_base + (arow ? stage * 32 * LD : 0);
     f16x part;
@@ -219,10 +284,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
         const h8 xa8 = *reinterpret_cast<const h8 *>(xa + 2 * CPL * l + 8 * q);
         if constexpr (GROUPED) {
           if (l % GL == 0 && q == 0) {
-            f16x zero;
+            f16x start;
+            if constexpr (BIASED) {
+              start = bias_start(stage, l / GL);
+            } else {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
-            part = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, zero, 0, 0, 0);
+              for (int r = 0; r < 16; ++r) start[r] = 0.0f;
+            }
+            part = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, start, 0, 0, 0);
           } else {
             part = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa8, bw, part, 0, 0, 0);
           }

@@ -618,9 +618,14 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
 template <int FMT, bool SCALED, int MP, int TT>
 void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
   const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT), block(256 * TT);
-  if (p.K <= 640) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT>), grid, block, 0, s, p);
-  else if (MP == 16 || p.K <= 2048) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT>), grid, block, 0, s, p);
-  else if constexpr (MP < 16) hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT>), grid, block, 0, s, p);
+#define LB_TILE_ROWS_ARGS p.codes, p.x, p.scales, p.bias, p.M, p.N, p.K, p.G, p.ldx, p
+  if (p.K <= 640)
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  else if (MP == 16 || p.K <= 2048)
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  else if constexpr (MP < 16)
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+#undef LB_TILE_ROWS_ARGS
 }
 
 template <int FMT, bool SCALED, int MP>

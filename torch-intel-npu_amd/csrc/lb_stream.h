@@ -694,8 +694,14 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
 // tiles, the scales of each tile's 16 rows too.  The reference's weights fp16(q * s) (decode8);
 // each tile's four partial sums are added in a fixed order through LDS.
 // y[m, n] = fp16(sum) (* per-row scale before rounding for per-row int8) (+ bias, fp16).
+// The operands of the first loads come as leading scalar arguments (pre_*, the same values as in
+// p), which the build preloads into registers at wave launch, so a workgroup dispatched while
+// earlier ones flood the memory system issues its loads without waiting for its argument block.
 template <int FMT, bool SCALED, int KMAX, int MP, int TT>
-__global__ __launch_bounds__(256 * TT) void tile_rows_kernel(StreamParams p) {
+__global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_codes, const f16 *pre_x,
+                                                             const f16 *pre_scales, const f16 *pre_bias, int pre_M,
+                                                             int pre_N, int pre_K, int pre_G, int pre_ldx,
+                                                             StreamParams p) {
   constexpr int CPL = FormatTraits<FMT>::CPL, BITS = FormatTraits<FMT>::BITS, T8 = CPL / 8;
   constexpr int KSTEP = 4 * CPL, KG = 4, WSTEP = KG * KSTEP;
   constexpr int D = (KMAX + WSTEP - 1) / WSTEP;      // weight loads per lane
@@ -709,6 +715,14 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(StreamParams p) {
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
   constexpr int kOutOfRange = (int)0x80000000u;
   static_assert(MP == 4 || MP == 8 || MP == 16, "MP is 4, 8 or 16");
+  // Four tiles per workgroup (1024 threads) measured slower with the preloaded operands: there the
+  // argument block is read as before (the leading arguments are then unused and not preloaded).
+  constexpr bool PRE = TT < 4;
+  const uint8_t *const codes_ = PRE ? pre_codes : p.codes;
+  const f16 *const x_ = PRE ? pre_x : p.x;
+  const f16 *const scales_ = PRE ? pre_scales : p.scales;
+  const f16 *const bias_ = PRE ? pre_bias : p.bias;
+  const int M_ = PRE ? pre_M : p.M, N_ = PRE ? pre_N : p.N, G_ = PRE ? pre_G : p.G, ldx_ = PRE ? pre_ldx : p.ldx;
   __shared__ __align__(16) f16 xs[(MP + 1) * XLD];   // MP rows, then the zero row
   __shared__ __align__(16) f16 ss[TT][SCALED ? 16 * GMAX + 8 : 8];
   __shared__ float red[TT][(KG - 1) * 64 * 4];
@@ -719,17 +733,17 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(StreamParams p) {
   const int tile = __builtin_amdgcn_readfirstlane(t >> 8);          // tile of the workgroup
   const int tt = t & 255;                                           // thread within the tile
   const int j = lane & 15, g = lane >> 4;
-  const int K = p.K;
+  const int K = PRE ? pre_K : p.K;
   const int n0 = (blockIdx.x * TT + tile) * 16;
-  const int rows = min(16, p.N - n0);  // <= 0: the tile lies past N (no loads, no stores)
+  const int rows = min(16, N_ - n0);  // <= 0: the tile lies past N (no loads, no stores)
   const int row_bytes = K * BITS / 8;
   const int blocks = K >> 3;
 
   // Epilogue operands of row n0 + j (lanes of group 0): bias, per-row scale.
   const int eoff = g == 0 && j < rows ? (n0 + j) * 2 : kOutOfRange;
-  const size_t nb = (size_t)p.N * 2;
-  const uint32_t ebias = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.bias, p.bias ? nb : 0), eoff, 0, 0);
-  const uint32_t erow = SCALED ? 0u : __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(p.scales, nb), eoff, 0, 0);
+  const size_t nb = (size_t)N_ * 2;
+  const uint32_t ebias = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(bias_, bias_ ? nb : 0), eoff, 0, 0);
+  const uint32_t erow = SCALED ? 0u : __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(scales_, nb), eoff, 0, 0);
   // Activation rows, issued before the weights (a wait for them leaves the weights in flight):
   // piece i = (row m, 8-code block b); blocks past K read zeros.
   h8 xv[XT];
@@ -737,21 +751,21 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(StreamParams p) {
   for (int i = 0; i < XT; ++i) {
     const int idx = i * NT + t;
     const int m = idx / NBR, b = idx - m * NBR;
-    const bool live = m < p.M && b < blocks;
+    const bool live = m < M_ && b < blocks;
     xv[i] = __builtin_bit_cast(
-        h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(p.x + (size_t)(live ? m : 0) * p.ldx, (size_t)K * 2),
+        h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(x_ + (size_t)(live ? m : 0) * ldx_, (size_t)K * 2),
                                                   live ? b * 16 : kOutOfRange, 0, 0));
   }
   // Scales of the tile's rows (16 x G halves), weights of this wave's k steps.
   uint32_t sreg[SC > 0 ? SC : 1];
   if constexpr (SCALED) {
     const __amdgpu_buffer_rsrc_t sb =
-        buffer_rsrc(p.scales + (size_t)(rows > 0 ? n0 : 0) * p.G, (size_t)max(rows, 0) * p.G * 2);
+        buffer_rsrc(scales_ + (size_t)(rows > 0 ? n0 : 0) * G_, (size_t)max(rows, 0) * G_ * 2);
 #pragma unroll
     for (int i = 0; i < SC; ++i) sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, (tt + 256 * i) * 2, 0, 0);
   }
   const __amdgpu_buffer_rsrc_t wb =
-      buffer_rsrc(p.codes + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)max(rows, 0) * row_bytes);
+      buffer_rsrc(codes_ + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)max(rows, 0) * row_bytes);
   u4 w[D];
 #pragma unroll
   for (int u = 0; u < D; ++u) {

@@ -844,10 +844,16 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
 #ifndef LB_TILE_ROWS_MIN_WGS
 #define LB_TILE_ROWS_MIN_WGS 224  // tile_rows_kernel groups 4 (or 2) tiles per workgroup while this many remain
 #endif
-// Tiles per tile_rows_kernel workgroup for `tiles` 16-row tiles: the staged activation rows are
-// shared by more tiles as long as the grid keeps LB_TILE_ROWS_MIN_WGS workgroups.
-inline int tile_rows_per_wg(long long tiles) {
-  return tiles >= 4ll * LB_TILE_ROWS_MIN_WGS ? 4 : tiles >= 2ll * LB_TILE_ROWS_MIN_WGS ? 2 : 1;
+#ifndef LB_TILE_ROWS_SHORT_K
+#define LB_TILE_ROWS_SHORT_K 1024  // rows of at most this many codes take at most 2 tiles per workgroup
+#endif
+// Tiles per tile_rows_kernel workgroup for `tiles` 16-row tiles of K codes: the staged activation
+// rows are shared by more tiles as long as the grid keeps LB_TILE_ROWS_MIN_WGS workgroups; four
+// tiles only over long rows (short ones stage little, and two tiles with preloaded operands
+// measured faster: the 49152x576 head at M = 4 8.9 -> 7.3 us, at M = 16 10.1 -> 9.3 us).
+inline int tile_rows_per_wg(long long tiles, long long K) {
+  if (K > LB_TILE_ROWS_SHORT_K && tiles >= 4ll * LB_TILE_ROWS_MIN_WGS) return 4;
+  return tiles >= 2ll * LB_TILE_ROWS_MIN_WGS ? 2 : 1;
 }
 
 // Launches tile_rows_kernel for 2 <= p.M <= 16 rows with M * K <= 32768 (K <= 4096): the staged

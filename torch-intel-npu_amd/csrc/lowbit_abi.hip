@@ -319,7 +319,7 @@ bool stream_rows_eligible(const lb_linear_args *a) {
 // over more tiles, measured faster.
 bool tile_rows_eligible(const lb_linear_args *a) {
   if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16 || a->K > 4096 || (a->M > 8 && a->K > 2048)) return false;
-  const int64_t tiles = (a->N + 15) / 16, wgs = (tiles + tile_rows_per_wg(tiles) - 1) / tile_rows_per_wg(tiles);
+  const int64_t tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles, a->K), wgs = (tiles + tt - 1) / tt;
   if (wgs * a->M * a->K * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
   return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
 }

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LB_ABI_VERSION 5
+#define LB_ABI_VERSION 6
 
 typedef enum lb_status {
   LB_OK = 0,
@@ -95,6 +95,18 @@ typedef enum lb_format {
  * then fp16(y + b).  The FakeQuantize graph of torch_npu_lowbit.py:224-231 as validated by
  * torch_npu_int8_demo.py:34-51.  No correction; K <= 131072. */
 #define LB_FLAG_W8A8 0x10u
+/* The workspace begins with LB_ZEROED_WORKSPACE_BYTES bytes that are zero, and the caller keeps
+ * them for this library: allocate the workspace zeroed once and reuse it.  Every call with this
+ * flag places its own scratch after those bytes and, once it has run, leaves them zero again (a
+ * launch error leaves the library failed instead).  The several-row GEMV (17..32 activation rows,
+ * N a multiple of 4 up to 262144) then adds its K slices in the kernel, in the last workgroup of
+ * each row block (one counter there per block), instead of in a second launch; the result is the
+ * same bit for bit.  lb_workspace_bytes counts the reserved bytes; a call whose plan needs no
+ * scratch needs only them.  lb_linear_noalloc ignores the flag.  Calls sharing a workspace
+ * must not overlap, as for any workspace.  No counterpart in the reference (its NPU graph owned
+ * its intermediates, torch_npu_lowbit.py:189-277). */
+#define LB_FLAG_ZEROED_WORKSPACE 0x80u
+#define LB_ZEROED_WORKSPACE_BYTES 4096u
 
 typedef struct lb_linear_args {
   uint32_t struct_size;     /* sizeof(lb_linear_args) */

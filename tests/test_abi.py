@@ -298,7 +298,7 @@ W8 = dict(format=0, group_size=128, K=128, flags=lowbit_hip.FLAG_W8A8, activatio
 
 
 @pytest.mark.parametrize('over,status,needle', [
-    (dict(flags=0x80), lowbit_hip.INVALID_ARGUMENT, 'unknown flags'),
+    (dict(flags=0x100), lowbit_hip.INVALID_ARGUMENT, 'unknown flags'),
     # compact groups (reference QuantizedLinear: at most 32 groups, packed weights only)
     (dict(K=4096, ldx=4096, group_size=32, flags=lowbit_hip.FLAG_COMPACT_GROUPS), lowbit_hip.INVALID_ARGUMENT,
      'at most 32 groups'),
@@ -376,6 +376,36 @@ def test_force_wide_workspace_holds_the_slices():
     status, size, _ = workspace(args(M=24, N=14336, K=4096, ldx=4096, ldy=14336, group_size=128, **far))
     slices = size // (24 * 14336 * 4)
     assert status == 0 and size == slices * 24 * 14336 * 4 and slices in (2, 4, 8)   # the default at 17..32 rows
+
+
+def test_zeroed_workspace_flag_reserves_its_bytes():
+    """LB_FLAG_ZEROED_WORKSPACE: every plan puts its scratch after LB_ZEROED_WORKSPACE_BYTES reserved
+    bytes (the counters), so a call that needed none needs exactly those; the header and the Python
+    constants agree; lb_linear_noalloc ignores the flag (its refusal of oversized calls is unchanged)."""
+    text = (Path(__file__).resolve().parents[1] / 'include' / 'lowbit_hip.h').read_text()
+    assert f'#define LB_FLAG_ZEROED_WORKSPACE 0x{lowbit_hip.FLAG_ZEROED_WORKSPACE:x}u' in text
+    assert f'#define LB_ZEROED_WORKSPACE_BYTES {lowbit_hip.ZEROED_WORKSPACE_BYTES}u' in text
+    Z, R = lowbit_hip.FLAG_ZEROED_WORKSPACE, lowbit_hip.ZEROED_WORKSPACE_BYTES
+    far = dict(x=0x1000000, y=0x8000000, scales=0x10000000, codes=0x20000000)
+    cases = [dict(),                                                                     # one-row GEMV: no scratch
+             dict(M=32, N=4096, K=4096, ldx=4096, ldy=4096, group_size=128, **far),      # wide, K slices
+             dict(M=24, N=14336, K=4096, ldx=4096, ldy=14336, group_size=128, **far),
+             dict(M=256, N=512, K=8192, ldx=8192, ldy=512, group_size=128, **far),       # GEMM
+             dict(W8, **far),                                                            # W8A8 activations
+             dict(K=1024, ldx=1024, group_size=128, flags=lowbit_hip.FLAG_COMPACT_GROUPS, **far)]
+    for over in cases:
+        base = args(**over)
+        status, plain, message = workspace(base)
+        assert status == 0, message
+        flagged = args(**over)
+        flagged.flags |= Z
+        status, size, message = workspace(flagged)
+        assert status == 0 and size == R + plain, (over, plain, size, message)
+    lib = lowbit_hip.library()
+    big = args(M=64, N=8200, K=1024, group_size=32, ldx=1024, ldy=8200, x=0x10000000, y=0x20000000,
+               scales=0x30000000, codes=0x40000000, flags=lowbit_hip.FLAG_COMPACT_GROUPS | Z)
+    assert lib.lb_linear_noalloc(ctypes.byref(big), None) == lowbit_hip.INVALID_ARGUMENT
+    assert 'scratch' in lib.lb_last_error().decode()
 
 
 @pytest.mark.parametrize('over', [dict(), dict(group_size=64), dict(group_size=128), dict(K=4096, ldx=4096, group_size=4096),

@@ -6,8 +6,9 @@ and a group's (or, for per-row INT8, the whole row's) integer sum is scaled in f
 is the exact x . (q s) product: the bars are those of every linear path, rel-L2 <= 1e-3 against
 the oracle and the reference's rounding-budget gate (torch_npu_lowbit_demo.py:91-106), and bit
 for bit on one-hot inputs with power-of-two scales (torch_npu_lowbit_demo.py:124-128).  Shapes
-cover one K slice and several (fp32 partials added in slice order), partial 32-row blocks, every
-group span (2, 4, 8 loads per group, and per row), bias, and strided activation / output rows.
+cover one K slice and several (fp32 partials added in slice order, by a second launch or, with a
+zeroed workspace, by each row block's last workgroup), partial 32-row blocks, every group span (2,
+4, 8 loads per group, and per row), bias, and strided activation / output rows.
 """
 import numpy as np
 import pytest
@@ -127,3 +128,71 @@ def test_wide_refuses_shapes_it_does_not_take(device, over):
     scales = torch.ones(n * (k // group), dtype=torch.float16, device=device)
     with pytest.raises(RuntimeError, match='LB_FLAG_FORCE_WIDE'):
         lowbit_hip.linear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, flags=WIDE)
+
+
+# (fmt, N, K, group, M, bias): 2, 3 and 4 K slices added in the kernel (partial last row blocks,
+# per-row INT8 with a bias, NF4), and two calls that keep the separate reduction (14 slices, more than
+# the kernel adds; N not a multiple of 4): still equal.
+IN_KERNEL = [('int4', 14336, 4096, 128, 32, False), ('int4', 300, 1024, 128, 32, False),
+             ('int4', 6000, 2048, 128, 17, False), ('int4', 8192, 1536, 128, 32, True),
+             ('int8', 14336, 4096, 4096, 24, True), ('nf4', 14336, 2048, 128, 20, False),
+             ('int4', 4096, 14336, 128, 32, False), ('int4', 1002, 2048, 256, 31, True)]
+
+
+@pytest.mark.parametrize('spec', IN_KERNEL, ids=lambda s: '-'.join(map(str, s)))
+def test_wide_slices_added_in_kernel_equal_separate_reduction(device, spec):
+    """LB_FLAG_ZEROED_WORKSPACE: the K slices added by each row block's last workgroup give the
+    separate reduction launch's output bit for bit, call after call, eagerly and replayed from a HIP
+    graph (with eager calls and synchronisations between replays), and every call leaves the
+    reserved counters zero."""
+    fmt, n, k, group, m, bias = spec
+    announce('wide in-kernel slices', spec)
+    rng = np.random.default_rng(n + k + m)
+    p = problem(rng, fmt, m, n, k, group, bias=bias)
+    codes = to_dev(np.frombuffer(p['data'], np.uint8), device)
+    scales = to_dev(np.frombuffer(p['scales'], np.float16), device)
+    kw = dict(bias=to_dev(p['bias'], device)) if bias else {}
+    x = to_dev(p['x'], device)
+    y_sep = torch.empty(m, n, dtype=torch.float16, device=device)
+    y_in = torch.empty(m, n, dtype=torch.float16, device=device)
+    probe = lowbit_hip.make_args(x, codes, scales, format=fmt, N=n, K=k, group_size=group, y=y_sep, flags=WIDE,
+                                 **kw)
+    need = lowbit_hip.workspace_bytes(probe)
+    assert need > 0  # several K slices
+    garbage = torch.full((need,), 0xA5, dtype=torch.uint8, device=device)  # no promise: separate launch
+    sep = lowbit_hip.PreparedLinear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, out=y_sep,
+                                    flags=WIDE, workspace=garbage, **kw)
+    ink = lowbit_hip.PreparedLinear(x, codes, scales, format=fmt, N=n, K=k, group_size=group, out=y_in,
+                                    flags=WIDE, **kw)
+    assert ink.args.flags & lowbit_hip.FLAG_ZEROED_WORKSPACE and not sep.args.flags & lowbit_hip.FLAG_ZEROED_WORKSPACE
+    assert ink.workspace_bytes == need + lowbit_hip.ZEROED_WORKSPACE_BYTES
+    counters = ink.workspace[:lowbit_hip.ZEROED_WORKSPACE_BYTES]
+    for step in range(4):
+        x.copy_(torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(device))
+        sep.run()
+        ink.run()
+        ink.run()  # twice: the second call starts from the counters the first left
+        torch.cuda.synchronize()
+        assert torch.equal(y_in, y_sep), step
+        assert int(counters.count_nonzero()) == 0, step
+    x.copy_(to_dev(p['x'], device))
+    ink.run()
+    torch.cuda.synchronize()
+    check(p, y_in.cpu().numpy(), f'wide in-kernel {spec}')
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        ink.run()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ink.run()
+    for step in range(3):
+        x.copy_(torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(device))
+        y_in.zero_()
+        graph.replay()
+        sep.run()
+        torch.cuda.synchronize()
+        assert torch.equal(y_in, y_sep), f'replay {step}'
+        assert int(counters.count_nonzero()) == 0, f'replay {step}'

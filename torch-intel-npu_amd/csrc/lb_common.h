@@ -141,6 +141,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, records, 0x00020000);
 }
 
+// Cache policy of a buffer access performed at the memory side past the per-XCD L2s (sc0 sc1):
+// a store is written through before it completes, a load reads what such stores and the
+// system-scope atomics wrote, whichever XCD wrote it.
+constexpr int kSysCoherent = 17;
+
 // Arguments shared by the linear kernels (device pointers, element strides).
 struct LinearParams {
   const uint8_t *codes;   // packed codes, or fp16 weights for FMT_FP16

@@ -141,10 +141,6 @@ __device__ __forceinline__ void wait_sentinel(const LayerParams &p, const uint64
   __syncthreads();
 }
 
-// Cache policy of a buffer load that reads at the memory side past the per-XCD L2s (sc0 sc1, the
-// coherence of the system-scope atomics above).
-constexpr int kSysCoherent = 17;
-
 // The workspace as a buffer over the header and every layer region.
 // Built from readfirstlane copies, so the descriptor stays in scalar registers after the
 // divergent wait that precedes its use.

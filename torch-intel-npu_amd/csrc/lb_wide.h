@@ -32,8 +32,9 @@
 // positions: the chunk's activations of all M rows are staged once per workgroup in one of two
 // LDS stages and serve the four waves; the next chunk's weights (registers) and activations are
 // loaded while the current one is computed, one barrier per chunk.  With one slice the workgroup
-// writes y; with several it writes fp32 partial sums [slice, M, N] that splitk_reduce_kernel adds
-// in slice order.
+// writes y; with several it writes fp32 partial sums [slice, M, N] that are added in slice order,
+// by splitk_reduce_kernel or, with a zeroed counter per row block, by the row block's last
+// workgroup (wide_add_slices).
 #pragma once
 #include "lb_common.h"
 
@@ -50,6 +51,8 @@ struct WideParams {
   int ldx, ldy;
   int kslice;             // codes per slice, a multiple of the chunk
   int per_row;            // INT8 with one scale per row: the scale multiplies the whole sum
+  uint32_t *tickets;      // several slices: one zero counter per row block, the slices added in the
+                          // kernel (null: splitk_reduce_kernel adds them in a launch of its own)
 };
 
 template <int FMT> struct WideTraits;
@@ -65,6 +68,86 @@ constexpr int kWideRows = 32 * kWideWaves;  // weight rows per workgroup
 constexpr int kWideLoads = 4;               // 16-byte loads per lane per position (128 bytes of a row)
 
 template <int FMT> constexpr int wide_position() { return kWideLoads * 2 * WideTraits<FMT>::CPL; }
+
+#ifndef LB_WIDE_TAIL_BATCH
+#define LB_WIDE_TAIL_BATCH 4  // slices whose partials the adding workgroup requests at once
+#endif
+// The K slices added in the kernel.  Every workgroup of a row block writes its fp32 partial sums
+// through to memory, waits until they are written, and counts itself in the block's ticket with a
+// returning system-scope atomic.  The workgroup that counts last reads every slice's partials at the
+// memory side (where the other XCDs' write-through stores are), adds them in slice order starting
+// from 0.0f -- the order and the values of splitk_reduce_kernel, so y is the same bit for bit --
+// applies the epilogue, and returns the ticket to zero for the next call.  No workgroup waits for
+// another.  The lane (col, half) holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col;
+// N is a multiple of 4 (the host launches this form only then).
+__device__ __forceinline__ void wide_add_slices(const WideParams &p, const f16x &acc, int col, int half, int row0,
+                                                int rows) {
+  constexpr int NT = 64 * kWideWaves;
+  constexpr int QUADS = kWideRows / 4;          // 4-row pieces of an activation row in a block
+  constexpr int PT = (32 * QUADS + NT - 1) / NT;  // pieces per thread (32 activation rows)
+  constexpr int kOutOfRange = (int)0x80000000u;
+  __shared__ uint32_t last;
+  const int S = gridDim.y;
+  const __amdgpu_buffer_rsrc_t pb = buffer_rsrc(p.partial, (size_t)S * p.M * p.N * 4);
+  if (col < rows) {
+    const int base = blockIdx.y * p.M * p.N + row0 + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+      const float v = acc[r];  // a value first: a bit cast of the vector element itself read element 0
+      if (m < p.M) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, (base + m * p.N) * 4, 0, kSysCoherent);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are written through
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(p.tickets + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+           (uint32_t)(S - 1);
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(p.tickets + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const int nb0 = blockIdx.x * kWideRows;
+  const int quads = min(kWideRows, p.N - nb0) / 4;
+  f4 sum[PT];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) sum[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  // SB slices' loads in flight per piece; a slice past S reads zeros, and adding +0.0f leaves
+  // every sum as it is (a sum that starts at +0.0f is never -0.0f).
+  constexpr int SB = LB_WIDE_TAIL_BATCH;
+  for (int s0 = 0; s0 < S; s0 += SB) {
+    f4 v[PT][SB];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int idx = i * NT + (int)threadIdx.x, m = idx / QUADS, q = idx - m * QUADS;
+      const bool live = m < p.M && q < quads;
+#pragma unroll
+      for (int e = 0; e < SB; ++e) {
+        const int off = live && s0 + e < S ? (((s0 + e) * p.M + m) * p.N + nb0 + 4 * q) * 4 : kOutOfRange;
+        v[i][e] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(pb, off, 0, kSysCoherent));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PT; ++i)
+#pragma unroll
+      for (int e = 0; e < SB; ++e)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sum[i][c] += v[i][e][c];
+  }
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int idx = i * NT + (int)threadIdx.x, m = idx / QUADS, q = idx - m * QUADS;
+    if (m >= p.M || q >= quads) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int n = nb0 + 4 * q + c;
+      float v = sum[i][c];
+      if (p.per_row) v *= (float)p.scales[n];
+      f16 h = (f16)v;
+      if (p.bias) h = (f16)((float)h + (float)p.bias[n]);
+      p.y[(size_t)m * p.ldy + n] = h;
+    }
+  }
+}
 
 // B operand of one 32x32x16 MFMA: the exact codes q of 8 k slots from the 16-byte load w (INT4:
 // dword t; INT8: dwords 2t, 2t + 1).
@@ -327,6 +410,10 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
 
   // Lane (col, half) holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col.
   const int n = row0 + col;
+  if (gridDim.y > 1 && p.tickets) {
+    wide_add_slices(p, acc, col, half, row0, rows);
+    return;
+  }
   if (col >= rows) return;
   if (gridDim.y > 1) {
     float *part = p.partial + (size_t)blockIdx.y * p.M * p.N + n;

@@ -45,6 +45,7 @@ struct Plan {
   size_t d_off = 0, d_bytes = 0;
   size_t part_off = 0, part_bytes = 0;
   size_t total = 0;
+  bool zeroed = false;  // LB_FLAG_ZEROED_WORKSPACE: [0, LB_ZEROED_WORKSPACE_BYTES) is zero and reserved
 };
 
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
@@ -339,6 +340,9 @@ bool tile_rows_eligible(const lb_linear_args *a) {
 #ifndef LB_WIDE_TARGET_WGS
 #define LB_WIDE_TARGET_WGS 200  // K slices: the fewest that give this many workgroups
 #endif
+#ifndef LB_WIDE_IN_KERNEL_SLICES
+#define LB_WIDE_IN_KERNEL_SLICES 4  // K slices added in the kernel (zeroed workspace) up to this many
+#endif
 #ifndef LB_WIDE_MAX_SLICES
 #define LB_WIDE_MAX_SLICES 16
 #endif
@@ -389,6 +393,7 @@ int wide_slices(int fmt, int64_t N, int64_t K) {
 Plan make_variant_plan(const lb_linear_args *a, int variant) {
   Plan pl;
   pl.variant = variant;
+  pl.zeroed = (a->flags & LB_FLAG_ZEROED_WORKSPACE) != 0;
   const int fmt = (int)a->format;
   bool eligible;
   if (variant == VAR_W8A8) {
@@ -402,7 +407,7 @@ Plan make_variant_plan(const lb_linear_args *a, int variant) {
   else if (a->flags & LB_FLAG_FORCE_GEMM) pl.path = PATH_GEMM;
   else if ((a->flags & LB_FLAG_FORCE_GEMV) || a->M <= kGemvMaxM) pl.path = PATH_GEMV;
   else pl.path = PATH_GEMM;
-  size_t off = 0;
+  size_t off = pl.zeroed ? LB_ZEROED_WORKSPACE_BYTES : 0;
   if (variant == VAR_W8A8 && pl.path != PATH_GENERIC) {
     pl.xq_off = off;
     off = round_up(off + (size_t)a->M * a->K, 256);
@@ -424,6 +429,7 @@ Plan make_variant_plan(const lb_linear_args *a, int variant) {
 Plan make_plan(const lb_linear_args *a, bool eligible) {
   Plan pl;
   const int fmt = (int)a->format;
+  pl.zeroed = (a->flags & LB_FLAG_ZEROED_WORKSPACE) != 0;
   if (a->flags & LB_FLAG_FORCE_STREAM) {  // validated: the stream kernel takes the shape
     pl.path = a->M == 1 ? PATH_ROW : PATH_STREAM;
   } else if (a->flags & LB_FLAG_FORCE_WIDE) {  // validated: the wide kernel takes the shape
@@ -445,7 +451,7 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
   } else {
     pl.path = PATH_GEMM;
   }
-  size_t off = 0;
+  size_t off = pl.zeroed ? LB_ZEROED_WORKSPACE_BYTES : 0;
   if (a->rank > 0 && pl.path != PATH_ROW) {
     pl.z_off = off;
     pl.z_bytes = (size_t)a->M * a->rank * 2;
@@ -541,7 +547,7 @@ lb_status validate(const lb_linear_args *a, bool check_workspace, Plan *plan) {
 
   constexpr uint32_t kForce =
       LB_FLAG_FORCE_GEMV | LB_FLAG_FORCE_GEMM | LB_FLAG_FORCE_GENERIC | LB_FLAG_FORCE_STREAM | LB_FLAG_FORCE_WIDE;
-  if (a->flags & ~(kForce | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8))
+  if (a->flags & ~(kForce | LB_FLAG_COMPACT_GROUPS | LB_FLAG_W8A8 | LB_FLAG_ZEROED_WORKSPACE))
     return fail(LB_INVALID_ARGUMENT, "lb_linear: unknown flags 0x%x", a->flags);
   if ((a->flags & LB_FLAG_FORCE_GEMV) && a->M > kGemvMaxM)
     return fail(LB_INVALID_ARGUMENT, "lb_linear: LB_FLAG_FORCE_GEMV needs M <= %d", kGemvMaxM);
@@ -944,8 +950,13 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     wp.per_row = p.per_row;
     wp.partial = plan.splits > 1 ? reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) + plan.part_off)
                                  : nullptr;
+    // With the zeroed counters the kernel adds the slices itself (one counter per 256-row block),
+    // up to LB_WIDE_IN_KERNEL_SLICES of them (the adding workgroup reads every slice's partials).
+    const bool in_kernel = plan.splits > 1 && plan.splits <= LB_WIDE_IN_KERNEL_SLICES && plan.zeroed && a->N % 4 == 0 &&
+                           (a->N + kWideRows - 1) / kWideRows <= (int64_t)(LB_ZEROED_WORKSPACE_BYTES / 4);
+    wp.tickets = in_kernel ? static_cast<uint32_t *>(a->workspace) : nullptr;
     launch_wide(wp, fmt, wide_group_loads(fmt, a->K, a->group_size), plan.splits, s);
-    if (plan.splits > 1) {  // partials [slice, M, N] -> y in slice order (per-row scale, bias)
+    if (plan.splits > 1 && !in_kernel) {  // partials [slice, M, N] -> y in slice order (per-row scale, bias)
       p.partial = wp.partial;
       p.splits = plan.splits;
       const size_t count = (size_t)p.M * p.N;
@@ -1017,10 +1028,15 @@ lb_status lb_linear_noalloc(const lb_linear_args *a, void *stream) {
   Plan plan;
   const lb_status st = validate(a, false, &plan);
   if (st != LB_OK) return st;
+  lb_linear_args b = *a;  // validated: struct_size covers the struct
+  b.flags &= ~LB_FLAG_ZEROED_WORKSPACE;  // the shared scratch promises nothing about its contents
+  if (b.flags != a->flags) {
+    const lb_status again = validate(&b, false, &plan);
+    if (again != LB_OK) return again;
+  }
   if (plan.total > LB_NOALLOC_SCRATCH_BYTES)
     return fail(LB_INVALID_ARGUMENT, "lb_linear_noalloc: the call needs %zu bytes of scratch; the allocation-free "
                 "entry holds %zu (use lb_linear with a workspace)", plan.total, (size_t)LB_NOALLOC_SCRATCH_BYTES);
-  lb_linear_args b = *a;
   if (plan.total > 0) {
     void *ptr = nullptr;
     const lb_status got = scratch_address(static_cast<hipStream_t>(stream), &ptr);

@@ -16,11 +16,14 @@ import torch
 
 LIBRARY_PATH = Path(os.environ.get('LOWBIT_HIP_LIBRARY', Path(__file__).resolve().parent.parent / 'liblowbit_hip.so'))
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 OK, INVALID_ARGUMENT, OUT_OF_MEMORY, UNSUPPORTED, DEVICE_FAILED, INTERNAL = 0, 1, 2, 5, 10, 12
 FORMATS = {'int8': 0, 'int4': 1, 'nf4': 2, 'fp16': 3}
 FLAG_FORCE_GEMV, FLAG_FORCE_GEMM, FLAG_FORCE_GENERIC, FLAG_FORCE_STREAM, FLAG_FORCE_WIDE = 0x1, 0x2, 0x4, 0x20, 0x40
 FLAG_COMPACT_GROUPS, FLAG_W8A8 = 0x8, 0x10
+# LB_FLAG_ZEROED_WORKSPACE / LB_ZEROED_WORKSPACE_BYTES: the workspace starts with that many zero bytes
+# the library keeps zero (its counters); the wrappers set it on the workspaces they allocate.
+FLAG_ZEROED_WORKSPACE, ZEROED_WORKSPACE_BYTES = 0x80, 4096
 EXPORTS = ('lb_abi_version', 'lb_status_name', 'lb_last_error', 'lb_failed', 'lb_mark_failed',
            'lb_workspace_bytes', 'lb_linear', 'lb_linear_noalloc', 'lb_unpack_codes', 'lb_dequantize')
 NOALLOC_SCRATCH_BYTES = 32 << 20   # LB_NOALLOC_SCRATCH_BYTES
@@ -373,10 +376,17 @@ def linear(x, codes, scales, *, format, N, K, group_size, bias=None, down=None, 
     need = workspace_bytes(args)
     if need:
         if workspace is None or workspace.numel() < need:
-            workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
+            workspace = zeroed_workspace(args, x.device)
         args.workspace, args.workspace_bytes = _ptr(workspace), workspace.numel()
     _check(library().lb_linear(ctypes.byref(args), _stream(x.device)), 'lb_linear')
     return y
+
+
+def zeroed_workspace(args, device):
+    """A workspace allocated zeroed for `args`, with FLAG_ZEROED_WORKSPACE added to args.flags (the
+    library keeps its first ZEROED_WORKSPACE_BYTES zero across the calls that use it)."""
+    args.flags |= FLAG_ZEROED_WORKSPACE
+    return torch.zeros(workspace_bytes(args), dtype=torch.uint8, device=device)
 
 
 def linear_noalloc(x, codes, scales, *, out, format, N, K, group_size, bias=None, down=None, up=None, rank=0,
@@ -444,9 +454,11 @@ class PreparedLinear:
         need = workspace_bytes(self.args)
         if need:
             if workspace is None or workspace.numel() < need:
-                workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
+                workspace = zeroed_workspace(self.args, x.device)
+                need = workspace.numel()
             self.args.workspace, self.args.workspace_bytes = _ptr(workspace), workspace.numel()
             self._keep.append(workspace)
+        self.workspace = workspace if need else None
         self.workspace_bytes = need
         self.out = out
         self._ref = ctypes.byref(self.args)

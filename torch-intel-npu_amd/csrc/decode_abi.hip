@@ -614,23 +614,31 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
   else launch_stream_wide_f<FMT_INT8, false>(p, s);
 }
 
-// tile_rows_kernel: TT 16-row tiles per workgroup, the staged row length for K.
+// tile_rows_kernel: TT 16-row tiles per workgroup, the staged row length for K (or the slice).
 template <int FMT, bool SCALED, int MP, int TT>
 void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
-  const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT), block(256 * TT);
+  const int slices = p.kslice > 0 ? p.K / p.kslice : 1;
+  const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT, slices), block(256 * TT);
 #define LB_TILE_ROWS_ARGS p.codes, p.x, p.scales, p.bias, p.M, p.N, p.K, p.G, p.ldx, p
-  if (p.K <= 640)
-    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
-  else if (MP == 16 || p.K <= 2048)
-    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
-  else if constexpr (MP < 16)
-    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  if (slices > 1) {
+    if constexpr (MP < 16)
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+    else
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  } else if (p.K <= 640) {
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  } else if (MP == 16 || p.K <= 2048) {
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  } else if constexpr (MP < 16) {
+    hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  }
 #undef LB_TILE_ROWS_ARGS
 }
 
 template <int FMT, bool SCALED, int MP>
 void launch_tile_rows_mp(const StreamParams &p, hipStream_t s) {
-  const int tt = tile_rows_per_wg((p.N + 15) / 16, p.K);
+  const int slices = p.kslice > 0 ? p.K / p.kslice : 1;
+  const int tt = tile_rows_per_wg((long long)(p.N + 15) / 16 * slices, p.kslice > 0 ? p.kslice : p.K);
   if (tt == 4) launch_tile_rows_tt<FMT, SCALED, MP, 4>(p, s);
   else if (tt == 2) launch_tile_rows_tt<FMT, SCALED, MP, 2>(p, s);
   else launch_tile_rows_tt<FMT, SCALED, MP, 1>(p, s);

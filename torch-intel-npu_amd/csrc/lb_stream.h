@@ -46,6 +46,10 @@ struct StreamParams {
   int M, N, K, G, group_shift;
   int ldx, ldy;
   int tiles, chunks;      // 16-row tiles; chunks per tile row
+  int kslice;             // tile_rows_kernel over K slices (grid y): codes per slice (0: none)
+  float *partial;         // K slices: fp32 partial sums [slices, M, N]
+  uint32_t *tickets;      // K slices: one zero counter per workgroup column, the slices added in the
+                          // kernel (null: splitk_reduce_kernel adds them in a launch of its own)
 };
 
 // Slot permutation of an 8-code group, the activation factor and the bias of each slot.
@@ -686,6 +690,75 @@ __global__ __launch_bounds__(64 * WAVES) void stream_wide_kernel(StreamParams p)
 // Launches stream_wide_kernel for 17 <= p.M <= 32 rows.
 void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t stream);
 
+// End of a SLICED tile_rows_kernel workgroup (every thread calls it).  Wave 0 of each tile adds the
+// other waves' sums (red, the order of the unsliced kernel) and writes the tile's fp32 partials of
+// its slice.  Without tickets that is all (splitk_reduce_kernel follows).  With them the partials are
+// written with system-scope coherent stores (as wide_add_slices does), and the workgroup counts itself
+// in its tile column's ticket with a returning system-scope atomic once every wave's stores are
+// complete; the one that counts last (gridDim.y - 1) reads the column's partials with coherent loads,
+// adds the slices in slice order from 0.0f (splitk_reduce_kernel's order and values: the same y bit
+// for bit), applies the epilogue (per-row scale, fp16, bias) and returns the ticket to zero.  No
+// workgroup waits for another.
+template <int TT, bool SCALED>
+__device__ __forceinline__ void tile_rows_slices(const StreamParams &p, f4 acc, const float *red, int wave, int lane,
+                                                 int n0, int rows, int M, int N) {
+  constexpr int kOutOfRange = (int)0x80000000u;
+  constexpr int SMAX = 8;  // slices whose partials the adding workgroup requests at once
+  __shared__ uint32_t last;
+  const int S = gridDim.y, j = lane & 15, g = lane >> 4;
+  const bool through = p.tickets != nullptr;
+  const __amdgpu_buffer_rsrc_t pb = buffer_rsrc(p.partial, (size_t)S * M * N * 4);
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = ((acc[r] + red[lane * 4 + r]) + red[(64 + lane) * 4 + r]) + red[(128 + lane) * 4 + r];
+    if (j < rows) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * g + r;
+        const float v = acc[r];
+        const int off = m < M ? ((blockIdx.y * M + m) * N + n0 + j) * 4 : kOutOfRange;
+        if (through) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, kSysCoherent);
+        else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, 0);
+      }
+    }
+  }
+  if (!through) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are written through
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(p.tickets + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+           (uint32_t)(S - 1);
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(p.tickets + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // Thread e: tile e / (16 M), activation row (e / 16) % M, column e % 16 of the workgroup's tiles.
+  const int e = threadIdx.x, tl = e / (16 * M), m = (e / 16) - tl * M, n = (blockIdx.x * TT + tl) * 16 + (e & 15);
+  const bool live = tl < TT && n < N;
+  float sum = 0.0f;
+  for (int s0 = 0; s0 < S; s0 += SMAX) {
+    float v[SMAX];
+#pragma unroll
+    for (int q = 0; q < SMAX; ++q) {
+      const int off = live && s0 + q < S ? (((s0 + q) * M + m) * N + n) * 4 : kOutOfRange;
+      v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pb, off, 0, kSysCoherent));
+    }
+    // a slice past S reads +0.0f, which leaves the sum as it is (a sum that starts at +0.0f is
+    // never -0.0f)
+#pragma unroll
+    for (int q = 0; q < SMAX; ++q) sum += v[q];
+  }
+  if (!live) return;
+  if constexpr (!SCALED) {
+    sum *= (float)p.scales[n];  // per-row INT8: the row's scale
+    // the fp32 product, then fp16 (two roundings, as splitk_reduce_kernel), not one mixed-precision
+    // multiply rounding straight to fp16
+    asm volatile("" : "+v"(sum));
+  }
+  f16 h = (f16)sum;
+  if (p.bias) h = (f16)((float)h + (float)p.bias[n]);
+  p.y[(size_t)m * p.ldy + n] = h;
+}
+
 // TT 16-row tiles per workgroup for 2 .. MP activation rows (MP = 4, 8 or 16), the multi-row
 // form of the single-tile one-row kernels: four waves per tile split K (wave 4 i + w of tile i
 // takes k steps w, w + 4, ...), every weight load of a lane is issued straight-line before the
@@ -697,7 +770,11 @@ void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStrea
 // The operands of the first loads come as leading scalar arguments (pre_*, the same values as in
 // p), which the build preloads into registers at wave launch, so a workgroup dispatched while
 // earlier ones flood the memory system issues its loads without waiting for its argument block.
-template <int FMT, bool SCALED, int KMAX, int MP, int TT>
+// SLICED: rows longer than KMAX are cut into p.kslice-code slices (grid y; a slice is whole scale
+// groups), each staged and summed as above into fp32 partials [slice, M, N]; with p.tickets the
+// last workgroup of a tile column to count itself adds the slices in slice order (as
+// splitk_reduce_kernel does otherwise) and writes y.
+template <int FMT, bool SCALED, int KMAX, int MP, int TT, bool SLICED>
 __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_codes, const f16 *pre_x,
                                                              const f16 *pre_scales, const f16 *pre_bias, int pre_M,
                                                              int pre_N, int pre_K, int pre_G, int pre_ldx,
@@ -737,7 +814,13 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
   const int n0 = (blockIdx.x * TT + tile) * 16;
   const int rows = min(16, N_ - n0);  // <= 0: the tile lies past N (no loads, no stores)
   const int row_bytes = K * BITS / 8;
-  const int blocks = K >> 3;
+  // This workgroup's codes of each row: [kbeg, kbeg + KS) (the whole row unless SLICED), and the
+  // scale groups of that range staged per row (GS; g0 the first).
+  const int kbeg = SLICED ? (int)blockIdx.y * p.kslice : 0;
+  const int KS = SLICED ? p.kslice : K;
+  const int GS = SLICED && SCALED ? KS >> p.group_shift : G_;
+  const int g0 = SLICED && SCALED ? kbeg >> p.group_shift : 0;
+  const int blocks = KS >> 3;
 
   // Epilogue operands of row n0 + j (lanes of group 0): bias, per-row scale.
   const int eoff = g == 0 && j < rows ? (n0 + j) * 2 : kOutOfRange;
@@ -753,7 +836,7 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
     const int m = idx / NBR, b = idx - m * NBR;
     const bool live = m < M_ && b < blocks;
     xv[i] = __builtin_bit_cast(
-        h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(x_ + (size_t)(live ? m : 0) * ldx_, (size_t)K * 2),
+        h8, __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(x_ + (size_t)(live ? m : 0) * ldx_ + kbeg, (size_t)KS * 2),
                                                   live ? b * 16 : kOutOfRange, 0, 0));
   }
   // Scales of the tile's rows (16 x G halves), weights of this wave's k steps.
@@ -762,7 +845,15 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
     const __amdgpu_buffer_rsrc_t sb =
         buffer_rsrc(scales_ + (size_t)(rows > 0 ? n0 : 0) * G_, (size_t)max(rows, 0) * G_ * 2);
 #pragma unroll
-    for (int i = 0; i < SC; ++i) sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, (tt + 256 * i) * 2, 0, 0);
+    for (int i = 0; i < SC; ++i) {
+      const int e = tt + 256 * i;  // staged entry: row e / GS, group e % GS of the slice
+      int off = e * 2;
+      if constexpr (SLICED) {
+        const int r = e / GS;
+        off = e < 16 * GS ? (r * G_ + g0 + (e - r * GS)) * 2 : kOutOfRange;
+      }
+      sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sb, off, 0, 0);
+    }
   }
   const __amdgpu_buffer_rsrc_t wb =
       buffer_rsrc(codes_ + (size_t)(rows > 0 ? n0 : 0) * row_bytes, (size_t)max(rows, 0) * row_bytes);
@@ -770,7 +861,8 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int k = (wave + KG * u) * KSTEP + g * CPL;
-    w[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wb, k < K ? j * row_bytes + k * BITS / 8 : kOutOfRange, 0, 0));
+    w[u] = __builtin_bit_cast(
+        u4, __builtin_amdgcn_raw_buffer_load_b128(wb, k < KS ? j * row_bytes + (kbeg + k) * BITS / 8 : kOutOfRange, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);  // no use of the loaded data is scheduled above this point
 #pragma unroll
@@ -799,13 +891,13 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
-    if (kb >= K) break;  // wave-uniform
+    if (kb >= KS) break;  // wave-uniform
     asm volatile("" : "+v"(w[u]));  // decode here, not at the load
     h2 s2 = {(f16)1.0f, (f16)1.0f};
     if constexpr (SCALED) {
-      // past K the scale is zero (index past the row's groups reads the next row or the pad,
-      // and the codes there are zero: only the zero scale makes fp16(q * s) zero for every format)
-      const f16 sc = kb + g * CPL < K ? ss[tile][j * p.G + ((kb + g * CPL) >> p.group_shift)] : (f16)0.0f;
+      // past the row (or slice) the scale is zero (index past the row's groups reads the next row or
+      // the pad, and the codes there are zero: only the zero scale makes fp16(q * s) zero for every format)
+      const f16 sc = kb + g * CPL < KS ? ss[tile][j * GS + ((kb + g * CPL) >> p.group_shift)] : (f16)0.0f;
       s2 = h2{sc, sc};
     }
 #pragma unroll
@@ -820,6 +912,10 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
     for (int r = 0; r < 4; ++r) red[tile][((wave - 1) * 64 + lane) * 4 + r] = acc[r];
   }
   __syncthreads();
+  if constexpr (SLICED) {
+    tile_rows_slices<TT, SCALED>(p, acc, red[tile], wave, lane, n0, rows, M_, N_);
+    return;
+  }
   if (wave > 0) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -856,8 +952,25 @@ inline int tile_rows_per_wg(long long tiles, long long K) {
   return tiles >= 2ll * LB_TILE_ROWS_MIN_WGS ? 2 : 1;
 }
 
-// Launches tile_rows_kernel for 2 <= p.M <= 16 rows with M * K <= 32768 (K <= 4096): the staged
-// rows are loaded in one batch of at most 16 loads per thread.
+// K slices of tile_rows_kernel for rows longer than it stages whole (4096 codes up to 8
+// activation rows, 2048 beyond): the fewest, at most 16, that cut K into equal slices of whole
+// 512-code steps and whole scale groups (any length for per-row scales); 1 when the row fits, 0 when
+// there is no such cut.
+inline int tile_rows_slices_for(int M, long long K, long long group, bool per_row) {
+  const long long kmax = M <= 8 ? 4096 : 2048;
+  if (K <= kmax) return 1;
+  for (int s = 2; s <= 16; ++s) {
+    if (K % s) continue;
+    const long long ks = K / s;
+    if (ks <= kmax && ks % 512 == 0 && (per_row || ks % group == 0)) return s;
+  }
+  return 0;
+}
+
+// Launches tile_rows_kernel for 2 <= p.M <= 16 rows with M * K <= 32768 (K <= 4096), or over K
+// slices of p.kslice codes (p.kslice > 0, the count from tile_rows_slices_for, fp32 partials in
+// p.partial; with p.tickets the kernel adds them, else the caller launches splitk_reduce_kernel):
+// the staged rows are loaded in one batch of at most 16 loads per thread.
 void launch_tile_rows(const StreamParams &p, int format, bool scaled, hipStream_t stream);
 
 // Launches stream_rows_kernel for 2 <= p.M <= 16 rows (K <= 4096, groups of at least 32 codes

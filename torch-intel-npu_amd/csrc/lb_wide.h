@@ -73,13 +73,16 @@ template <int FMT> constexpr int wide_position() { return kWideLoads * 2 * WideT
 #define LB_WIDE_TAIL_BATCH 4  // slices whose partials the adding workgroup requests at once
 #endif
 // The K slices added in the kernel.  Every workgroup of a row block writes its fp32 partial sums
-// through to memory, waits until they are written, and counts itself in the block's ticket with a
-// returning system-scope atomic.  The workgroup that counts last reads every slice's partials at the
-// memory side (where the other XCDs' write-through stores are), adds them in slice order starting
-// from 0.0f -- the order and the values of splitk_reduce_kernel, so y is the same bit for bit --
-// applies the epilogue, and returns the ticket to zero for the next call.  No workgroup waits for
-// another.  The lane (col, half) holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col;
-// N is a multiple of 4 (the host launches this form only then).
+// with system-scope coherent stores (sc0 sc1: written through to memory, as a relaxed system-scope
+// atomic store is), waits until they are complete, and counts itself in the block's ticket with a
+// returning system-scope atomic.  The workgroup that counts last reads every slice's partials with
+// system-scope coherent loads, adds them in slice order starting from 0.0f -- the order and the
+// values of splitk_reduce_kernel, so y is the same bit for bit -- applies the epilogue, and returns
+// the ticket to zero for the next call.  No workgroup waits for another, and every access to the
+// partials is coherent in itself, so no cache-wide write-back or invalidate is needed (agent-scope
+// release / acquire fences around the count measured 12-14 us more per call).  The lane (col, half)
+// holds rows m = 8 (r / 4) + 4 half + r % 4 of weight row row0 + col; N is a multiple of 4 (the host
+// launches this form only then).
 __device__ __forceinline__ void wide_add_slices(const WideParams &p, const f16x &acc, int col, int half, int row0,
                                                 int rows) {
   constexpr int NT = 64 * kWideWaves;

@@ -318,10 +318,20 @@ bool stream_rows_eligible(const lb_linear_args *a) {
 // 2 or 4 tiles, so the workgroups together read the activations that many times: past
 // LB_TILE_ROWS_MAX_X_BYTES of those reads the tiled GEMV, whose workgroups share the staged rows
 // over more tiles, measured faster.
+// Longer rows go in K slices (tile_rows_slices_for: equal slices of whole 512-code steps and scale
+// groups, fp32 partials added in slice order).
+int tile_rows_slices(const lb_linear_args *a) {
+  const bool per_row = a->format == LB_FORMAT_INT8 && a->group_size == a->K;
+  return tile_rows_slices_for((int)a->M, a->K, a->group_size, per_row);
+}
+
 bool tile_rows_eligible(const lb_linear_args *a) {
-  if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16 || a->K > 4096 || (a->M > 8 && a->K > 2048)) return false;
-  const int64_t tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles, a->K), wgs = (tiles + tt - 1) / tt;
-  if (wgs * a->M * a->K * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
+  if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16) return false;
+  const int slices = tile_rows_slices(a);
+  if (slices < 1) return false;
+  const int64_t ks = a->K / slices, tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles * slices, ks);
+  const int64_t wgs = (tiles + tt - 1) / tt * slices;
+  if (wgs * a->M * ks * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
   return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
 }
 
@@ -466,6 +476,15 @@ Plan make_plan(const lb_linear_args *a, bool eligible) {
     const GemmShape gs = gemm_shape(a->M, a->N, a->K, 1, true);
     pl.splits = gs.splits;
     pl.kslice = gs.kslice;
+    if (pl.splits > 1) {
+      pl.part_off = off;
+      pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
+      off = round_up(off + pl.part_bytes, 256);
+    }
+  }
+  if (pl.path == PATH_TILE) {
+    pl.splits = tile_rows_slices(a);
+    pl.kslice = (int)(a->K / pl.splits);
     if (pl.splits > 1) {
       pl.part_off = off;
       pl.part_bytes = (size_t)pl.splits * a->M * a->N * 4;
@@ -979,8 +998,23 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     sp.ldx = p.ldx;
     sp.ldy = p.ldy;
     sp.tiles = (int)((a->N + 15) / 16);
-    if (plan.path == PATH_TILE) launch_tile_rows(sp, fmt, !p.per_row, s);
-    else if (a->M > 16) launch_stream_wide(sp, fmt, !p.per_row, s);
+    if (plan.path == PATH_TILE) {
+      bool in_kernel = false;
+      if (plan.splits > 1) {  // K slices: fp32 partials, added by the kernel or by a second launch
+        const int64_t tt = tile_rows_per_wg((int64_t)sp.tiles * plan.splits, plan.kslice);
+        in_kernel = plan.zeroed && (sp.tiles + tt - 1) / tt <= (int64_t)(LB_ZEROED_WORKSPACE_BYTES / 4);
+        sp.kslice = plan.kslice;
+        sp.partial = reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) + plan.part_off);
+        sp.tickets = in_kernel ? static_cast<uint32_t *>(a->workspace) : nullptr;
+      }
+      launch_tile_rows(sp, fmt, !p.per_row, s);
+      if (plan.splits > 1 && !in_kernel) {  // partials [slice, M, N] -> y in slice order (per-row scale, bias)
+        p.partial = sp.partial;
+        p.splits = plan.splits;
+        const size_t count = (size_t)p.M * p.N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p);
+      }
+    } else if (a->M > 16) launch_stream_wide(sp, fmt, !p.per_row, s);
     else if (a->M >= LB_STREAM_ROWS_DECODE_MIN_M) launch_stream_rows(sp, fmt, !p.per_row, s);
     else launch_stream(sp, fmt, !p.per_row, stream_group_span(fmt, a->K, a->group_size), s);
     return launch_status("lb_linear");

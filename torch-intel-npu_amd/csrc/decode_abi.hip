@@ -621,10 +621,10 @@ void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
   const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT, slices), block(256 * TT);
 #define LB_TILE_ROWS_ARGS p.codes, p.x, p.scales, p.bias, p.M, p.N, p.K, p.G, p.ldx, p
   if (slices > 1) {
-    if constexpr (MP < 16)
-      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
-    else
+    if (MP == 16 || p.kslice <= 2048)
       hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+    else if constexpr (MP < 16)
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 4096, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
   } else if (p.K <= 640) {
     hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
   } else if (MP == 16 || p.K <= 2048) {

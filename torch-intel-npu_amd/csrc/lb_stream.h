@@ -956,8 +956,15 @@ inline int tile_rows_per_wg(long long tiles, long long K) {
 // activation rows, 2048 beyond): the fewest, at most 16, that cut K into equal slices of whole
 // 512-code steps and whole scale groups (any length for per-row scales); 1 when the row fits, 0 when
 // there is no such cut.
+#ifndef LB_TILE_ROWS_KMAX8
+#define LB_TILE_ROWS_KMAX8 4096  // longest row tile_rows_kernel stages whole for up to 8 activation rows
+#endif
+#ifndef LB_TILE_ROWS_KMAX16
+#define LB_TILE_ROWS_KMAX16 2048  // ... and for 9..16 rows
+#endif
+static_assert(LB_TILE_ROWS_KMAX8 <= 4096 && LB_TILE_ROWS_KMAX16 <= 2048, "the staged lengths the launches instantiate");
 inline int tile_rows_slices_for(int M, long long K, long long group, bool per_row) {
-  const long long kmax = M <= 8 ? 4096 : 2048;
+  const long long kmax = M <= 8 ? LB_TILE_ROWS_KMAX8 : LB_TILE_ROWS_KMAX16;
   if (K <= kmax) return 1;
   for (int s = 2; s <= 16; ++s) {
     if (K % s) continue;

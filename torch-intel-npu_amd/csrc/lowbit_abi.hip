@@ -342,7 +342,8 @@ bool tile_rows_eligible(const lb_linear_args *a) {
 #define LB_WIDE_MIN_BYTES (4ll << 20)  // ... over weights of at least this many bytes
 #endif
 #ifndef LB_WIDE_MID_M
-#define LB_WIDE_MID_M 9  // and from this many rows over weights of LB_WIDE_MID_BYTES up to the streaming sizes
+#define LB_WIDE_MID_M 17  // and from this many rows over weights of LB_WIDE_MID_BYTES up to the streaming sizes
+                          // (none by default: 9..16 rows measured faster on tile_rows_kernel over K slices)
 #endif
 #ifndef LB_WIDE_MID_BYTES
 #define LB_WIDE_MID_BYTES (16ll << 20)
@@ -377,8 +378,8 @@ bool wide_shape_ok(const lb_linear_args *a) {
   return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
 }
 
-// 17..32 rows over >= 4 MB; 9..16 rows over 16..64 MB (the streaming kernels keep larger weights,
-// where they measured faster at these rows, and the one-tile kernels smaller ones).
+// 17..32 rows over >= 4 MB; with LB_WIDE_MID_M lowered, also fewer rows over LB_WIDE_MID_BYTES up
+// to the streaming sizes (the streaming kernels keep larger weights, where they measured faster).
 bool wide_eligible(const lb_linear_args *a) {
   if (a->M < LB_WIDE_MID_M || !wide_shape_ok(a)) return false;
   const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;

@@ -601,6 +601,14 @@ __device__ __forceinline__ void layer_tile_role(const LayerParams &p, const Laye
 }
 
 // ---------------------------------------------------------------- attention
+#ifndef LB_ATTN_FAST_EXP
+#define LB_ATTN_FAST_EXP 1  // the hardware exponential (v_exp_f32) in the softmax
+#endif
+__device__ __forceinline__ float attn_exp(float x) {
+  if constexpr (LB_ATTN_FAST_EXP) return __expf(x);
+  else return expf(x);
+}
+
 // Query head h, output dims [d0, d0 + kSliceDims): the staging of decode_attention_kernel on q, k
 // and v rows read from the q|k|v words; the output dims are published as att words.
 __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const LayerCtx &c, const LayerWeights &W,
@@ -736,12 +744,12 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
   for (int i = 0; i < kScoreSlots; ++i) {
     ev[i] = 0.0f;
     if (t + 256 * i <= pos) {
-      ev[i] = expf(scv[i] - lmax);
+      ev[i] = attn_exp(scv[i] - lmax);
       lsum += ev[i];
     }
   }
   for (int s = t + 256 * kScoreSlots; s <= pos; s += 256) {
-    const float e = expf(sc[s] - lmax);
+    const float e = attn_exp(sc[s] - lmax);
     sc[s] = e;
     lsum += e;
   }
@@ -754,8 +762,8 @@ __device__ __forceinline__ void layer_attention_role(const LayerParams &p, const
   const float m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
   float total = 0.0f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) total += wred[4 + w] * expf(wred[w] - m);
-  const float f = expf(lmax - m) / total;
+  for (int w = 0; w < 4; ++w) total += wred[4 + w] * attn_exp(wred[w] - m);
+  const float f = attn_exp(lmax - m) / total;
 #pragma unroll
   for (int i = 0; i < kScoreSlots; ++i)
     if (t + 256 * i <= pos) sc[t + 256 * i] = (float)(f16)(ev[i] * f);

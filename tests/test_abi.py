@@ -378,6 +378,23 @@ def test_force_wide_workspace_holds_the_slices():
     assert status == 0 and size == slices * 24 * 14336 * 4 and slices in (2, 4, 8)   # the default at 17..32 rows
 
 
+@pytest.mark.parametrize('m,n,k,group,fmt,slices', [
+    (8, 4096, 14336, 128, 1, 4),     # 4 x 3584 codes (up to 8 rows: 4096 staged)
+    (2, 576, 12288, 32, 1, 3),       # 3 x 4096
+    (16, 1024, 14336, 128, 1, 7),    # 7 x 2048 (beyond 8 rows: 2048 staged)
+    (12, 600, 4096, 128, 2, 2),      # NF4, 2 x 2048
+    (8, 1030, 8192, 8192, 0, 2),     # per-row INT8: any slice length
+    (8, 4096, 4096, 128, 1, 1),      # staged whole: no workspace
+])
+def test_tile_rows_k_slices_take_their_partials(m, n, k, group, fmt, slices):
+    """2..16 rows over rows longer than tile_rows_kernel stages whole: equal K slices of whole
+    512-code steps and scale groups, each writing fp32 partials [slices, M, N] into the workspace."""
+    far = dict(x=0x1000000, y=0x8000000, scales=0x10000000, codes=0x20000000)
+    status, size, message = workspace(args(M=m, N=n, K=k, ldx=k, ldy=n, group_size=group, format=fmt, **far))
+    want = 0 if slices == 1 else -(-slices * m * n * 4 // 256) * 256
+    assert status == 0 and size == want, (size, want, message)
+
+
 def test_zeroed_workspace_flag_reserves_its_bytes():
     """LB_FLAG_ZEROED_WORKSPACE: every plan puts its scratch after LB_ZEROED_WORKSPACE_BYTES reserved
     bytes (the counters), so a call that needed none needs exactly those; the header and the Python

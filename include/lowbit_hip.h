@@ -98,13 +98,14 @@ typedef enum lb_format {
 /* The workspace begins with LB_ZEROED_WORKSPACE_BYTES bytes that are zero, and the caller keeps
  * them for this library: allocate the workspace zeroed once and reuse it.  Every call with this
  * flag places its own scratch after those bytes and, once it has run, leaves them zero again (a
- * launch error leaves the library failed instead).  The several-row GEMV (17..32 activation rows,
- * N a multiple of 4 up to 262144) then adds its K slices in the kernel, in the last workgroup of
- * each row block (one counter there per block), instead of in a second launch; the result is the
- * same bit for bit.  lb_workspace_bytes counts the reserved bytes; a call whose plan needs no
- * scratch needs only them.  lb_linear_noalloc ignores the flag.  Calls sharing a workspace
- * must not overlap, as for any workspace.  No counterpart in the reference (its NPU graph owned
- * its intermediates, torch_npu_lowbit.py:189-277). */
+ * launch error leaves the library failed instead).  The GEMVs that split K into slices then add
+ * the slices in the kernel, in the last workgroup of each block of output rows (one counter there
+ * per block), instead of in a second launch, with the same result bit for bit: the 17..32-row
+ * kernel (up to 4 slices, N a multiple of 4 up to 262144) and the 2..16-row one-tile kernel over
+ * rows longer than it stages whole (up to 1024 workgroup columns).  lb_workspace_bytes counts the
+ * reserved bytes; a call whose plan needs no scratch needs only them.  lb_linear_noalloc ignores
+ * the flag.  Calls sharing a workspace must not overlap, as for any workspace.  No counterpart in
+ * the reference (its NPU graph owned its intermediates, torch_npu_lowbit.py:189-277). */
 #define LB_FLAG_ZEROED_WORKSPACE 0x80u
 #define LB_ZEROED_WORKSPACE_BYTES 4096u
 

@@ -531,7 +531,7 @@ def main():
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
         print(json.dumps(dict(error='single-GPU build: the low-bit linear path is measured on one MI355X; '
-                                    'multi-GPU sharding is design-only (see DESIGN.md)', n_gpus=args.gpus)))
+                                    'sharding it over several GPUs is designed but not built', n_gpus=args.gpus)))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps(dict(error='no ROCm device visible')))

@@ -267,10 +267,11 @@ lb_status lb_decode_check(const void *workspace, size_t timeout_offset, void *st
 lb_status lb_argmax_next(const void *logits, int64_t vocab, const void *embedding, int64_t hidden, void *h_next,
                          int64_t *tokens, int64_t *token, int64_t *position, int64_t limit, void *stream);
 
-/* Workspace of lb_head_next for a head of `vocab` rows: a 64-bit maximum word and a 64-bit
- * counter per group of 32 workgroups (64 rows each), and one pair for the total. */
+/* Workspace of lb_head_next for a head of `vocab` rows: room for a 64-bit maximum word and a
+ * 64-bit counter per group of 8 workgroups (64 rows each), and one pair for the total (the kernel
+ * groups at least 8 workgroups; larger groups use fewer of the words). */
 #define LB_HEAD_NEXT_WORKGROUPS(vocab) (((size_t)(vocab) + 63u) / 64u)
-#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 31u) / 32u + 1u))
+#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 7u) / 8u + 1u))
 
 /*
  * Final RMSNorm -> lm_head -> greedy step in one launch: lb_fused_linear(head) followed by

@@ -289,8 +289,8 @@ def test_head_next_workspace_size_matches_header():
     from pathlib import Path
     text = (Path(__file__).resolve().parents[1] / 'include' / 'lowbit_decode_hip.h').read_text()
     assert re.search(r'#define LB_HEAD_NEXT_WORKGROUPS\(vocab\) \(\(\(size_t\)\(vocab\) \+ 63u\) / 64u\)', text)
-    assert '#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 31u) / 32u + 1u))' in text
-    for vocab, want in ((1, 32), (2048, 32), (2049, 48), (49152, 16 * 25), (70001, 16 * 36)):
+    assert '#define LB_HEAD_NEXT_WORKSPACE_BYTES(vocab) (16u * ((LB_HEAD_NEXT_WORKGROUPS(vocab) + 7u) / 8u + 1u))' in text
+    for vocab, want in ((1, 32), (512, 32), (513, 48), (49152, 16 * 97), (70001, 16 * 138)):
         assert lowbit_hip.head_next_workspace_bytes(vocab) == want, vocab
 
 

@@ -827,8 +827,9 @@ lb_status lb_head_next(const lb_fused_linear_args *a, const void *embedding, voi
   if (limit < 0 || limit > INT32_MAX) return fail(LB_INVALID_ARGUMENT, "lb_head_next: limit outside 0..2^31-1");
   const int64_t vocab = q.N, hidden = a->K;
   const size_t ws_bytes = LB_HEAD_NEXT_WORKSPACE_BYTES(vocab);
-  static_assert(kHeadNextGroup == 32 && LB_HEAD_NEXT_WORKSPACE_BYTES(64 * 32 * 3) == 16u * 4u,
-                "the workspace macro's group size is the kernel's");
+  // The macro counts groups of 8 workgroups of 64 rows (a larger kernel group uses fewer words).
+  static_assert(kHeadNextGroup >= 8 && LB_HEAD_NEXT_WORKSPACE_BYTES(64 * 8 * 3) == 16u * 4u,
+                "the workspace macro's words cover the kernel's groups");
   if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < ws_bytes)
     return fail(LB_INVALID_ARGUMENT, "lb_head_next: workspace must be 256-byte aligned with %zu bytes", ws_bytes);
   const Range ins[] = {range_of(a->x, (size_t)hidden * 2, "x"), range_of(a->gamma, (size_t)hidden * 2, "gamma"),

@@ -543,7 +543,12 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedParams p) {
 // maximum raised before it; no workgroup waits for another and no cache is written back or
 // invalidated.  Maximum words and counters are set back to zero by the workgroup that completes
 // them, so a zeroed workspace is zero again after every call.
-constexpr int kHeadNextGroup = 32;  // LB_HEAD_NEXT_WORKSPACE_BYTES counts groups of 32
+#ifndef LB_HEAD_NEXT_GROUP
+#define LB_HEAD_NEXT_GROUP 16  // workgroups per first-level group (48 groups for the 49152-row head)
+#endif
+// LB_HEAD_NEXT_WORKSPACE_BYTES counts groups of 8: larger groups use fewer of its words.
+constexpr int kHeadNextGroup = LB_HEAD_NEXT_GROUP;
+static_assert(kHeadNextGroup >= 8, "the workspace holds the words of groups of 8");
 struct HeadNextParams {
   uint64_t *ws;              // maximum words [groups + 1] (the last one the total's), counters [groups + 1]
   const f16 *embedding;      // [vocab, hidden]

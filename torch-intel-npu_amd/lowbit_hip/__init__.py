@@ -42,10 +42,10 @@ DECODE_TIMEOUT_OFFSET = 8    # LB_DECODE_TIMEOUT_OFFSET (lb_decode_layer / lb_de
 
 
 def head_next_workspace_bytes(vocab):
-    """LB_HEAD_NEXT_WORKSPACE_BYTES: a maximum word and a counter (u64) per group of 32 workgroups
-    of 64 rows, and one pair for the total."""
+    """LB_HEAD_NEXT_WORKSPACE_BYTES: room for a maximum word and a counter (u64) per group of 8
+    workgroups of 64 rows, and one pair for the total."""
     wgs = (vocab + 63) // 64
-    return 16 * ((wgs + 31) // 32 + 1)
+    return 16 * ((wgs + 7) // 8 + 1)
 
 
 def attention_timeout_offset(heads, capacity):

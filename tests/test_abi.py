@@ -385,6 +385,9 @@ def test_force_wide_workspace_holds_the_slices():
     (12, 600, 4096, 128, 2, 2),      # NF4, 2 x 2048
     (8, 1030, 8192, 8192, 0, 2),     # per-row INT8: any slice length
     (8, 4096, 4096, 128, 1, 1),      # staged whole: no workspace
+    (8, 1024, 4096, 128, 1, 4),      # fits, but 64 tiles: 4 x 1024 codes give 256 tile slices
+    (4, 1000, 2048, 64, 1, 2),       # 63 tiles: 2 x 1024 (no smaller slice)
+    (8, 576, 1536, 128, 1, 1),       # 36 tiles, but no slice of >= 1024 codes
 ])
 def test_tile_rows_k_slices_take_their_partials(m, n, k, group, fmt, slices):
     """2..16 rows over rows longer than tile_rows_kernel stages whole: equal K slices of whole

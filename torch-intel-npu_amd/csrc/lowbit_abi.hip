@@ -322,7 +322,7 @@ bool stream_rows_eligible(const lb_linear_args *a) {
 // groups, fp32 partials added in slice order).
 int tile_rows_slices(const lb_linear_args *a) {
   const bool per_row = a->format == LB_FORMAT_INT8 && a->group_size == a->K;
-  return tile_rows_slices_for((int)a->M, a->K, a->group_size, per_row);
+  return tile_rows_slices_for((int)a->M, a->N, a->K, a->group_size, per_row);
 }
 
 bool tile_rows_eligible(const lb_linear_args *a) {

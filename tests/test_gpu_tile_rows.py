@@ -1,5 +1,7 @@
 """GPU parity of the one-tile multi-row GEMV (tile_rows_kernel): 2..16 activation rows over weights
-below the streaming sizes take it without a flag (rows staged whole: K <= 4096, M * K <= 32768).
+below the streaming sizes, and 17..32 rows of INT4 / NF4 below the several-row kernel's 4 MB, take
+it without a flag (rows staged whole up to 4096 / 2048 / 1024 codes for 8 / 16 / 32 rows, longer
+ones in K slices).
 
 Bars as for every linear: rel-L2 <= 1e-3 against the oracle plus the reference's rounding-budget
 gate; identity inputs with power-of-two scales are bit-exact; the result agrees with the forced
@@ -24,6 +26,9 @@ CASES = [
     ('int4', 16, 576, 1536, 128), ('int4', 16, 2000, 2048, 2048),
     ('nf4', 4, 960, 2560, 64), ('nf4', 12, 2560, 960, 64),
     ('int8', 2, 1536, 576, 576), ('int8', 7, 1000, 4096, 4096), ('int8', 16, 576, 1536, 64),
+    # 17..32 rows: two 16-row MFMA A operands per weight fragment, rows of up to 1024 codes staged
+    ('int4', 17, 1000, 1024, 128), ('int4', 32, 576, 576, 64), ('nf4', 24, 960, 1024, 64),
+    ('nf4', 29, 700, 1024, 128),
 ]
 
 
@@ -80,6 +85,7 @@ SLICED = [
     ('int4', 8, 4096, 14336, 128), ('int4', 4, 1000, 8192, 64), ('int4', 2, 576, 12288, 32),
     ('int4', 16, 1024, 14336, 128), ('int4', 12, 600, 4096, 128), ('nf4', 6, 2048, 14336, 128),
     ('int8', 8, 1030, 8192, 8192), ('int8', 5, 2000, 6144, 128),
+    ('int4', 32, 1024, 4096, 128), ('int4', 20, 600, 2048, 64), ('nf4', 32, 1024, 4096, 128),
 ]
 
 
@@ -114,7 +120,8 @@ def test_tile_rows_slices_identity_is_bit_exact(device):
 
 
 @pytest.mark.parametrize('spec', [('int4', 8, 4096, 14336, 128), ('int8', 8, 1030, 8192, 8192),
-                                  ('int4', 16, 1000, 14336, 128)], ids=lambda s: '-'.join(map(str, s)))
+                                  ('int4', 16, 1000, 14336, 128), ('int4', 32, 1024, 4096, 128),
+                                  ('nf4', 27, 1032, 2048, 128)], ids=lambda s: '-'.join(map(str, s)))
 def test_tile_rows_slices_added_in_kernel_equal_separate_reduction(device, spec):
     """LB_FLAG_ZEROED_WORKSPACE: the slices added by each tile column's last workgroup give the
     separate reduction launch's output bit for bit, call after call and replayed from a HIP graph,

@@ -1,6 +1,6 @@
 """GPU parity of the several-row GEMV on 32x32 MFMA tiles (wide_rows_kernel) against the CPU oracle.
 
-INT4 / NF4 / INT8 calls of 17..32 rows over >= 4 MB of weights run there by default; the tests force it
+INT4 / NF4 calls of 17..32 rows over >= 16 MB of weights (INT8: 4 MB) run there by default; the tests force it
 (LB_FLAG_FORCE_WIDE) on other shapes and row counts.  Every code is decoded to its exact integer q
 and a group's (or, for per-row INT8, the whole row's) integer sum is scaled in fp32, so its value
 is the exact x . (q s) product: the bars are those of every linear path, rel-L2 <= 1e-3 against

@@ -620,7 +620,14 @@ void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
   const int slices = p.kslice > 0 ? p.K / p.kslice : 1;
   const dim3 grid(((p.N + 15) / 16 + TT - 1) / TT, slices), block(256 * TT);
 #define LB_TILE_ROWS_ARGS p.codes, p.x, p.scales, p.bias, p.M, p.N, p.K, p.G, p.ldx, p
-  if (slices > 1) {
+  if constexpr (MP == 32) {  // staged rows of up to 1024 codes (33 rows of them fill the LDS budget)
+    if (slices > 1)
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 1024, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+    else if (p.K <= 640)
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 640, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+    else
+      hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 1024, MP, TT, false>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
+  } else if (slices > 1) {
     if (MP == 16 || p.kslice <= 2048)
       hipLaunchKernelGGL((tile_rows_kernel<FMT, SCALED, 2048, MP, TT, true>), grid, block, 0, s, LB_TILE_ROWS_ARGS);
     else if constexpr (MP < 16)
@@ -648,7 +655,8 @@ template <int FMT, bool SCALED>
 void launch_tile_rows_f(const StreamParams &p, hipStream_t s) {
   if (p.M <= 4) launch_tile_rows_mp<FMT, SCALED, 4>(p, s);
   else if (p.M <= 8) launch_tile_rows_mp<FMT, SCALED, 8>(p, s);
-  else launch_tile_rows_mp<FMT, SCALED, 16>(p, s);
+  else if (p.M <= 16) launch_tile_rows_mp<FMT, SCALED, 16>(p, s);
+  else launch_tile_rows_mp<FMT, SCALED, 32>(p, s);
 }
 
 void launch_tile_rows(const StreamParams &p, int format, bool scaled, hipStream_t s) {

@@ -690,49 +690,14 @@ __global__ __launch_bounds__(64 * WAVES) void stream_wide_kernel(StreamParams p)
 // Launches stream_wide_kernel for 17 <= p.M <= 32 rows.
 void launch_stream_wide(const StreamParams &p, int format, bool scaled, hipStream_t stream);
 
-// End of a SLICED tile_rows_kernel workgroup (every thread calls it).  Wave 0 of each tile adds the
-// other waves' sums (red, the order of the unsliced kernel) and writes the tile's fp32 partials of
-// its slice.  Without tickets that is all (splitk_reduce_kernel follows).  With them the partials are
-// written with system-scope coherent stores (as wide_add_slices does), and the workgroup counts itself
-// in its tile column's ticket with a returning system-scope atomic once every wave's stores are
-// complete; the one that counts last (gridDim.y - 1) reads the column's partials with coherent loads,
-// adds the slices in slice order from 0.0f (splitk_reduce_kernel's order and values: the same y bit
-// for bit), applies the epilogue (per-row scale, fp16, bias) and returns the ticket to zero.  No
-// workgroup waits for another.
+// Element e of a SLICED workgroup's tiles (tile e / (16 M), activation row (e / 16) % M, column
+// e % 16): the slices' partials added in slice order from 0.0f, then the epilogue.
 template <int TT, bool SCALED>
-__device__ __forceinline__ void tile_rows_slices(const StreamParams &p, f4 acc, const float *red, int wave, int lane,
-                                                 int n0, int rows, int M, int N) {
+__device__ __forceinline__ void tile_rows_slice_sum(const StreamParams &p, __amdgpu_buffer_rsrc_t pb, int e, int M, int N,
+                                                    int S) {
   constexpr int kOutOfRange = (int)0x80000000u;
-  constexpr int SMAX = 8;  // slices whose partials the adding workgroup requests at once
-  __shared__ uint32_t last;
-  const int S = gridDim.y, j = lane & 15, g = lane >> 4;
-  const bool through = p.tickets != nullptr;
-  const __amdgpu_buffer_rsrc_t pb = buffer_rsrc(p.partial, (size_t)S * M * N * 4);
-  if (wave == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = ((acc[r] + red[lane * 4 + r]) + red[(64 + lane) * 4 + r]) + red[(128 + lane) * 4 + r];
-    if (j < rows) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * g + r;
-        const float v = acc[r];
-        const int off = m < M ? ((blockIdx.y * M + m) * N + n0 + j) * 4 : kOutOfRange;
-        if (through) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, kSysCoherent);
-        else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, 0);
-      }
-    }
-  }
-  if (!through) return;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are written through
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(p.tickets + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
-           (uint32_t)(S - 1);
-  __syncthreads();
-  if (!last) return;
-  if (threadIdx.x == 0) __hip_atomic_store(p.tickets + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  // Thread e: tile e / (16 M), activation row (e / 16) % M, column e % 16 of the workgroup's tiles.
-  const int e = threadIdx.x, tl = e / (16 * M), m = (e / 16) - tl * M, n = (blockIdx.x * TT + tl) * 16 + (e & 15);
+  constexpr int SMAX = 8;  // slices whose partials are requested at once
+  const int tl = e / (16 * M), m = (e / 16) - tl * M, n = (blockIdx.x * TT + tl) * 16 + (e & 15);
   const bool live = tl < TT && n < N;
   float sum = 0.0f;
   for (int s0 = 0; s0 < S; s0 += SMAX) {
@@ -759,7 +724,57 @@ __device__ __forceinline__ void tile_rows_slices(const StreamParams &p, f4 acc, 
   p.y[(size_t)m * p.ldy + n] = h;
 }
 
-// TT 16-row tiles per workgroup for 2 .. MP activation rows (MP = 4, 8 or 16), the multi-row
+// End of a SLICED tile_rows_kernel workgroup (every thread calls it).  Wave 0 of each tile adds the
+// other waves' sums (red, the order of the unsliced kernel) and writes the tile's fp32 partials of
+// its slice.  Without tickets that is all (splitk_reduce_kernel follows).  With them the partials are
+// written with system-scope coherent stores (as wide_add_slices does), and the workgroup counts itself
+// in its tile column's ticket with a returning system-scope atomic once every wave's stores are
+// complete; the one that counts last (gridDim.y - 1) reads the column's partials with coherent loads,
+// adds the slices in slice order from 0.0f (splitk_reduce_kernel's order and values: the same y bit
+// for bit), applies the epilogue (per-row scale, fp16, bias) and returns the ticket to zero.  No
+// workgroup waits for another.
+template <int TT, bool SCALED, int MH>
+__device__ __forceinline__ void tile_rows_slices(const StreamParams &p, f4 (&acc)[MH], const float *red, int wave,
+                                                 int lane, int n0, int rows, int M, int N) {
+  constexpr int kOutOfRange = (int)0x80000000u;
+  __shared__ uint32_t last;
+  const int S = gridDim.y, j = lane & 15, g = lane >> 4;
+  const bool through = p.tickets != nullptr;
+  const __amdgpu_buffer_rsrc_t pb = buffer_rsrc(p.partial, (size_t)S * M * N * 4);
+  if (wave == 0) {
+#pragma unroll
+    for (int h = 0; h < MH; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        acc[h][r] = ((acc[h][r] + red[(h * 64 + lane) * 4 + r]) + red[((MH + h) * 64 + lane) * 4 + r]) +
+                    red[((2 * MH + h) * 64 + lane) * 4 + r];
+    if (j < rows) {
+#pragma unroll
+      for (int hr = 0; hr < 4 * MH; ++hr) {
+        const int m = 16 * (hr / 4) + 4 * g + hr % 4;
+        const float v = acc[hr / 4][hr % 4];
+        const int off = m < M ? ((blockIdx.y * M + m) * N + n0 + j) * 4 : kOutOfRange;
+        if (through) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, kSysCoherent);
+        else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pb, off, 0, 0);
+      }
+    }
+  }
+  if (!through) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are written through
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(p.tickets + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+           (uint32_t)(S - 1);
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(p.tickets + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // Every element of the workgroup's tiles (up to 32 rows: two elements per thread).
+  for (int e = threadIdx.x; e < TT * 16 * M; e += 256 * TT)
+    tile_rows_slice_sum<TT, SCALED>(p, pb, e, M, N, S);
+}
+
+// TT 16-row tiles per workgroup for 2 .. MP activation rows (MP = 4, 8, 16, or 32 as two 16-row
+// MFMA A operands against each decoded weight fragment), the multi-row
 // form of the single-tile one-row kernels: four waves per tile split K (wave 4 i + w of tile i
 // takes k steps w, w + 4, ...), every weight load of a lane is issued straight-line before the
 // first wait (up to 32 x 16 bytes), the M activation rows are staged once per workgroup in LDS in
@@ -791,7 +806,8 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
   constexpr int GMAX = KMAX / 32;                    // groups per row at most (groups >= 32)
   constexpr int SC = SCALED ? (16 * GMAX + 255) / 256 : 0;
   constexpr int kOutOfRange = (int)0x80000000u;
-  static_assert(MP == 4 || MP == 8 || MP == 16, "MP is 4, 8 or 16");
+  static_assert(MP == 4 || MP == 8 || MP == 16 || MP == 32, "MP is 4, 8, 16 or 32");
+  constexpr int MH = MP > 16 ? 2 : 1;                // 16-row halves of the activation rows (MFMA A operands)
   // Four tiles per workgroup (1024 threads) measured slower with the preloaded operands: there the
   // argument block is read as before (the leading arguments are then unused and not preloaded).
   constexpr bool PRE = TT < 4;
@@ -802,7 +818,7 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
   const int M_ = PRE ? pre_M : p.M, N_ = PRE ? pre_N : p.N, G_ = PRE ? pre_G : p.G, ldx_ = PRE ? pre_ldx : p.ldx;
   __shared__ __align__(16) f16 xs[(MP + 1) * XLD];   // MP rows, then the zero row
   __shared__ __align__(16) f16 ss[TT][SCALED ? 16 * GMAX + 8 : 8];
-  __shared__ float red[TT][(KG - 1) * 64 * 4];
+  __shared__ float red[TT][(KG - 1) * 64 * 4 * MH];
   __shared__ uint32_t nf4_table[FMT == FMT_NF4 ? 256 : 1];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -886,8 +902,11 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
   if constexpr (FMT == FMT_NF4) build_nf4_pair_table(nf4_table);
   __syncthreads();
 
-  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  f4 acc[MH];
+#pragma unroll
+  for (int h = 0; h < MH; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
   const f16 *a0 = xs + (j < p.M ? j : MP) * XLD + g * CPL;
+  const f16 *a1 = xs + (MH > 1 && j + 16 < p.M ? j + 16 : MP) * XLD + g * CPL;
 #pragma unroll
   for (int u = 0; u < D; ++u) {
     const int kb = (wave + KG * u) * KSTEP;
@@ -902,34 +921,41 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
     }
 #pragma unroll
     for (int q = 0; q < T8; ++q) {
-      const h8 a = *reinterpret_cast<const h8 *>(a0 + kb + 8 * q);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, decode8<FMT, !SCALED>(w[u], q, s2, nf4_table), acc, 0, 0, 0);
+      const h8 bw = decode8<FMT, !SCALED>(w[u], q, s2, nf4_table);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(a0 + kb + 8 * q), bw, acc[0], 0, 0, 0);
+      if constexpr (MH > 1)
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8 *>(a1 + kb + 8 * q), bw, acc[1], 0, 0, 0);
     }
   }
   // Partial sums of waves 1..3 of each tile through LDS; its wave 0 adds them in order and writes it.
   if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[tile][((wave - 1) * 64 + lane) * 4 + r] = acc[r];
+    for (int h = 0; h < MH; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[tile][(((wave - 1) * MH + h) * 64 + lane) * 4 + r] = acc[h][r];
   }
   __syncthreads();
   if constexpr (SLICED) {
-    tile_rows_slices<TT, SCALED>(p, acc, red[tile], wave, lane, n0, rows, M_, N_);
+    tile_rows_slices<TT, SCALED, MH>(p, acc, red[tile], wave, lane, n0, rows, M_, N_);
     return;
   }
   if (wave > 0) return;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    acc[r] = ((acc[r] + red[tile][lane * 4 + r]) + red[tile][(64 + lane) * 4 + r]) + red[tile][(128 + lane) * 4 + r];
-  // Lane (j, g) holds rows 4g .. 4g+3 of column j (weight row n0 + j).  The bias / per-row
-  // scale of column j sit in lane j (group 0).
+  for (int h = 0; h < MH; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      acc[h][r] = ((acc[h][r] + red[tile][(h * 64 + lane) * 4 + r]) + red[tile][((MH + h) * 64 + lane) * 4 + r]) +
+                  red[tile][((2 * MH + h) * 64 + lane) * 4 + r];
+  // Lane (j, g) holds rows 16 h + 4g .. + 3 of column j (weight row n0 + j) in acc[h].  The bias /
+  // per-row scale of column j sit in lane j (group 0).
   const f16 bias = __builtin_bit_cast(f16, (unsigned short)__shfl((int)ebias, j, 64));
   const f16 rowscale = __builtin_bit_cast(f16, (unsigned short)__shfl((int)erow, j, 64));
   if (j >= rows) return;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * g + r;
+  for (int hr = 0; hr < 4 * MH; ++hr) {
+    const int m = 16 * (hr / 4) + 4 * g + hr % 4;
     if (m >= p.M) continue;
-    float v = acc[r];
+    float v = acc[hr / 4][hr % 4];
     if constexpr (!SCALED) v *= (float)rowscale;
     f16 h = (f16)v;
     if (p.bias) h = (f16)((float)h + (float)bias);
@@ -953,7 +979,7 @@ inline int tile_rows_per_wg(long long tiles, long long K) {
 }
 
 // K slices of tile_rows_kernel for rows longer than it stages whole (4096 codes up to 8
-// activation rows, 2048 beyond): the fewest, at most 16, that cut K into equal slices of whole
+// activation rows, 2048 up to 16, 1024 up to 32): the fewest, at most 16, that cut K into equal slices of whole
 // 512-code steps and whole scale groups (any length for per-row scales); 0 when there is no such
 // cut.  Rows that fit stay whole (1), unless there are fewer than LB_TILE_ROWS_FEW_TILES tiles: then
 // the fewest slices of at least 1024 codes, at most 8, that give 256 tile slices (or the most there
@@ -962,14 +988,18 @@ inline int tile_rows_per_wg(long long tiles, long long K) {
 #define LB_TILE_ROWS_KMAX8 4096  // longest row tile_rows_kernel stages whole for up to 8 activation rows
 #endif
 #ifndef LB_TILE_ROWS_KMAX16
-#define LB_TILE_ROWS_KMAX16 2048  // ... and for 9..16 rows
+#define LB_TILE_ROWS_KMAX16 2048  // ... for 9..16 rows
 #endif
-static_assert(LB_TILE_ROWS_KMAX8 <= 4096 && LB_TILE_ROWS_KMAX16 <= 2048, "the staged lengths the launches instantiate");
+#ifndef LB_TILE_ROWS_KMAX32
+#define LB_TILE_ROWS_KMAX32 1024  // ... and for 17..32 rows
+#endif
+static_assert(LB_TILE_ROWS_KMAX8 <= 4096 && LB_TILE_ROWS_KMAX16 <= 2048 && LB_TILE_ROWS_KMAX32 <= 1024,
+              "the staged lengths the launches instantiate");
 #ifndef LB_TILE_ROWS_FEW_TILES
 #define LB_TILE_ROWS_FEW_TILES 128  // rows that fit are sliced too (slices of >= 1024 codes) while the tiles number fewer than this
 #endif
 inline int tile_rows_slices_for(int M, long long N, long long K, long long group, bool per_row) {
-  const long long kmax = M <= 8 ? LB_TILE_ROWS_KMAX8 : LB_TILE_ROWS_KMAX16;
+  const long long kmax = M <= 8 ? LB_TILE_ROWS_KMAX8 : M <= 16 ? LB_TILE_ROWS_KMAX16 : LB_TILE_ROWS_KMAX32;
   if (K <= kmax) {
     const long long tiles = (N + 15) / 16;
     int best = 1;

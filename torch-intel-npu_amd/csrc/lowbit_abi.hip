@@ -309,6 +309,9 @@ bool stream_rows_eligible(const lb_linear_args *a) {
 #ifndef LB_TILE_ROWS
 #define LB_TILE_ROWS 1  // 2..16 rows below the streaming sizes: tile_rows_kernel (one workgroup per tile)
 #endif
+#ifndef LB_TILE_ROWS_MAX_M
+#define LB_TILE_ROWS_MAX_M 32  // tile_rows_kernel up to this many activation rows (16 or 32)
+#endif
 #ifndef LB_TILE_ROWS_MAX_X_BYTES
 #define LB_TILE_ROWS_MAX_X_BYTES (32ll << 20)  // activation bytes all tiles stage together, at most
 #endif
@@ -326,20 +329,25 @@ int tile_rows_slices(const lb_linear_args *a) {
 }
 
 bool tile_rows_eligible(const lb_linear_args *a) {
-  if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > 16) return false;
+  if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > LB_TILE_ROWS_MAX_M) return false;
   const int slices = tile_rows_slices(a);
   if (slices < 1) return false;
   const int64_t ks = a->K / slices, tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles * slices, ks);
   const int64_t wgs = (tiles + tt - 1) / tt * slices;
   if (wgs * a->M * ks * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
-  return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || a->format == LB_FORMAT_INT8;
+  // Past 16 rows INT8 stays on the tiled GEMV (per-row 1024x4096 at M = 32: 12.0 against 12.9 us).
+  return a->format == LB_FORMAT_INT4 || a->format == LB_FORMAT_NF4 || (a->format == LB_FORMAT_INT8 && a->M <= 16);
 }
 
 #ifndef LB_WIDE_MIN_M
 #define LB_WIDE_MIN_M 17  // wide_rows_kernel from this many activation rows (up to 32) ...
 #endif
 #ifndef LB_WIDE_MIN_BYTES
-#define LB_WIDE_MIN_BYTES (4ll << 20)  // ... over weights of at least this many bytes
+#define LB_WIDE_MIN_BYTES (4ll << 20)  // ... over INT8 weights of at least this many bytes
+#endif
+#ifndef LB_WIDE_MIN_BYTES_4BIT
+#define LB_WIDE_MIN_BYTES_4BIT (16ll << 20)  // ... and INT4 / NF4 weights of at least this many (smaller
+                                              // ones measured faster on tile_rows_kernel)
 #endif
 #ifndef LB_WIDE_MID_M
 #define LB_WIDE_MID_M 17  // and from this many rows over weights of LB_WIDE_MID_BYTES up to the streaming sizes
@@ -378,12 +386,13 @@ bool wide_shape_ok(const lb_linear_args *a) {
   return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
 }
 
-// 17..32 rows over >= 4 MB; with LB_WIDE_MID_M lowered, also fewer rows over LB_WIDE_MID_BYTES up
-// to the streaming sizes (the streaming kernels keep larger weights, where they measured faster).
+// 17..32 rows over >= 16 MB of INT4 / NF4 or >= 4 MB of INT8; with LB_WIDE_MID_M lowered, also fewer
+// rows over LB_WIDE_MID_BYTES up to the streaming sizes (the streaming kernels keep larger weights,
+// where they measured faster).
 bool wide_eligible(const lb_linear_args *a) {
   if (a->M < LB_WIDE_MID_M || !wide_shape_ok(a)) return false;
   const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
-  if (a->M >= LB_WIDE_MIN_M) return bytes >= LB_WIDE_MIN_BYTES;
+  if (a->M >= LB_WIDE_MIN_M) return bytes >= (a->format == LB_FORMAT_INT8 ? LB_WIDE_MIN_BYTES : LB_WIDE_MIN_BYTES_4BIT);
   return bytes >= LB_WIDE_MID_BYTES && bytes < LB_STREAM_ROWS_MIN_BYTES;
 }
 

@@ -645,7 +645,7 @@ void launch_tile_rows_tt(const StreamParams &p, hipStream_t s) {
 template <int FMT, bool SCALED, int MP>
 void launch_tile_rows_mp(const StreamParams &p, hipStream_t s) {
   const int slices = p.kslice > 0 ? p.K / p.kslice : 1;
-  const int tt = tile_rows_per_wg((long long)(p.N + 15) / 16 * slices, p.kslice > 0 ? p.kslice : p.K);
+  const int tt = tile_rows_per_wg((long long)(p.N + 15) / 16 * slices, p.kslice > 0 ? p.kslice : p.K, p.M);
   if (tt == 4) launch_tile_rows_tt<FMT, SCALED, MP, 4>(p, s);
   else if (tt == 2) launch_tile_rows_tt<FMT, SCALED, MP, 2>(p, s);
   else launch_tile_rows_tt<FMT, SCALED, MP, 1>(p, s);

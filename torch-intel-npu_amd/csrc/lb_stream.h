@@ -966,16 +966,26 @@ __global__ __launch_bounds__(256 * TT) void tile_rows_kernel(const uint8_t *pre_
 #ifndef LB_TILE_ROWS_MIN_WGS
 #define LB_TILE_ROWS_MIN_WGS 224  // tile_rows_kernel groups 4 (or 2) tiles per workgroup while this many remain
 #endif
+#ifndef LB_TILE_ROWS_FEW_ROWS
+#define LB_TILE_ROWS_FEW_ROWS 4  // calls of at most this many activation rows ...
+#endif
+#ifndef LB_TILE_ROWS_MIN_WGS_FEW
+#define LB_TILE_ROWS_MIN_WGS_FEW 256  // ... keep this many workgroups instead
+#endif
 #ifndef LB_TILE_ROWS_SHORT_K
 #define LB_TILE_ROWS_SHORT_K 1024  // rows of at most this many codes take at most 2 tiles per workgroup
 #endif
-// Tiles per tile_rows_kernel workgroup for `tiles` 16-row tiles of K codes: the staged activation
-// rows are shared by more tiles as long as the grid keeps LB_TILE_ROWS_MIN_WGS workgroups; four
-// tiles only over long rows (short ones stage little, and two tiles with preloaded operands
-// measured faster: the 49152x576 head at M = 4 8.9 -> 7.3 us, at M = 16 10.1 -> 9.3 us).
-inline int tile_rows_per_wg(long long tiles, long long K) {
-  if (K > LB_TILE_ROWS_SHORT_K && tiles >= 4ll * LB_TILE_ROWS_MIN_WGS) return 4;
-  return tiles >= 2ll * LB_TILE_ROWS_MIN_WGS ? 2 : 1;
+// Tiles per tile_rows_kernel workgroup for `tiles` 16-row tiles of K codes and M activation rows:
+// the staged activation rows are shared by more tiles as long as the grid keeps LB_TILE_ROWS_MIN_WGS
+// workgroups (LB_TILE_ROWS_MIN_WGS_FEW for up to LB_TILE_ROWS_FEW_ROWS rows, which stage little:
+// INT4 14336x4096 as 448 workgroups of two tiles instead of 224 of four, M = 2 11.6 -> 10.5 us,
+// M = 4 11.9 -> 10.9 us, where M = 8 measured 12.3 -> 13.8 us); four tiles only over long rows
+// (short ones stage little, and two tiles with preloaded operands measured faster: the 49152x576
+// head at M = 4 8.9 -> 7.3 us, at M = 16 10.1 -> 9.3 us).
+inline int tile_rows_per_wg(long long tiles, long long K, long long M) {
+  const long long min_wgs = M <= LB_TILE_ROWS_FEW_ROWS ? LB_TILE_ROWS_MIN_WGS_FEW : LB_TILE_ROWS_MIN_WGS;
+  if (K > LB_TILE_ROWS_SHORT_K && tiles >= 4ll * min_wgs) return 4;
+  return tiles >= 2ll * min_wgs ? 2 : 1;
 }
 
 // K slices of tile_rows_kernel for rows longer than it stages whole (4096 codes up to 8

@@ -332,7 +332,7 @@ bool tile_rows_eligible(const lb_linear_args *a) {
   if (!LB_TILE_ROWS || a->rank > 0 || a->M < 2 || a->M > LB_TILE_ROWS_MAX_M) return false;
   const int slices = tile_rows_slices(a);
   if (slices < 1) return false;
-  const int64_t ks = a->K / slices, tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles * slices, ks);
+  const int64_t ks = a->K / slices, tiles = (a->N + 15) / 16, tt = tile_rows_per_wg(tiles * slices, ks, a->M);
   const int64_t wgs = (tiles + tt - 1) / tt * slices;
   if (wgs * a->M * ks * 2 > LB_TILE_ROWS_MAX_X_BYTES) return false;
   // Past 16 rows INT8 stays on the tiled GEMV (per-row 1024x4096 at M = 32: 12.0 against 12.9 us).
@@ -1011,7 +1011,7 @@ lb_status lb_linear(const lb_linear_args *a, void *stream) {
     if (plan.path == PATH_TILE) {
       bool in_kernel = false;
       if (plan.splits > 1) {  // K slices: fp32 partials, added by the kernel or by a second launch
-        const int64_t tt = tile_rows_per_wg((int64_t)sp.tiles * plan.splits, plan.kslice);
+        const int64_t tt = tile_rows_per_wg((int64_t)sp.tiles * plan.splits, plan.kslice, a->M);
         in_kernel = plan.zeroed && (sp.tiles + tt - 1) / tt <= (int64_t)(LB_ZEROED_WORKSPACE_BYTES / 4);
         sp.kslice = plan.kslice;
         sp.partial = reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) + plan.part_off);

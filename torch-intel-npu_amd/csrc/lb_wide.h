@@ -443,9 +443,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void wide_rows_kernel(const uint8_
 
 namespace lb {
 
-// Positions per chunk and chunks of weights in flight of the launched kernels.
+// Positions per chunk and chunks of weights in flight of the launched kernels (two buffers, the next
+// chunk requested while one runs: against three, INT4 g128 M = 32 14336x4096 18.9 -> 18.1 us, M = 24
+// 17.7 -> 16.9 us, 4096x14336 22.4 -> 21.8 us, NF4 M = 32 21.9 -> 19.9 us, the head and per-row
+// INT8 unchanged; four measured 10-25% slower).
 #ifndef LB_WIDE_PD
-#define LB_WIDE_PD 3
+#define LB_WIDE_PD 2
 #endif
 constexpr int kWidePC = 2, kWidePD = LB_WIDE_PD;
 template <int FMT> constexpr int wide_chunk() { return kWidePC * wide_position<FMT>(); }

@@ -397,7 +397,7 @@ bool wide_eligible(const lb_linear_args *a) {
 }
 
 // K slices of wide_rows_kernel: the fewest dividing the chunk count that give LB_WIDE_TARGET_WGS
-// workgroups (row blocks of 128 rows x slices), at most LB_WIDE_MAX_SLICES.
+// workgroups (row blocks of kWideRows rows x slices), at most LB_WIDE_MAX_SLICES.
 int wide_slices(int fmt, int64_t N, int64_t K) {
   const int64_t blocks = (N + kWideRows - 1) / kWideRows, chunks = K / wide_chunk_codes(fmt);
   int best = 1;

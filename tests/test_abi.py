@@ -378,6 +378,24 @@ def test_force_wide_workspace_holds_the_slices():
     assert status == 0 and size == slices * 24 * 14336 * 4 and slices in (2, 4, 8)   # the default at 17..32 rows
 
 
+@pytest.mark.parametrize('fmt,m,n,k,slices', [
+    ('int4', 16, 14336, 4096, 4),    # 9..16 rows, INT4 / NF4, slices the kernel adds: wide_rows_kernel, 4 x 1024
+    ('nf4', 9, 14336, 4096, 4),
+    ('int4', 8, 14336, 4096, 0),     # 8 rows: tile_rows_kernel, 4096 codes staged whole
+    ('int8', 16, 14336, 4096, 2),    # INT8: tile_rows_kernel, 2 x 2048
+    ('int4', 16, 4096, 14336, 7),    # 14 wide slices, more than the kernel adds: tile_rows_kernel, 7 x 2048
+    ('int4', 16, 8192, 4096, 2),     # 8 wide slices: tile_rows_kernel, 2 x 2048
+])
+def test_nine_to_sixteen_rows_take_wide_only_where_it_adds_its_slices(fmt, m, n, k, slices):
+    """The default dispatch of 9..16 rows over 16..64 MB: the workspace holds the chosen kernel's
+    fp32 partials [slices, M, N] (none for rows staged whole), which names the kernel."""
+    far = dict(x=0x1000000, y=0x8000000, scales=0x10000000, codes=0x20000000)
+    group = k if fmt == 'int8' else 128
+    code = {'int8': 0, 'int4': 1, 'nf4': 2}[fmt]
+    status, size, _ = workspace(args(M=m, N=n, K=k, ldx=k, ldy=n, group_size=group, format=code, **far))
+    assert status == 0 and size == slices * m * n * 4
+
+
 @pytest.mark.parametrize('m,n,k,group,fmt,slices', [
     (8, 4096, 14336, 128, 1, 4),     # 4 x 3584 codes (up to 8 rows: 4096 staged)
     (2, 576, 12288, 32, 1, 3),       # 3 x 4096

@@ -1,6 +1,7 @@
 """GPU parity of the several-row GEMV on 32x32 MFMA tiles (wide_rows_kernel) against the CPU oracle.
 
-INT4 / NF4 calls of 17..32 rows over >= 16 MB of weights (INT8: 4 MB) run there by default; the tests force it
+INT4 / NF4 calls of 17..32 rows over >= 16 MB of weights (INT8: 4 MB), and of 9..16 rows over 16..64 MB
+whose K slices the kernel adds itself, run there by default; the tests force it
 (LB_FLAG_FORCE_WIDE) on other shapes and row counts.  Every code is decoded to its exact integer q
 and a group's (or, for per-row INT8, the whole row's) integer sum is scaled in fp32, so its value
 is the exact x . (q s) product: the bars are those of every linear path, rel-L2 <= 1e-3 against
@@ -108,15 +109,17 @@ def test_wide_identity_is_bit_exact(device, fmt, group, n, k):
         np.testing.assert_array_equal(got[i], w[:, cols[i % len(cols)]], err_msg=f'row {i}')
 
 
-def test_wide_is_the_default_for_17_to_32_rows(device):
-    """14336x4096 INT4 g128 at M = 24 (config-5 shape): the default dispatch gives the forced
-    kernel's result bit for bit, and the oracle's values."""
-    announce('wide default dispatch')
-    rng = np.random.default_rng(5)
-    p = problem(rng, 'int4', 24, 14336, 4096, 128)
+@pytest.mark.parametrize('fmt,m', [('int4', 24), ('int4', 12), ('nf4', 16)])
+def test_wide_is_the_default_on_the_tall_config5_shape(device, fmt, m):
+    """14336x4096 g128 (config-5 shape) at 17..32 rows, and at 9..16 INT4 / NF4 rows (four K slices,
+    added by the kernel): the default dispatch gives the forced kernel's result bit for bit, and
+    the oracle's values."""
+    announce('wide default dispatch', fmt, m)
+    rng = np.random.default_rng(5 + m)
+    p = problem(rng, fmt, m, 14336, 4096, 128)
     default = run(p, device)
     np.testing.assert_array_equal(default, run(p, device, WIDE))
-    check(p, default, 'wide default')
+    check(p, default, f'wide default {fmt} M={m}')
 
 
 @pytest.mark.parametrize('over', [dict(K=4096 + 256), dict(group=64), dict(fmt='nf4', group=64), dict(M=33)])

@@ -350,8 +350,8 @@ bool tile_rows_eligible(const lb_linear_args *a) {
                                               // ones measured faster on tile_rows_kernel)
 #endif
 #ifndef LB_WIDE_MID_M
-#define LB_WIDE_MID_M 17  // and from this many rows over weights of LB_WIDE_MID_BYTES up to the streaming sizes
-                          // (none by default: 9..16 rows measured faster on tile_rows_kernel over K slices)
+#define LB_WIDE_MID_M 9  // and from this many rows over INT4 / NF4 weights of LB_WIDE_MID_BYTES up to the
+                         // streaming sizes, when the kernel adds its K slices itself
 #endif
 #ifndef LB_WIDE_MID_BYTES
 #define LB_WIDE_MID_BYTES (16ll << 20)
@@ -386,14 +386,20 @@ bool wide_shape_ok(const lb_linear_args *a) {
   return aligned(a->codes, 16) && aligned(a->x, 16) && a->ldx % 8 == 0;
 }
 
-// 17..32 rows over >= 16 MB of INT4 / NF4 or >= 4 MB of INT8; with LB_WIDE_MID_M lowered, also fewer
-// rows over LB_WIDE_MID_BYTES up to the streaming sizes (the streaming kernels keep larger weights,
-// where they measured faster).
+int wide_slices(int fmt, int64_t N, int64_t K);
+
+// 17..32 rows over >= 16 MB of INT4 / NF4 or >= 4 MB of INT8; LB_WIDE_MID_M..16 rows over INT4 / NF4
+// weights of LB_WIDE_MID_BYTES up to the streaming sizes (which keep larger weights, where they measured
+// faster) whose K slices are few enough for the kernel to add (LB_WIDE_IN_KERNEL_SLICES): INT4 g128
+// 14336x4096 M = 16 17.5 -> 16.7 us, M = 12 16.8 -> 16.2, NF4 M = 16 20.0 -> 18.7 against
+// tile_rows_kernel, which stays faster with more slices or on INT8 (4096x14336 M = 16 17.2 against
+// 20.0 us, 8192x4096 9.8 against 12.7, INT8 14336x4096 20.5 against 21.7).
 bool wide_eligible(const lb_linear_args *a) {
   if (a->M < LB_WIDE_MID_M || !wide_shape_ok(a)) return false;
   const int64_t bytes = a->format == LB_FORMAT_INT8 ? a->N * a->K : a->N * a->K / 2;
   if (a->M >= LB_WIDE_MIN_M) return bytes >= (a->format == LB_FORMAT_INT8 ? LB_WIDE_MIN_BYTES : LB_WIDE_MIN_BYTES_4BIT);
-  return bytes >= LB_WIDE_MID_BYTES && bytes < LB_STREAM_ROWS_MIN_BYTES;
+  return a->format != LB_FORMAT_INT8 && bytes >= LB_WIDE_MID_BYTES && bytes < LB_STREAM_ROWS_MIN_BYTES &&
+         wide_slices((int)a->format, a->N, a->K) <= LB_WIDE_IN_KERNEL_SLICES;
 }
 
 // K slices of wide_rows_kernel: the fewest dividing the chunk count that give LB_WIDE_TARGET_WGS

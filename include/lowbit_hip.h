@@ -75,7 +75,8 @@ typedef enum lb_format {
  * No counterpart in the reference: the path choice is internal there. */
 #define LB_FLAG_FORCE_STREAM  0x20u
 /* The several-row GEMV on 32x32 MFMA tiles (the kernel 17..32-row calls over >= 16 MB of INT4 / NF4
- * or >= 4 MB of INT8 weights take by themselves) regardless of size: INT4/NF4/INT8 codes, no
+ * or >= 4 MB of INT8 weights take by themselves, and 9..16-row INT4 / NF4 calls over 16..64 MB split
+ * into at most 4 K slices) regardless of size: INT4/NF4/INT8 codes, no
  * correction or variant, M <= 32,
  * 16-byte aligned codes and x rows, K a multiple of 512 (INT4, NF4) / 256 (INT8) up to 65536, and
  * per-row INT8 or power-of-two groups of at least 128 (INT4, NF4) / 64 (INT8) codes dividing that.
